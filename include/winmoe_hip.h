@@ -1,0 +1,206 @@
+/*
+ * winmoe_hip.h -- C-ABI of libwinmoe_hip.so, the MI355X (gfx950) MoE
+ * expert-layer library.
+ *
+ * Two surfaces:
+ *   1. wm_*   device-pointer, stream-ordered entry points.  Pointers are device
+ *             (HBM) addresses, `stream` is a hipStream_t passed as void*
+ *             (NULL = the null stream).  No call synchronises the host unless
+ *             its comment says so.  The routing trace, per-expert hit counters
+ *             and all scratch live in one caller-allocated workspace sized by
+ *             wm_workspace_size().
+ *   2. gpu_*  the expert subset of the reference's GPU offload ABI
+ *             (engine/runtime/gpu_offload.h:15-100), same names, argument
+ *             meaning and 0 / -1 / slot returns, caller-owned host buffers,
+ *             blocking.  Any supported quant type may back a slot.
+ *
+ * Return codes: WM_OK (0) success, WM_ERR (-1) HIP runtime error (message on
+ * stderr, as CHECK_CUDA does in gpu_offload.cu:23-29), WM_EINVAL (-2) bad
+ * argument (unsupported type, misaligned pointer, shape outside the supported
+ * set, undersized workspace).
+ *
+ * Threading: a workspace serves one stream at a time; distinct workspaces on
+ * distinct streams may run concurrently.  The gpu_* shims keep global state
+ * and are single-threaded like the reference.
+ */
+#ifndef WINMOE_HIP_H
+#define WINMOE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WM_OK 0
+#define WM_ERR (-1)
+#define WM_EINVAL (-2)
+
+/* ggml tensor type ids (engine/runtime/gguf_parser.h:21-29; Q2_K = 10 and
+ * Q3_K = 11 are the public ggml ids the reference table lacks). */
+enum {
+    WM_F32 = 0, WM_F16 = 1, WM_Q8_0 = 8, WM_Q2_K = 10, WM_Q3_K = 11,
+    WM_Q4_K = 12, WM_Q5_K = 13, WM_Q6_K = 14
+};
+
+/* Workspace status bits (read back with wm_workspace_status). */
+#define WM_STATUS_DEGENERATE_ROUTING 1   /* a top-K pass found no logit > -1e30 */
+#define WM_STATUS_BAD_EXPERT_ID      2   /* forced routing named an id outside [0, E) */
+#define WM_STATUS_NONFINITE_WEIGHT   4   /* a routing weight was NaN/Inf */
+
+/* One MoE layer.  Expert tensors are the raw GGUF blocks, stacked by expert:
+ * gate/up expert e = [inter rows][hidden/QK blocks] at gate_exps + e*gate_stride,
+ * down expert e = [hidden rows][inter/QK blocks] at down_exps + e*down_stride
+ * (the per-expert slicing of winmoe_inference.c:467-489,1770-1775).  A stride
+ * of 0 means densely packed.  Replaces the reference's LayerWeights expert
+ * fields (engine/runtime/transformer.h:80-99). */
+typedef struct wm_layer_desc {
+    int32_t hidden;          /* H */
+    int32_t inter;           /* I, routed expert intermediate */
+    int32_t inter_shared;    /* I of the shared expert (0 = inter) */
+    int32_t n_experts;       /* E */
+    int32_t top_k;           /* K, 1..16 (no silent clamp, unlike winmoe_inference.c:812) */
+    int32_t gate_type, up_type, down_type;
+    int32_t sh_gate_type, sh_up_type, sh_down_type;
+    int32_t reserved;
+    const float* router;     /* [E][H] fp32, row-major; NULL only for forced routing */
+    const void* gate_exps;
+    const void* up_exps;
+    const void* down_exps;
+    int64_t gate_stride, up_stride, down_stride;
+    const void* sh_gate;     /* shared expert [I_s][H/QK]; NULL = no shared expert */
+    const void* sh_up;
+    const void* sh_down;     /* [H][I_s/QK] */
+    const float* sh_gate_inp;/* [H] fp32 sigmoid gate of the shared expert, or NULL */
+} wm_layer_desc;
+
+/* ---------------------------------------------------------------- library */
+
+/* Selects the current HIP device and caches its properties.  Optional: every
+ * entry point calls it on first use.  Returns WM_OK or WM_ERR. */
+int wm_init(void);
+const char* wm_version(void);
+int wm_block_bytes(int qtype);          /* 0 if unsupported */
+int wm_block_elems(int qtype);          /* 0 if unsupported */
+
+/* -------------------------------------------------- device-pointer API */
+
+/* Dequantise nblocks raw blocks to fp32 (bit-exact checking hook; the same
+ * per-block decode the expert kernels use).  blocks must be 4-byte aligned. */
+int wm_dequant(int qtype, const void* blocks, int64_t nblocks, float* out, void* stream);
+
+/* Quantise n fp32 values (n a multiple of the block size) into qtype blocks.
+ * Used to build synthetic expert tensors.  wm_quantize_host is the same
+ * quantiser on host memory, bit-identical to the device one. */
+int wm_quantize(int qtype, const float* x, int64_t n, void* blocks, void* stream);
+int wm_quantize_host(int qtype, const float* x, int64_t n, void* blocks);
+
+/* y[r] = sum_c W[r][c] x[c] for one raw quantised matrix [rows][in/QK]
+ * (quant_matvec, engine/runtime/transformer.h:157-194, on the GPU). */
+int wm_quant_matvec(int qtype, const void* W, const float* x, int rows, int in, float* y,
+                    void* ws, int64_t ws_bytes, void* stream);
+
+/* Router + top-K on the GPU: reference-order fp32 logits, K-pass arg-max with
+ * ties to the lower index, softmax over the K picks
+ * (router_topk, engine/runtime/transformer.h:107-152).  ids/w are device
+ * arrays of length K.  Needs a workspace of wm_router_workspace_size(E). */
+int64_t wm_router_workspace_size(int E);
+/* Router logits only, fp32 [E], bit-identical to the reference's fp32 AVX-512
+ * accumulation (quant_matvec default case, transformer.h:172-191; the device
+ * counterpart of gpu_router, gpu_offload.h:66-67). */
+int wm_router_logits(const float* x, const float* W_r, int H, int E, float* logits, void* stream);
+int wm_router_topk(const float* x, const float* W_r, int H, int E, int K, int32_t* ids, float* w,
+                   void* ws, int64_t ws_bytes, void* stream);
+
+/* Bytes of the fixed HBM workspace for a layer: routing trace of max_tokens
+ * entries, hit counters, activation scratch and the prefill buffers for up to
+ * max_tokens tokens.  < 0 on bad descriptor. */
+int64_t wm_workspace_size(const wm_layer_desc* d, int max_tokens);
+
+/* Clears the trace, counters and status of a workspace (stream-ordered). */
+int wm_workspace_reset(const wm_layer_desc* d, int max_tokens, void* ws, int64_t ws_bytes, void* stream);
+
+/* Host-synchronous read of the workspace status bits (WM_STATUS_*). */
+int wm_workspace_status(void* ws, int64_t ws_bytes, int32_t* status_out);
+
+/* Device offsets (bytes from ws) of the routing trace: ids int32 [max_tokens][K],
+ * weights fp32 [max_tokens][K], hit counters uint32 [E]. */
+int wm_workspace_trace(const wm_layer_desc* d, int max_tokens, int64_t* ids_off, int64_t* w_off,
+                       int64_t* hits_off);
+
+/* One decode token through the MoE block (winmoe_inference.c:1684-2027):
+ * router -> top-K -> K experts (gate/up -> SwiGLU -> down) -> weighted
+ * combine -> shared expert with its sigmoid gate.  x fp32[H] in, out fp32[H]
+ * = moe_out before the residual add.  step selects the trace entry
+ * (step % max_tokens).  No host synchronisation. */
+int wm_moe_decode(const wm_layer_desc* d, const float* x, float* out, void* ws, int64_t ws_bytes,
+                  int max_tokens, int step, void* stream);
+
+/* Same with routing supplied by the caller: ids int32[K], w fp32[K] (device).
+ * Out-of-range ids set WM_STATUS_BAD_EXPERT_ID and contribute zero. */
+int wm_moe_decode_forced(const wm_layer_desc* d, const float* x, const int32_t* ids, const float* w,
+                         float* out, void* ws, int64_t ws_bytes, int max_tokens, int step, void* stream);
+
+/* Batched prefill of T tokens: x bf16 [T][H], out fp32 [T][H].  Routes every
+ * token, sorts (token, slot) pairs by expert in the workspace, runs grouped
+ * expert GEMMs on MFMA and a weighted gather-combine.  T <= max_tokens. */
+int wm_moe_prefill(const wm_layer_desc* d, const uint16_t* x_bf16, int T, float* out, void* ws,
+                   int64_t ws_bytes, int max_tokens, void* stream);
+
+/* One expert FFN: out = down(SwiGLU(gate x, up x)) (gpu_expert_ffn_fused's
+ * maths on device pointers, any supported types). */
+int wm_expert_ffn(const void* gate, int gate_type, const void* up, int up_type, const void* down,
+                  int down_type, const float* x, int H, int I, float* out, void* ws, int64_t ws_bytes,
+                  void* stream);
+int64_t wm_expert_workspace_size(int H, int I);
+
+/* ------------------------------------------------------------ profiling */
+/* Per-phase device timers of wm_moe_decode / wm_moe_decode_forced /
+ * wm_moe_prefill, the counterpart of the reference's per-phase
+ * QueryPerformanceCounter accumulators (winmoe_inference.c:1031-1037,
+ * 1685-1697, 1795-1806): when enabled, every phase launch is bracketed by HIP
+ * events on the caller's stream.  wm_profile_read synchronises those events
+ * and returns, per phase, the summed milliseconds and the launch count since
+ * the last read (arrays of WM_PROF_NPHASE; names via wm_profile_phase_name). */
+#define WM_PROF_NPHASE 8
+int wm_profile_enable(int on);
+int wm_profile_read(double* ms, int64_t* count, int nphase);
+const char* wm_profile_phase_name(int phase);
+
+/* ------------------------------- reference-compatible shims (host pointers) */
+/* engine/runtime/gpu_offload.h:18-21 */
+int gpu_init(void);
+void gpu_shutdown(void);
+int gpu_is_initialized(void);
+float gpu_vram_used_mb(void);
+/* engine/runtime/gpu_offload.h:66-67 */
+int gpu_upload_router(int layer, const float* weights, int hidden_dim, int num_experts);
+int gpu_router(int layer, const float* normed, int hidden_dim, float* logits_out, int num_experts);
+/* engine/runtime/gpu_offload.h:70-74: copy one expert's raw [gate|up|down]
+ * blocks into HBM; returns the slot or -1.  The quant types are inferred from
+ * the byte sizes at compute time (every supported type has a distinct
+ * bytes-per-weight ratio); gpu_cache_expert_typed records them explicitly. */
+int gpu_cache_expert(int layer, int expert_id, const void* gate_data, int gate_size,
+                     const void* up_data, int up_size, const void* down_data, int down_size);
+int gpu_cache_expert_typed(int layer, int expert_id, const void* gate_data, int gate_size, int gate_type,
+                           const void* up_data, int up_size, int up_type, const void* down_data,
+                           int down_size, int down_type);
+int gpu_find_cached_expert(int layer, int expert_id);                      /* gpu_offload.h:75 */
+/* gpu_offload.h:76-80: gate/up outputs (pre-SwiGLU) and the expert output. */
+int gpu_expert_ffn(int cache_idx, const float* input, int hidden_dim, int intermediate, float* gate_out,
+                   float* up_out, float* expert_out, int gate_type, int down_type);
+int gpu_expert_down(int cache_idx, const float* act, int intermediate, float* output, int hidden_dim);
+/* gpu_offload.h:82-83: gate+up+SwiGLU+down on the GPU, blocking. */
+int gpu_expert_ffn_fused(int cache_idx, const float* input, int hidden_dim, int intermediate,
+                         float* expert_out);
+/* gpu_offload.h:86-88 */
+int gpu_expert_batch_start(const float* normed, int hidden_dim);
+int gpu_expert_batch_add(int cache_idx, int hidden_dim, int intermediate, float weight);
+int gpu_expert_batch_finish(float* moe_out, int hidden_dim);
+int gpu_expert_cache_count(void);                                           /* gpu_offload.h:90 */
+void gpu_set_expert_limit(int limit);                                       /* gpu_offload.h:93 */
+
+#ifdef __cplusplus
+}
+#endif
+#endif

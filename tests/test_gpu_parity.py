@@ -1,0 +1,308 @@
+"""GPU parity: the HIP path through the C-ABI vs the CPU oracle on the same bytes.
+
+Bars: dequantised weights and router logits bit-exact, top-K ids exact,
+routing weights within 2 ulp (device expf), expert / layer outputs rel-L2
+<= 1e-3 against the oracle's fp32-dequant + fp64 maths.
+"""
+import numpy as np
+import pytest
+
+from golden.blocks import Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, rand_blocks
+from helpers import rel_l2, same_bits_nan, ulp_diff
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K]
+LAYER_TOL = 1e-3          # rel-L2 of layer / expert outputs vs the fp64 oracle
+MATVEC_TOL = 2e-4         # rel-L2 of a single quantised matrix-vector product
+
+
+@pytest.fixture(scope="module")
+def wm():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    import winmoe_amd
+    winmoe_amd.load()
+    return winmoe_amd
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+# ------------------------------------------------------------------ dequant / quantise
+
+@pytest.mark.parametrize("t", TYPES)
+def test_dequant_bit_exact(wm, orc, t):
+    rng = np.random.default_rng(100 + t)
+    for nb in (1, 3, 16, 17, 129, 1000):
+        case(f"dequant type={t} nblocks={nb}")
+        blocks = rand_blocks(t, nb, rng, lo=1e-6, hi=30.0)
+        got = host(wm.dequantize(dev(blocks.reshape(-1)), t))
+        assert same_bits_nan(got, orc.dequant(t, blocks)), (t, nb)
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_dequant_special_scales(wm, orc, t):
+    from golden.blocks import SCALE_FIELDS
+    rng = np.random.default_rng(7 + t)
+    specials = np.array([0x0000, 0x8000, 0x0001, 0x03FF, 0x0400, 0x7BFF, 0x7C00, 0xFC00, 0x7E00, 0x3C00],
+                        np.uint16)
+    blocks = rand_blocks(t, len(specials) * 2, rng)
+    d_off, m_off = SCALE_FIELDS[t]
+    for i, s in enumerate(specials):
+        blocks[i, d_off:d_off + 2] = np.array([s], np.uint16).view(np.uint8)
+        if m_off is not None:
+            blocks[len(specials) + i, m_off:m_off + 2] = np.array([s], np.uint16).view(np.uint8)
+    case(f"dequant special fp16 scales type={t}")
+    got = host(wm.dequantize(dev(blocks.reshape(-1)), t))
+    assert same_bits_nan(got, orc.dequant(t, blocks))
+
+
+def test_dequant_rejects_misaligned(wm):
+    import torch
+    buf = torch.zeros(34 * 8, dtype=torch.uint8, device="cuda")
+    with pytest.raises(wm.WinMoEError):
+        wm.dequantize(buf[34:34 * 4], Q8_0)        # 34-byte offset: 2-byte aligned only
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_quantize_device_matches_host(wm, t):
+    import ctypes as C
+    rng = np.random.default_rng(t)
+    x = (rng.standard_normal(256 * 300) * 0.02).astype(np.float32)
+    x[:256] *= 1e-30      # tiny values, subnormal fp16 scales
+    x[256:512] = 0.0
+    case(f"quantize type={t}")
+    got = host(wm.quantize(dev(x), t))
+    ref = np.zeros_like(got)
+    assert wm.load().wm_quantize_host(t, x.ctypes.data, x.size, ref.ctypes.data) == 0
+    assert np.array_equal(got, ref)
+
+
+# ------------------------------------------------------------------ router
+
+def router_case(E, H, seed, tie=False, nan_row=None):
+    rng = np.random.default_rng(seed)
+    W = (rng.standard_normal((E, H), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    x = rng.standard_normal(H, dtype=np.float32)
+    if tie:
+        top = int(np.argmax(W.astype(np.float64) @ x.astype(np.float64)))
+        W[0] = W[top]
+        W[E - 1] = W[top]
+    if nan_row is not None:
+        W[nan_row, 5] = np.nan
+    return x, W
+
+
+@pytest.mark.parametrize("E,H,K,seed,tie", [(512, 4096, 10, 1, False), (512, 4096, 3, 2, True),
+                                            (64, 2048, 4, 3, False), (64, 512, 4, 4, True),
+                                            (100, 1000, 7, 5, False), (1024, 256, 16, 6, True)])
+def test_router_bit_exact(wm, orc, E, H, K, seed, tie):
+    x, W = router_case(E, H, seed, tie=tie, nan_row=E // 3)
+    case(f"router E={E} H={H} K={K}")
+    lg = host(wm.router_logits(dev(x), dev(W)))
+    assert same_bits_nan(lg, orc.router_logits(x, W))
+    ids, w = wm.router_topk(dev(x), dev(W), K)
+    oid, ow, _ = orc.router_topk(x, W, K)
+    assert host(ids).tolist() == oid.tolist()
+    assert ulp_diff(host(w), ow).max() <= 2
+    if tie:
+        assert host(ids)[:3].tolist()[0] == 0
+
+
+# ------------------------------------------------------------------ matvec / expert
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("inp", [256, 512, 1024, 2048, 4096])
+def test_quant_matvec(wm, orc, t, inp):
+    rng = np.random.default_rng(inp + t)
+    rows = 96
+    nb = rows * inp // orc.BLOCK_ELEMS[t]
+    W = rand_blocks(t, nb, rng)
+    x = rng.standard_normal(inp).astype(np.float32)
+    case(f"matvec type={t} in={inp}")
+    y = host(wm.quant_matvec(dev(W.reshape(-1)), dev(x), rows, inp, t))
+    want = orc.matvec(t, W, x, rows, inp)
+    assert rel_l2(y, want) <= MATVEC_TOL
+
+
+@pytest.mark.parametrize("types", [(Q8_0, Q8_0, Q8_0), (Q4_K, Q4_K, Q6_K), (Q2_K, Q2_K, Q3_K), (Q5_K, Q5_K, Q5_K),
+                                   (Q4_K, Q8_0, Q2_K)])
+def test_expert_ffn(wm, orc, types):
+    import torch
+    H, I = 4096, 1024
+    g = torch.Generator(device="cuda").manual_seed(5)
+    gt, ut, dt = types
+    mats = []
+    for t, r, c in ((gt, I, H), (ut, I, H), (dt, H, I)):
+        w = torch.randn(r * c, generator=g, device="cuda") * 0.02
+        mats.append(wm.quantize(w, t))
+    x = torch.randn(H, generator=g, device="cuda")
+    case(f"expert_ffn types={types}")
+    y = host(wm.expert_ffn(*mats, x, H, I, types))
+    want = orc.expert_ffn(host(mats[0]), gt, host(mats[1]), ut, host(mats[2]), dt, host(x), H, I)
+    assert rel_l2(y, want) <= LAYER_TOL
+
+
+# ------------------------------------------------------------------ MoE layer
+
+def oracle_token(orc, sl, x, ids=None, w=None):
+    """fp64 MoE block for one token over the synthetic layer's bytes."""
+    from winmoe_amd.moe import matrix_bytes
+    cfg, L = sl.cfg, sl.layer
+    H, I, K = cfg.H, cfg.I, cfg.K
+    if ids is None:
+        ids, w, _ = orc.router_topk(x, host(sl.router), K)
+    gt, ut, dt = cfg.types
+    pg, pu, pd = matrix_bytes(gt, I, H), matrix_bytes(ut, I, H), matrix_bytes(dt, H, I)
+    out = np.zeros(H)
+    for k, e in enumerate(ids):
+        e = int(e)
+        y = orc.expert_ffn(host(sl.gate[e * pg:(e + 1) * pg]), gt, host(sl.up[e * pu:(e + 1) * pu]), ut,
+                           host(sl.down[e * pd:(e + 1) * pd]), dt, x, H, I)
+        out += float(w[k]) * y
+    if sl.shared is not None:
+        s = sl.shared
+        Is = s.inter or I
+        ys = orc.expert_ffn(host(s.gate), s.types[0], host(s.up), s.types[1], host(s.down), s.types[2], x, H, Is)
+        gate = 1.0
+        if s.gate_inp is not None:
+            gate = orc.lib().wmo_sigmoid(float(host(s.gate_inp).astype(np.float64) @ x.astype(np.float64)))
+        out += gate * ys
+    return np.asarray(ids), np.asarray(w), out
+
+
+def decode_check(wm, orc, cfg, E, tokens, seed_offset=0):
+    from winmoe_amd import synth
+    sl = synth.build_layer(cfg, E=E, max_tokens=max(tokens, 4))
+    X = synth.make_hidden(cfg, tokens=tokens, seed_offset=seed_offset)
+    for t in range(tokens):
+        case(f"decode {cfg.name} E={E} token={t}")
+        out = host(sl.layer.decode(X[t]))
+        ids_t, w_t = sl.layer.trace()
+        xi = host(X[t])
+        oid, ow, ref = oracle_token(orc, sl, xi)
+        assert host(ids_t[t]).tolist() == oid.tolist(), t
+        assert ulp_diff(host(w_t[t]), ow).max() <= 2
+        assert rel_l2(out, ref) <= LAYER_TOL, (t, rel_l2(out, ref))
+    assert sl.layer.status() == 0
+    return sl
+
+
+def test_decode_c1_full(wm, orc):
+    from winmoe_amd import synth
+    cfg = synth.CONFIGS["c1"]
+    decode_check(wm, orc, cfg, E=cfg.E, tokens=3)
+
+
+def test_decode_c2_shape_small_e(wm, orc):
+    from winmoe_amd import synth
+    decode_check(wm, orc, synth.CONFIGS["c2"], E=24, tokens=3)
+
+
+def test_decode_c2_full(wm, orc):
+    from winmoe_amd import synth
+    sl = decode_check(wm, orc, synth.CONFIGS["c2"], E=512, tokens=2)
+    hits = host(sl.layer.hits())
+    assert hits.sum() == 2 * 10
+
+
+def test_decode_c3_types(wm, orc):
+    from winmoe_amd import synth
+    decode_check(wm, orc, synth.CONFIGS["c3"], E=16, tokens=3)
+
+
+def test_decode_forced_c4_types(wm, orc):
+    import torch
+    from winmoe_amd import synth
+    cfg = synth.CONFIGS["c4"]
+    E, T = 24, 4
+    sl = synth.build_layer(cfg, E=E, max_tokens=8)
+    X = synth.make_hidden(cfg, tokens=T)
+    ids, w = synth.forced_routes(cfg, E=E, tokens=T)
+    for t in range(T):
+        case(f"forced decode {cfg.name} token={t}")
+        out = host(sl.layer.decode_forced(X[t], dev(ids[t]), dev(w[t])))
+        _, _, ref = oracle_token(orc, sl, host(X[t]), ids[t], w[t])
+        assert rel_l2(out, ref) <= LAYER_TOL
+    tid, tw = sl.layer.trace()
+    assert np.array_equal(host(tid[:T]), ids) and np.array_equal(host(tw[:T]), w)
+    assert sl.layer.status() == 0
+    del torch
+
+
+def test_forced_bad_expert_id_flags_and_zeroes(wm, orc):
+    from winmoe_amd import synth
+    cfg = synth.CONFIGS["c1"]
+    sl = synth.build_layer(cfg, E=8, max_tokens=4)
+    x = synth.make_hidden(cfg, tokens=1)[0]
+    ids = np.array([1, 99, 2, -1], np.int32)
+    w = np.array([0.4, 0.3, 0.2, 0.1], np.float32)
+    case("forced decode with out-of-range ids")
+    out = host(sl.layer.decode_forced(x, dev(ids), dev(w)))
+    assert sl.layer.status() & wm._lib.STATUS_BAD_EXPERT_ID
+    _, _, ref = oracle_token(orc, sl, host(x), np.array([1, 2]), np.array([0.4, 0.2]))
+    assert rel_l2(out, ref) <= LAYER_TOL
+
+
+def test_decode_deterministic(wm):
+    from winmoe_amd import synth
+    cfg = synth.CONFIGS["c2"]
+    sl = synth.build_layer(cfg, E=16, max_tokens=4)
+    x = synth.make_hidden(cfg, tokens=1)[0]
+    case("decode determinism")
+    a = host(sl.layer.decode(x))
+    b = host(sl.layer.decode(x))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# ------------------------------------------------------------------ gpu_offload.h shims
+
+def test_legacy_expert_cache_and_ffn(wm, orc):
+    import ctypes as C
+    import torch
+    L = wm.load()
+    H, I = 4096, 1024
+    g = torch.Generator(device="cuda").manual_seed(9)
+    mats = [host(wm.quantize(torch.randn(r * c, generator=g, device="cuda") * 0.02, t))
+            for t, r, c in ((Q4_K, I, H), (Q4_K, I, H), (Q5_K, H, I))]
+    x = np.random.default_rng(0).standard_normal(H).astype(np.float32)
+    case("legacy gpu_* shims")
+    assert L.gpu_init() == 0 and L.gpu_is_initialized() == 1
+    slot = L.gpu_cache_expert(3, 213, mats[0].ctypes.data, mats[0].size, mats[1].ctypes.data, mats[1].size,
+                              mats[2].ctypes.data, mats[2].size)
+    assert slot >= 0 and L.gpu_find_cached_expert(3, 213) == slot and L.gpu_find_cached_expert(3, 212) == -1
+    out = np.zeros(H, np.float32)
+    assert L.gpu_expert_ffn_fused(slot, x.ctypes.data, H, I, out.ctypes.data) == 0
+    want = orc.expert_ffn(mats[0], Q4_K, mats[1], Q4_K, mats[2], Q5_K, x, H, I)
+    assert rel_l2(out, want) <= LAYER_TOL
+    go, uo, eo = np.zeros(I, np.float32), np.zeros(I, np.float32), np.zeros(H, np.float32)
+    assert L.gpu_expert_ffn(slot, x.ctypes.data, H, I, go.ctypes.data, uo.ctypes.data, eo.ctypes.data, 12, 13) == 0
+    assert rel_l2(go, orc.matvec(Q4_K, mats[0], x, I, H)) <= MATVEC_TOL
+    # batch API: two weighted copies of the same expert
+    acc = np.zeros(H, np.float32)
+    assert L.gpu_expert_batch_start(x.ctypes.data, H) == 0
+    assert L.gpu_expert_batch_add(slot, H, I, C.c_float(0.25)) == 0
+    assert L.gpu_expert_batch_add(slot, H, I, C.c_float(0.5)) == 0
+    assert L.gpu_expert_batch_finish(acc.ctypes.data, H) == 0
+    assert rel_l2(acc, 0.75 * want) <= LAYER_TOL
+    # router shim
+    E = 64
+    W = (np.random.default_rng(1).standard_normal((E, H)) * 0.02).astype(np.float32)
+    lg = np.zeros(E, np.float32)
+    assert L.gpu_upload_router(0, W.ctypes.data, H, E) == 0
+    assert L.gpu_router(0, x.ctypes.data, H, lg.ctypes.data, E) == 0
+    assert same_bits_nan(lg, orc.router_logits(x, W))
+    assert L.gpu_expert_cache_count() == 1 and L.gpu_vram_used_mb() > 0
+    L.gpu_shutdown()
+    assert L.gpu_is_initialized() == 0

@@ -1,0 +1,819 @@
+// wm_capi.hip -- the extern "C" surface of libwinmoe_hip.so (include/winmoe_hip.h):
+// argument validation, the fixed workspace layout, stream-ordered
+// orchestration of the expert kernels, and the gpu_* shims of
+// engine/runtime/gpu_offload.h.  Host code only.
+#include <hip/hip_runtime.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "../../include/winmoe_hip.h"
+#include "wm_launch.h"
+#include "wm_quant.h"
+
+using namespace wm;
+
+#define WM_FAIL_HIP(expr)                                                                                  \
+    do {                                                                                                   \
+        hipError_t e_ = (hipError_t)(expr);                                                                \
+        if (e_ != hipSuccess) {                                                                            \
+            fprintf(stderr, "winmoe_hip: HIP error at %s:%d: %s\n", __FILE__, __LINE__, hipGetErrorString(e_)); \
+            return WM_ERR;                                                                                 \
+        }                                                                                                  \
+    } while (0)
+
+#define WM_CHECK_ARG(cond)                                                                \
+    do {                                                                                  \
+        if (!(cond)) {                                                                    \
+            fprintf(stderr, "winmoe_hip: invalid argument (%s) in %s\n", #cond, __func__); \
+            return WM_EINVAL;                                                             \
+        }                                                                                 \
+    } while (0)
+
+static inline hipStream_t S(void* s) { return (hipStream_t)s; }
+static inline bool al(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+static inline int64_t up256(int64_t v) { return (v + 255) & ~(int64_t)255; }
+
+static bool g_dev_ready = false;
+
+// ------------------------------------------------------------------ phase profiler
+namespace {
+enum Phase { PH_ROUTER = 0, PH_TOPK, PH_XPREP, PH_GATEUP, PH_ACTPREP, PH_DOWN, PH_COMBINE, PH_STEP };
+const char* kPhaseNames[WM_PROF_NPHASE] = {"router_logits", "topk", "x_operand", "gate_up_swiglu",
+                                           "act_operand", "down", "combine", "step"};
+struct Prof {
+    bool on = false;
+    std::vector<hipEvent_t> pool;                 // free events
+    std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> pending;
+    double ms[WM_PROF_NPHASE] = {0};
+    int64_t cnt[WM_PROF_NPHASE] = {0};
+};
+Prof P;
+
+hipEvent_t prof_event() {
+    if (!P.pool.empty()) {
+        hipEvent_t e = P.pool.back();
+        P.pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+// Brackets one phase on stream s when profiling is on.
+struct PhaseTimer {
+    int ph;
+    hipStream_t s;
+    hipEvent_t a = nullptr, b = nullptr;
+    PhaseTimer(int phase, hipStream_t st) : ph(phase), s(st) {
+        if (!P.on) return;
+        a = prof_event();
+        b = prof_event();
+        if (a && b) (void)hipEventRecord(a, s);
+    }
+    ~PhaseTimer() {
+        if (!a || !b) return;
+        (void)hipEventRecord(b, s);
+        P.pending.push_back({ph, {a, b}});
+    }
+};
+}  // namespace
+
+extern "C" int wm_profile_enable(int on) {
+    P.on = on != 0;
+    return WM_OK;
+}
+
+extern "C" int wm_profile_read(double* ms, int64_t* count, int nphase) {
+    WM_CHECK_ARG(nphase >= 0 && nphase <= WM_PROF_NPHASE);
+    for (auto& p : P.pending) {
+        float t = 0.0f;
+        WM_FAIL_HIP(hipEventSynchronize(p.second.second));
+        WM_FAIL_HIP(hipEventElapsedTime(&t, p.second.first, p.second.second));
+        P.ms[p.first] += t;
+        P.cnt[p.first] += 1;
+        P.pool.push_back(p.second.first);
+        P.pool.push_back(p.second.second);
+    }
+    P.pending.clear();
+    for (int i = 0; i < nphase; i++) {
+        if (ms) ms[i] = P.ms[i];
+        if (count) count[i] = P.cnt[i];
+        P.ms[i] = 0.0;
+        P.cnt[i] = 0;
+    }
+    return WM_OK;
+}
+
+extern "C" const char* wm_profile_phase_name(int phase) {
+    return (phase >= 0 && phase < WM_PROF_NPHASE) ? kPhaseNames[phase] : "";
+}
+
+extern "C" int wm_init(void) {
+    if (g_dev_ready) return WM_OK;
+    int n = 0;
+    WM_FAIL_HIP(hipGetDeviceCount(&n));
+    if (n <= 0) {
+        fprintf(stderr, "winmoe_hip: no HIP device\n");
+        return WM_ERR;
+    }
+    g_dev_ready = true;
+    return WM_OK;
+}
+
+extern "C" const char* wm_version(void) { return "winmoe_hip 0.1 (gfx950)"; }
+extern "C" int wm_block_bytes(int t) { return block_bytes(t); }
+extern "C" int wm_block_elems(int t) { return block_elems(t); }
+
+// ------------------------------------------------------------------ simple entry points
+
+extern "C" int wm_dequant(int t, const void* blocks, int64_t nblocks, float* out, void* stream) {
+    WM_CHECK_ARG(supported(t));
+    WM_CHECK_ARG(nblocks >= 0);
+    if (nblocks == 0) return WM_OK;
+    WM_CHECK_ARG(blocks && out && al(blocks, 4) && al(out, 4));
+    if (wm_init()) return WM_ERR;
+    WM_FAIL_HIP(launch_dequant(t, blocks, nblocks, out, S(stream)));
+    return WM_OK;
+}
+
+extern "C" int wm_quantize(int t, const float* x, int64_t n, void* blocks, void* stream) {
+    WM_CHECK_ARG(supported(t));
+    WM_CHECK_ARG(n >= 0 && n % block_elems(t) == 0);
+    if (n == 0) return WM_OK;
+    WM_CHECK_ARG(x && blocks);
+    if (wm_init()) return WM_ERR;
+    WM_FAIL_HIP(launch_quantize(t, x, n / block_elems(t), blocks, S(stream)));
+    return WM_OK;
+}
+
+extern "C" int wm_quantize_host(int t, const float* x, int64_t n, void* blocks) {
+    WM_CHECK_ARG(supported(t));
+    WM_CHECK_ARG(n >= 0 && n % block_elems(t) == 0);
+    WM_CHECK_ARG(n == 0 || (x && blocks));
+    int64_t nb = n / block_elems(t);
+    for (int64_t b = 0; b < nb; b++)
+        quant_block(t, x + b * block_elems(t), (uint8_t*)blocks + b * block_bytes(t));
+    return WM_OK;
+}
+
+static int check_matrix(int t, const void* W, int in) {
+    if (!gemv_shape_ok(t, in)) {
+        fprintf(stderr, "winmoe_hip: unsupported matrix shape: type %d, in %d (in must be 64..4096, a power-of-two "
+                        "multiple of 64 and of the block size)\n", t, in);
+        return WM_EINVAL;
+    }
+    if (!al(W, 16)) {
+        fprintf(stderr, "winmoe_hip: expert tensor base must be 16-byte aligned\n");
+        return WM_EINVAL;
+    }
+    return WM_OK;
+}
+
+static int64_t xop_bytes(int in) { return (int64_t)(in / SEG) * XOP_DW * 4; }
+
+extern "C" int wm_quant_matvec(int t, const void* W, const float* x, int rows, int in, float* y, void* ws,
+                               int64_t ws_bytes, void* stream) {
+    WM_CHECK_ARG(supported(t) && W && x && y && rows >= 0);
+    if (int rc = check_matrix(t, W, in)) return rc;
+    WM_CHECK_ARG(ws && al(ws, 256) && ws_bytes >= xop_bytes(in));
+    if (rows == 0) return WM_OK;
+    if (wm_init()) return WM_ERR;
+    hipStream_t s = S(stream);
+    uint32_t* xop = (uint32_t*)ws;
+    XPrepArgs xp = {0, 1, in, x, nullptr, 0, xop, 0, nullptr, 0};
+    WM_FAIL_HIP(launch_xprep(t, xp, s));
+    GemvArgs g = {};
+    g.m = MatSet{(const uint8_t*)W, 0, nullptr, 1, 1, nullptr};
+    g.slot0 = 0;
+    g.rows = rows;
+    g.in = in;
+    g.xop = xop;
+    g.y = y;
+    WM_FAIL_HIP(launch_gemv(t, g, 1, s));
+    return WM_OK;
+}
+
+extern "C" int64_t wm_router_workspace_size(int E) { return E > 0 ? up256((int64_t)E * 4) + 256 : WM_EINVAL; }
+
+extern "C" int wm_router_logits(const float* x, const float* W, int H, int E, float* logits, void* stream) {
+    WM_CHECK_ARG(x && W && logits && H > 0 && E > 0);
+    WM_CHECK_ARG(2 * (int64_t)H * 4 <= 65536);
+    if (wm_init()) return WM_ERR;
+    WM_FAIL_HIP(launch_router_logits(x, W, H, E, logits, S(stream)));
+    return WM_OK;
+}
+
+extern "C" int wm_router_topk(const float* x, const float* W, int H, int E, int K, int32_t* ids, float* w, void* ws,
+                              int64_t ws_bytes, void* stream) {
+    WM_CHECK_ARG(x && W && ids && w && H > 0 && E > 0 && E <= 1024 && K >= 1 && K <= 16 && K <= E);
+    WM_CHECK_ARG(2 * (int64_t)H * 4 <= 65536);
+    WM_CHECK_ARG(ws && al(ws, 256) && ws_bytes >= wm_router_workspace_size(E));
+    if (wm_init()) return WM_ERR;
+    hipStream_t s = S(stream);
+    float* logits = (float*)ws;
+    int32_t* status = (int32_t*)((uint8_t*)ws + up256((int64_t)E * 4));
+    WM_FAIL_HIP(launch_router_logits(x, W, H, E, logits, s));
+    WM_FAIL_HIP(launch_topk(logits, E, K, ids, w, nullptr, status, s));
+    return WM_OK;
+}
+
+// ------------------------------------------------------------------ layer descriptor + workspace
+
+struct WsLayout {
+    int64_t status, logits, tr_ids, tr_w, hits, shgate, xop, gbuf, ubuf, act, actop, ypart, total;
+    int K1, Imax, Is;
+};
+
+static int Ishared(const wm_layer_desc* d) { return d->inter_shared > 0 ? d->inter_shared : d->inter; }
+static bool has_shared(const wm_layer_desc* d) { return d->sh_gate && d->sh_up && d->sh_down; }
+
+static int validate_desc(const wm_layer_desc* d, bool need_router) {
+    WM_CHECK_ARG(d);
+    WM_CHECK_ARG(d->hidden > 0 && d->inter > 0 && d->n_experts > 0 && d->n_experts <= 1024);
+    WM_CHECK_ARG(d->top_k >= 1 && d->top_k <= 16 && d->top_k <= d->n_experts);
+    WM_CHECK_ARG(d->gate_exps && d->up_exps && d->down_exps);
+    if (int rc = check_matrix(d->gate_type, d->gate_exps, d->hidden)) return rc;
+    if (int rc = check_matrix(d->up_type, d->up_exps, d->hidden)) return rc;
+    if (int rc = check_matrix(d->down_type, d->down_exps, d->inter)) return rc;
+    WM_CHECK_ARG(d->gate_stride >= 0 && d->up_stride >= 0 && d->down_stride >= 0);
+    WM_CHECK_ARG(d->gate_stride % 16 == 0 && d->up_stride % 16 == 0 && d->down_stride % 16 == 0);
+    if (need_router) {
+        WM_CHECK_ARG(d->router != nullptr);
+        WM_CHECK_ARG(2 * (int64_t)d->hidden * 4 <= 65536);
+    }
+    if (has_shared(d)) {
+        int Is = Ishared(d);
+        if (int rc = check_matrix(d->sh_gate_type, d->sh_gate, d->hidden)) return rc;
+        if (int rc = check_matrix(d->sh_up_type, d->sh_up, d->hidden)) return rc;
+        if (int rc = check_matrix(d->sh_down_type, d->sh_down, Is)) return rc;
+    } else {
+        WM_CHECK_ARG(!d->sh_gate && !d->sh_up && !d->sh_down);
+    }
+    return WM_OK;
+}
+
+static WsLayout layout(const wm_layer_desc* d, int max_tokens) {
+    WsLayout L;
+    int K = d->top_k, E = d->n_experts, H = d->hidden;
+    L.K1 = K + 1;
+    L.Is = Ishared(d);
+    L.Imax = std::max(d->inter, L.Is);
+    int64_t o = 0;
+    L.status = o; o += 256;
+    L.logits = o; o += up256((int64_t)E * 4);
+    L.tr_ids = o; o += up256((int64_t)max_tokens * K * 4);
+    L.tr_w = o; o += up256((int64_t)max_tokens * K * 4);
+    L.hits = o; o += up256((int64_t)E * 4);
+    L.shgate = o; o += 256;
+    L.xop = o; o += 4 * up256(xop_bytes(H));
+    L.gbuf = o; o += up256((int64_t)L.K1 * L.Imax * 4);
+    L.ubuf = o; o += up256((int64_t)L.K1 * L.Imax * 4);
+    L.act = o; o += up256((int64_t)L.K1 * L.Imax * 4);
+    L.actop = o; o += up256((int64_t)L.K1 * xop_bytes(L.Imax));
+    L.ypart = o; o += up256((int64_t)L.K1 * H * 4);
+    L.total = o;
+    return L;
+}
+
+extern "C" int64_t wm_workspace_size(const wm_layer_desc* d, int max_tokens) {
+    if (!d || max_tokens <= 0 || d->top_k <= 0 || d->n_experts <= 0 || d->hidden <= 0 || d->inter <= 0) return WM_EINVAL;
+    return layout(d, max_tokens).total;
+}
+
+extern "C" int wm_workspace_trace(const wm_layer_desc* d, int max_tokens, int64_t* ids_off, int64_t* w_off,
+                                  int64_t* hits_off) {
+    WM_CHECK_ARG(d && max_tokens > 0 && d->top_k > 0 && d->n_experts > 0);
+    WsLayout L = layout(d, max_tokens);
+    if (ids_off) *ids_off = L.tr_ids;
+    if (w_off) *w_off = L.tr_w;
+    if (hits_off) *hits_off = L.hits;
+    return WM_OK;
+}
+
+extern "C" int wm_workspace_reset(const wm_layer_desc* d, int max_tokens, void* ws, int64_t ws_bytes, void* stream) {
+    WM_CHECK_ARG(d && ws && max_tokens > 0 && al(ws, 256));
+    int64_t total = wm_workspace_size(d, max_tokens);
+    WM_CHECK_ARG(total > 0 && ws_bytes >= total);
+    if (wm_init()) return WM_ERR;
+    WM_FAIL_HIP(launch_fill_i32((int32_t*)ws, 0, total / 4, S(stream)));
+    return WM_OK;
+}
+
+extern "C" int wm_workspace_status(void* ws, int64_t ws_bytes, int32_t* status_out) {
+    WM_CHECK_ARG(ws && status_out && ws_bytes >= 4);
+    if (wm_init()) return WM_ERR;
+    WM_FAIL_HIP(hipDeviceSynchronize());
+    WM_FAIL_HIP(hipMemcpy(status_out, ws, 4, hipMemcpyDeviceToHost));
+    return WM_OK;
+}
+
+// The expert part of one decode token, given routing already in the trace
+// entry (ids_d / w_d): gate/up + SwiGLU, activation operands, down, combine.
+static int run_experts(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, const float* x, const int32_t* ids_d,
+                       const float* w_d, float* out, hipStream_t s) {
+    const int H = d->hidden, I = d->inter, K = d->top_k, E = d->n_experts, Is = L.Is;
+    const bool sh = has_shared(d);
+    int32_t* status = (int32_t*)(ws + L.status);
+    float* act = (float*)(ws + L.act);
+    float* gbuf = (float*)(ws + L.gbuf);
+    float* ubuf = (float*)(ws + L.ubuf);
+    uint32_t* actop = (uint32_t*)(ws + L.actop);
+    float* ypart = (float*)(ws + L.ypart);
+    const int64_t act_stride = L.Imax, actop_stride = xop_bytes(L.Imax) / 4;
+
+    // activation operands of x, one per distinct input type
+    int types[4] = {d->gate_type, d->up_type, sh ? d->sh_gate_type : -1, sh ? d->sh_up_type : -1};
+    int tslot[16];
+    for (int i = 0; i < 16; i++) tslot[i] = -1;
+    int nts = 0;
+    uint32_t* xop = (uint32_t*)(ws + L.xop);
+    const int64_t xop_slot = up256(xop_bytes(H)) / 4;
+    {
+        PhaseTimer pt(PH_XPREP, s);
+        for (int i = 0; i < 4; i++) {
+            int t = types[i];
+            if (t < 0 || tslot[t] >= 0) continue;
+            tslot[t] = nts++;
+            XPrepArgs xp = {0, 1, H, x, nullptr, 0, xop + tslot[t] * xop_slot, 0, nullptr, 0};
+            WM_FAIL_HIP(launch_xprep(t, xp, s));
+        }
+        if (sh && d->sh_gate_inp) WM_FAIL_HIP(launch_shgate(x, d->sh_gate_inp, H, (float*)(ws + L.shgate), s));
+    }
+
+    MatSet mg = {(const uint8_t*)d->gate_exps, d->gate_stride ? d->gate_stride : matrix_bytes(d->gate_type, I, H),
+                 ids_d, K, E, (const uint8_t*)d->sh_gate};
+    MatSet mu = {(const uint8_t*)d->up_exps, d->up_stride ? d->up_stride : matrix_bytes(d->up_type, I, H), ids_d, K,
+                 E, (const uint8_t*)d->sh_up};
+    MatSet md = {(const uint8_t*)d->down_exps, d->down_stride ? d->down_stride : matrix_bytes(d->down_type, H, I),
+                 ids_d, K, E, (const uint8_t*)d->sh_down};
+
+    // gate/up (+ SwiGLU) for the routed slots [0, K) and the shared slot K
+    auto gate_up = [&](int slot0, int nslots, int gt, int ut, int rows) -> int {
+        if (gt == ut) {
+            GateUpArgs a = {};
+            a.gate = mg; a.up = mu;
+            a.slot0 = slot0; a.rows = rows; a.in = H;
+            a.xop = xop + tslot[gt] * xop_slot;
+            a.act = act; a.act_slot_stride = act_stride; a.status = status;
+            return launch_gateup(gt, a, nslots, s);
+        }
+        GemvArgs a = {};
+        a.slot0 = slot0; a.rows = rows; a.in = H; a.status = status;
+        a.m = mg; a.xop = xop + tslot[gt] * xop_slot; a.y = gbuf; a.y_slot_stride = act_stride;
+        if (int e = launch_gemv(gt, a, nslots, s)) return e;
+        a.m = mu; a.xop = xop + tslot[ut] * xop_slot; a.y = ubuf;
+        return launch_gemv(ut, a, nslots, s);
+    };
+    // activation operands of the SwiGLU output in the down type's layout
+    auto act_prep = [&](int slot0, int nslots, int gt, int ut, int dt, int rows) -> int {
+        XPrepArgs xp = {};
+        xp.nslots = nslots; xp.in = rows;
+        xp.out = actop + slot0 * actop_stride; xp.out_stride = actop_stride;
+        xp.src_stride = act_stride;
+        if (gt == ut) { xp.mode = 0; xp.src = act + slot0 * act_stride; }
+        else {
+            xp.mode = 1; xp.src = gbuf + slot0 * act_stride; xp.src2 = ubuf + slot0 * act_stride;
+            xp.act_out = act + slot0 * act_stride; xp.act_stride = act_stride;
+        }
+        return launch_xprep(dt, xp, s);
+    };
+    auto down = [&](int slot0, int nslots, int dt, int in) -> int {
+        GemvArgs a = {};
+        a.m = md; a.slot0 = slot0; a.rows = H; a.in = in; a.status = status;
+        a.xop = actop; a.xop_slot_stride = actop_stride; a.y = ypart; a.y_slot_stride = H;
+        return launch_gemv(dt, a, nslots, s);
+    };
+
+    const bool merge = sh && d->sh_gate_type == d->gate_type && d->sh_up_type == d->up_type &&
+                       d->sh_down_type == d->down_type && Is == I;
+    const int n_main = merge ? K + 1 : K;
+    {
+        PhaseTimer pt(PH_GATEUP, s);
+        WM_FAIL_HIP(gate_up(0, n_main, d->gate_type, d->up_type, I));
+        if (sh && !merge) WM_FAIL_HIP(gate_up(K, 1, d->sh_gate_type, d->sh_up_type, Is));
+    }
+    {
+        PhaseTimer pt(PH_ACTPREP, s);
+        WM_FAIL_HIP(act_prep(0, n_main, d->gate_type, d->up_type, d->down_type, I));
+        if (sh && !merge) WM_FAIL_HIP(act_prep(K, 1, d->sh_gate_type, d->sh_up_type, d->sh_down_type, Is));
+    }
+    {
+        PhaseTimer pt(PH_DOWN, s);
+        WM_FAIL_HIP(down(0, n_main, d->down_type, I));
+        if (sh && !merge) WM_FAIL_HIP(down(K, 1, d->sh_down_type, Is));
+    }
+
+    CombineArgs c = {};
+    c.ypart = ypart; c.y_stride = H; c.w = w_d; c.ids = ids_d; c.K = K; c.E = E; c.H = H;
+    c.has_shared = sh ? 1 : 0;
+    c.sh_gate = (sh && d->sh_gate_inp) ? (const float*)(ws + L.shgate) : nullptr;
+    c.out = out;
+    PhaseTimer pt(PH_COMBINE, s);
+    WM_FAIL_HIP(launch_combine(c, s));
+    return WM_OK;
+}
+
+extern "C" int wm_moe_decode(const wm_layer_desc* d, const float* x, float* out, void* ws, int64_t ws_bytes,
+                             int max_tokens, int step, void* stream) {
+    if (int rc = validate_desc(d, true)) return rc;
+    WM_CHECK_ARG(x && out && ws && al(ws, 256) && max_tokens > 0 && step >= 0);
+    WsLayout L = layout(d, max_tokens);
+    WM_CHECK_ARG(ws_bytes >= L.total);
+    if (wm_init()) return WM_ERR;
+    hipStream_t s = S(stream);
+    uint8_t* w8 = (uint8_t*)ws;
+    int slot = step % max_tokens;
+    int32_t* ids = (int32_t*)(w8 + L.tr_ids) + (int64_t)slot * d->top_k;
+    float* wts = (float*)(w8 + L.tr_w) + (int64_t)slot * d->top_k;
+    float* logits = (float*)(w8 + L.logits);
+    PhaseTimer step_timer(PH_STEP, s);
+    {
+        PhaseTimer pt(PH_ROUTER, s);
+        WM_FAIL_HIP(launch_router_logits(x, d->router, d->hidden, d->n_experts, logits, s));
+    }
+    {
+        PhaseTimer pt(PH_TOPK, s);
+        WM_FAIL_HIP(launch_topk(logits, d->n_experts, d->top_k, ids, wts, (uint32_t*)(w8 + L.hits),
+                                (int32_t*)(w8 + L.status), s));
+    }
+    return run_experts(d, L, w8, x, ids, wts, out, s);
+}
+
+extern "C" int wm_moe_decode_forced(const wm_layer_desc* d, const float* x, const int32_t* ids_in, const float* w_in,
+                                    float* out, void* ws, int64_t ws_bytes, int max_tokens, int step, void* stream) {
+    if (int rc = validate_desc(d, false)) return rc;
+    WM_CHECK_ARG(x && out && ids_in && w_in && ws && al(ws, 256) && max_tokens > 0 && step >= 0);
+    WsLayout L = layout(d, max_tokens);
+    WM_CHECK_ARG(ws_bytes >= L.total);
+    if (wm_init()) return WM_ERR;
+    hipStream_t s = S(stream);
+    uint8_t* w8 = (uint8_t*)ws;
+    int slot = step % max_tokens;
+    int32_t* ids = (int32_t*)(w8 + L.tr_ids) + (int64_t)slot * d->top_k;
+    float* wts = (float*)(w8 + L.tr_w) + (int64_t)slot * d->top_k;
+    PhaseTimer step_timer(PH_STEP, s);
+    WM_FAIL_HIP(hipMemcpyAsync(ids, ids_in, (size_t)d->top_k * 4, hipMemcpyDeviceToDevice, s));
+    WM_FAIL_HIP(hipMemcpyAsync(wts, w_in, (size_t)d->top_k * 4, hipMemcpyDeviceToDevice, s));
+    return run_experts(d, L, w8, x, ids, wts, out, s);
+}
+
+extern "C" int64_t wm_expert_workspace_size(int H, int I) {
+    if (H <= 0 || I <= 0) return WM_EINVAL;
+    return 256 + 2 * up256(xop_bytes(H)) + 3 * up256((int64_t)I * 4) + up256(xop_bytes(I));
+}
+
+extern "C" int wm_expert_ffn(const void* gate, int gt, const void* up, int ut, const void* down, int dt, const float* x,
+                             int H, int I, float* out, void* ws, int64_t ws_bytes, void* stream) {
+    WM_CHECK_ARG(gate && up && down && x && out && ws && al(ws, 256));
+    if (int rc = check_matrix(gt, gate, H)) return rc;
+    if (int rc = check_matrix(ut, up, H)) return rc;
+    if (int rc = check_matrix(dt, down, I)) return rc;
+    WM_CHECK_ARG(ws_bytes >= wm_expert_workspace_size(H, I));
+    if (wm_init()) return WM_ERR;
+    hipStream_t s = S(stream);
+    uint8_t* w8 = (uint8_t*)ws;
+    int32_t* status = (int32_t*)w8;
+    int64_t o = 256;
+    uint32_t* xop_g = (uint32_t*)(w8 + o); o += up256(xop_bytes(H));
+    uint32_t* xop_u = (uint32_t*)(w8 + o); o += up256(xop_bytes(H));
+    float* gb = (float*)(w8 + o); o += up256((int64_t)I * 4);
+    float* ub = (float*)(w8 + o); o += up256((int64_t)I * 4);
+    float* act = (float*)(w8 + o); o += up256((int64_t)I * 4);
+    uint32_t* actop = (uint32_t*)(w8 + o);
+    MatSet mg = {(const uint8_t*)gate, 0, nullptr, 1, 1, nullptr};
+    MatSet mu = {(const uint8_t*)up, 0, nullptr, 1, 1, nullptr};
+    MatSet md = {(const uint8_t*)down, 0, nullptr, 1, 1, nullptr};
+    XPrepArgs xp = {0, 1, H, x, nullptr, 0, xop_g, 0, nullptr, 0};
+    WM_FAIL_HIP(launch_xprep(gt, xp, s));
+    if (gt == ut) {
+        GateUpArgs a = {};
+        a.gate = mg; a.up = mu; a.rows = I; a.in = H; a.xop = xop_g; a.act = act; a.status = status;
+        WM_FAIL_HIP(launch_gateup(gt, a, 1, s));
+        XPrepArgs ap = {0, 1, I, act, nullptr, 0, actop, 0, nullptr, 0};
+        WM_FAIL_HIP(launch_xprep(dt, ap, s));
+    } else {
+        GemvArgs a = {};
+        a.m = mg; a.rows = I; a.in = H; a.xop = xop_g; a.y = gb; a.status = status;
+        WM_FAIL_HIP(launch_gemv(gt, a, 1, s));
+        XPrepArgs xu = {0, 1, H, x, nullptr, 0, xop_u, 0, nullptr, 0};
+        WM_FAIL_HIP(launch_xprep(ut, xu, s));
+        a.m = mu; a.xop = xop_u; a.y = ub;
+        WM_FAIL_HIP(launch_gemv(ut, a, 1, s));
+        XPrepArgs ap = {1, 1, I, gb, ub, 0, actop, 0, act, 0};
+        WM_FAIL_HIP(launch_xprep(dt, ap, s));
+    }
+    GemvArgs dn = {};
+    dn.m = md; dn.rows = H; dn.in = I; dn.xop = actop; dn.y = out; dn.status = status;
+    WM_FAIL_HIP(launch_gemv(dt, dn, 1, s));
+    return WM_OK;
+}
+
+extern "C" int wm_moe_prefill(const wm_layer_desc* d, const uint16_t* x_bf16, int T, float* out, void* ws,
+                              int64_t ws_bytes, int max_tokens, void* stream) {
+    (void)d; (void)x_bf16; (void)T; (void)out; (void)ws; (void)ws_bytes; (void)max_tokens; (void)stream;
+    fprintf(stderr, "winmoe_hip: wm_moe_prefill is not built yet\n");
+    return WM_ERR;
+}
+
+// ------------------------------------------------------------------ gpu_offload.h shims
+
+namespace {
+
+struct Slot {
+    int layer = -1, eid = -1;
+    void* d[3] = {nullptr, nullptr, nullptr};   // gate, up, down
+    int size[3] = {0, 0, 0};
+    int type[3] = {-1, -1, -1};                 // -1 = infer from size
+};
+
+constexpr int kLookupLayers = 80, kLookupExperts = 1024, kMaxSlots = 16384;
+
+struct Legacy {
+    bool init = false;
+    hipStream_t stream = nullptr;
+    std::vector<Slot> slots;
+    std::vector<int> lookup;
+    int limit = 300;
+    int evict = 0;
+    double used_bytes = 0.0;
+    double ceiling_bytes = 0.0;
+    void* ws = nullptr;           // expert workspace
+    int64_t ws_bytes = 0;
+    float* dio = nullptr;         // device in/out staging
+    int64_t dio_floats = 0;
+    float* moe_acc = nullptr;     // batch API accumulator
+    int moe_h = 0;
+    float* router[64] = {nullptr};
+    int router_dims[64][2] = {{0}};
+};
+Legacy G;
+
+int ensure_ws(int H, int I) {
+    int64_t need = wm_expert_workspace_size(H, I);
+    // staging for input, output and gate/up copies; sized once for any shape
+    // up to 16384 so the batch API's uploaded input is never reallocated away
+    int64_t fl = 4 * (int64_t)std::max(std::max(H, I), 16384) + 1024;
+    if (need > G.ws_bytes) {
+        if (G.ws) (void)hipFree(G.ws);
+        G.ws = nullptr;
+        G.ws_bytes = 0;
+        WM_FAIL_HIP(hipMalloc(&G.ws, need));
+        G.ws_bytes = need;
+    }
+    if (fl > G.dio_floats) {
+        if (G.dio) (void)hipFree(G.dio);
+        G.dio = nullptr;
+        G.dio_floats = 0;
+        WM_FAIL_HIP(hipMalloc((void**)&G.dio, fl * sizeof(float)));
+        G.dio_floats = fl;
+    }
+    return WM_OK;
+}
+
+// Quant type of a cached matrix: recorded, or inferred from its byte size
+// (bytes per weight differ for every supported type).
+int slot_type(const Slot& sl, int k, int rows, int in) {
+    if (sl.type[k] >= 0) return sl.type[k];
+    const int cand[6] = {Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K};
+    for (int t : cand)
+        if (in % block_elems(t) == 0 && matrix_bytes(t, rows, in) == (int64_t)sl.size[k]) return t;
+    return -1;
+}
+
+}  // namespace
+
+extern "C" int gpu_init(void) {
+    if (G.init) return 0;
+    if (wm_init()) return -1;
+    WM_FAIL_HIP(hipStreamCreateWithFlags(&G.stream, hipStreamNonBlocking));
+    size_t free_b = 0, total_b = 0;
+    WM_FAIL_HIP(hipMemGetInfo(&free_b, &total_b));
+    G.ceiling_bytes = 0.9 * (double)total_b;
+    G.lookup.assign((size_t)kLookupLayers * kLookupExperts, -1);
+    G.slots.clear();
+    G.init = true;
+    return 0;
+}
+
+extern "C" void gpu_shutdown(void) {
+    if (!G.init) return;
+    (void)hipStreamSynchronize(G.stream);
+    for (Slot& sl : G.slots)
+        for (int k = 0; k < 3; k++)
+            if (sl.d[k]) (void)hipFree(sl.d[k]);
+    for (int l = 0; l < 64; l++)
+        if (G.router[l]) { (void)hipFree(G.router[l]); G.router[l] = nullptr; }
+    if (G.ws) (void)hipFree(G.ws);
+    if (G.dio) (void)hipFree(G.dio);
+    if (G.moe_acc) (void)hipFree(G.moe_acc);
+    (void)hipStreamDestroy(G.stream);
+    G = Legacy();
+}
+
+extern "C" int gpu_is_initialized(void) { return G.init ? 1 : 0; }
+extern "C" float gpu_vram_used_mb(void) { return (float)(G.used_bytes / (1024.0 * 1024.0)); }
+extern "C" int gpu_expert_cache_count(void) { return (int)G.slots.size(); }
+
+extern "C" void gpu_set_expert_limit(int limit) {
+    if (limit < 1) limit = 1;
+    if (limit > kMaxSlots) limit = kMaxSlots;
+    G.limit = limit;
+    fprintf(stderr, "GPU expert cache: limit set to %d (MAX_GPU_EXPERTS=%d)\n", G.limit, kMaxSlots);
+}
+
+extern "C" int gpu_upload_router(int layer, const float* weights, int hidden_dim, int num_experts) {
+    if (!G.init && gpu_init()) return -1;
+    if (layer < 0 || layer >= 64 || !weights || hidden_dim <= 0 || num_experts <= 0) return -1;
+    size_t bytes = (size_t)hidden_dim * num_experts * sizeof(float);
+    if (G.router[layer]) { (void)hipFree(G.router[layer]); G.used_bytes -= (double)G.router_dims[layer][0] * G.router_dims[layer][1] * 4; }
+    G.router[layer] = nullptr;
+    if (hipMalloc((void**)&G.router[layer], bytes) != hipSuccess) return -1;
+    if (hipMemcpy(G.router[layer], weights, bytes, hipMemcpyHostToDevice) != hipSuccess) return -1;
+    G.router_dims[layer][0] = hidden_dim;
+    G.router_dims[layer][1] = num_experts;
+    G.used_bytes += (double)bytes;
+    return 0;
+}
+
+extern "C" int gpu_router(int layer, const float* normed, int hidden_dim, float* logits_out, int num_experts) {
+    if (!G.init || layer < 0 || layer >= 64 || !G.router[layer]) return -1;
+    if (G.router_dims[layer][0] != hidden_dim || G.router_dims[layer][1] != num_experts) return -1;
+    if (2 * (int64_t)hidden_dim * 4 > 65536) return -1;
+    if (ensure_ws(hidden_dim, std::max(num_experts, 64))) return -1;
+    float* dx = G.dio;
+    float* dl = G.dio + ((hidden_dim + 255) & ~255);
+    WM_FAIL_HIP(hipMemcpyAsync(dx, normed, hidden_dim * sizeof(float), hipMemcpyHostToDevice, G.stream));
+    WM_FAIL_HIP(launch_router_logits(dx, G.router[layer], hidden_dim, num_experts, dl, G.stream));
+    WM_FAIL_HIP(hipMemcpyAsync(logits_out, dl, num_experts * sizeof(float), hipMemcpyDeviceToHost, G.stream));
+    WM_FAIL_HIP(hipStreamSynchronize(G.stream));
+    return 0;
+}
+
+static int cache_expert(int layer, int expert_id, const void* data[3], const int size[3], const int type[3]) {
+    if (!G.init && gpu_init()) return -1;
+    if (layer < 0 || expert_id < 0 || layer >= kLookupLayers || expert_id >= kLookupExperts) return -1;
+    for (int k = 0; k < 3; k++)
+        if (!data[k] || size[k] <= 0) return -1;
+    double nb = (double)size[0] + size[1] + size[2];
+    if (G.used_bytes + nb > G.ceiling_bytes) {
+        static int warned = 0;
+        if (!warned) {
+            fprintf(stderr, "GPU VRAM ceiling hit (%.0f MB used + %.0f MB new > %.0f MB)\n", G.used_bytes / 1048576.0,
+                    nb / 1048576.0, G.ceiling_bytes / 1048576.0);
+            warned = 1;
+        }
+        return -1;
+    }
+    int idx;
+    if ((int)G.slots.size() < G.limit) {
+        idx = (int)G.slots.size();
+        G.slots.emplace_back();
+    } else {
+        idx = G.evict;
+        G.evict = (G.evict + 1) % G.limit;
+        Slot& old = G.slots[idx];
+        if (old.layer >= 0) G.lookup[(size_t)old.layer * kLookupExperts + old.eid] = -1;
+        WM_FAIL_HIP(hipStreamSynchronize(G.stream));
+        for (int k = 0; k < 3; k++) {
+            if (old.d[k]) (void)hipFree(old.d[k]);
+            G.used_bytes -= old.size[k];
+            old.d[k] = nullptr;
+        }
+        old = Slot();
+    }
+    Slot& sl = G.slots[idx];
+    for (int k = 0; k < 3; k++) {
+        WM_FAIL_HIP(hipMalloc(&sl.d[k], (size_t)size[k]));
+        WM_FAIL_HIP(hipMemcpyAsync(sl.d[k], data[k], (size_t)size[k], hipMemcpyHostToDevice, G.stream));
+        sl.size[k] = size[k];
+        sl.type[k] = type[k];
+    }
+    WM_FAIL_HIP(hipStreamSynchronize(G.stream));
+    sl.layer = layer;
+    sl.eid = expert_id;
+    G.lookup[(size_t)layer * kLookupExperts + expert_id] = idx;
+    G.used_bytes += nb;
+    return idx;
+}
+
+extern "C" int gpu_cache_expert(int layer, int expert_id, const void* gate_data, int gate_size, const void* up_data,
+                                int up_size, const void* down_data, int down_size) {
+    const void* d[3] = {gate_data, up_data, down_data};
+    int sz[3] = {gate_size, up_size, down_size}, ty[3] = {-1, -1, -1};
+    return cache_expert(layer, expert_id, d, sz, ty);
+}
+
+extern "C" int gpu_cache_expert_typed(int layer, int expert_id, const void* gate_data, int gate_size, int gate_type,
+                                      const void* up_data, int up_size, int up_type, const void* down_data,
+                                      int down_size, int down_type) {
+    if (!supported(gate_type) || !supported(up_type) || !supported(down_type)) return -1;
+    const void* d[3] = {gate_data, up_data, down_data};
+    int sz[3] = {gate_size, up_size, down_size}, ty[3] = {gate_type, up_type, down_type};
+    return cache_expert(layer, expert_id, d, sz, ty);
+}
+
+extern "C" int gpu_find_cached_expert(int layer, int expert_id) {
+    if (!G.init || layer < 0 || expert_id < 0 || layer >= kLookupLayers || expert_id >= kLookupExperts) return -1;
+    return G.lookup[(size_t)layer * kLookupExperts + expert_id];
+}
+
+static const Slot* get_slot(int idx) {
+    if (!G.init || idx < 0 || idx >= (int)G.slots.size() || !G.slots[idx].d[0]) return nullptr;
+    return &G.slots[idx];
+}
+
+// Runs the expert of `sl` on device input G.dio (H floats) into dout (H floats).
+static int expert_on_device(const Slot& sl, int H, int I, float* dout) {
+    int gt = slot_type(sl, 0, I, H), ut = slot_type(sl, 1, I, H), dt = slot_type(sl, 2, H, I);
+    if (gt < 0 || ut < 0 || dt < 0) {
+        fprintf(stderr, "winmoe_hip: cached expert sizes do not match hidden %d / intermediate %d\n", H, I);
+        return -1;
+    }
+    int rc = wm_expert_ffn(sl.d[0], gt, sl.d[1], ut, sl.d[2], dt, G.dio, H, I, dout, G.ws, G.ws_bytes, G.stream);
+    return rc == WM_OK ? 0 : -1;
+}
+
+extern "C" int gpu_expert_ffn_fused(int cache_idx, const float* input, int hidden_dim, int intermediate,
+                                    float* expert_out) {
+    const Slot* sl = get_slot(cache_idx);
+    if (!sl || !input || !expert_out) return -1;
+    if (ensure_ws(hidden_dim, intermediate)) return -1;
+    float* dout = G.dio + ((std::max(hidden_dim, intermediate) + 255) & ~255);
+    WM_FAIL_HIP(hipMemcpyAsync(G.dio, input, hidden_dim * sizeof(float), hipMemcpyHostToDevice, G.stream));
+    if (expert_on_device(*sl, hidden_dim, intermediate, dout)) return -1;
+    WM_FAIL_HIP(hipMemcpyAsync(expert_out, dout, hidden_dim * sizeof(float), hipMemcpyDeviceToHost, G.stream));
+    WM_FAIL_HIP(hipStreamSynchronize(G.stream));
+    return 0;
+}
+
+extern "C" int gpu_expert_ffn(int cache_idx, const float* input, int hidden_dim, int intermediate, float* gate_out,
+                              float* up_out, float* expert_out, int gate_type, int down_type) {
+    (void)expert_out; (void)gate_type; (void)down_type;   // as gpu_offload.cu:675-698: types come from the slot
+    const Slot* sl = get_slot(cache_idx);
+    if (!sl || !input || !gate_out || !up_out) return -1;
+    int H = hidden_dim, I = intermediate;
+    int gt = slot_type(*sl, 0, I, H), ut = slot_type(*sl, 1, I, H);
+    if (gt < 0 || ut < 0) return -1;
+    if (ensure_ws(H, I)) return -1;
+    float* dg = G.dio + ((std::max(H, I) + 255) & ~255);
+    float* du = dg + ((I + 255) & ~255);
+    if ((int64_t)(du - G.dio) + I > G.dio_floats) return -1;
+    WM_FAIL_HIP(hipMemcpyAsync(G.dio, input, H * sizeof(float), hipMemcpyHostToDevice, G.stream));
+    if (wm_quant_matvec(gt, sl->d[0], G.dio, I, H, dg, G.ws, G.ws_bytes, G.stream)) return -1;
+    if (wm_quant_matvec(ut, sl->d[1], G.dio, I, H, du, G.ws, G.ws_bytes, G.stream)) return -1;
+    WM_FAIL_HIP(hipMemcpyAsync(gate_out, dg, I * sizeof(float), hipMemcpyDeviceToHost, G.stream));
+    WM_FAIL_HIP(hipMemcpyAsync(up_out, du, I * sizeof(float), hipMemcpyDeviceToHost, G.stream));
+    WM_FAIL_HIP(hipStreamSynchronize(G.stream));
+    return 0;
+}
+
+extern "C" int gpu_expert_down(int cache_idx, const float* act, int intermediate, float* output, int hidden_dim) {
+    const Slot* sl = get_slot(cache_idx);
+    if (!sl || !act || !output) return -1;
+    int H = hidden_dim, I = intermediate;
+    int dt = slot_type(*sl, 2, H, I);
+    if (dt < 0) return -1;
+    if (ensure_ws(H, I)) return -1;
+    float* dout = G.dio + ((std::max(H, I) + 255) & ~255);
+    WM_FAIL_HIP(hipMemcpyAsync(G.dio, act, I * sizeof(float), hipMemcpyHostToDevice, G.stream));
+    if (wm_quant_matvec(dt, sl->d[2], G.dio, H, I, dout, G.ws, G.ws_bytes, G.stream)) return -1;
+    WM_FAIL_HIP(hipMemcpyAsync(output, dout, H * sizeof(float), hipMemcpyDeviceToHost, G.stream));
+    WM_FAIL_HIP(hipStreamSynchronize(G.stream));
+    return 0;
+}
+
+extern "C" int gpu_expert_batch_start(const float* normed, int hidden_dim) {
+    if (!G.init || !normed || hidden_dim <= 0) return -1;
+    if (ensure_ws(hidden_dim, 64)) return -1;
+    if (G.moe_h < hidden_dim) {
+        if (G.moe_acc) (void)hipFree(G.moe_acc);
+        G.moe_acc = nullptr;
+        WM_FAIL_HIP(hipMalloc((void**)&G.moe_acc, hidden_dim * sizeof(float)));
+        G.moe_h = hidden_dim;
+    }
+    WM_FAIL_HIP(hipMemcpyAsync(G.dio, normed, hidden_dim * sizeof(float), hipMemcpyHostToDevice, G.stream));
+    WM_FAIL_HIP(launch_fill_i32((int32_t*)G.moe_acc, 0, hidden_dim, G.stream));
+    return 0;
+}
+
+extern "C" int gpu_expert_batch_add(int cache_idx, int hidden_dim, int intermediate, float weight) {
+    const Slot* sl = get_slot(cache_idx);
+    if (!sl || !G.moe_acc || hidden_dim > G.moe_h) return -1;
+    if (ensure_ws(hidden_dim, intermediate)) return -1;   // never reallocates dio once sized for hidden_dim
+    float* dout = G.dio + ((std::max(hidden_dim, intermediate) + 255) & ~255);
+    if (expert_on_device(*sl, hidden_dim, intermediate, dout)) return -1;
+    WM_FAIL_HIP(launch_axpy(G.moe_acc, dout, weight, hidden_dim, G.stream));
+    return 0;
+}
+
+extern "C" int gpu_expert_batch_finish(float* moe_out, int hidden_dim) {
+    if (!G.init || !G.moe_acc || !moe_out || hidden_dim > G.moe_h) return -1;
+    WM_FAIL_HIP(hipMemcpyAsync(moe_out, G.moe_acc, hidden_dim * sizeof(float), hipMemcpyDeviceToHost, G.stream));
+    WM_FAIL_HIP(hipStreamSynchronize(G.stream));
+    return 0;
+}

@@ -1,0 +1,107 @@
+// wm_launch.h -- internal interface between the C-ABI layer (wm_capi.cpp) and
+// the kernel launchers (wm_kernels.hip).  Not part of the public ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "wm_format.h"
+
+namespace wm {
+
+// Where the matrix of slot s lives: routed slots s < n_routed use expert
+// ids[s] (or s when ids == NULL) of a stacked tensor; slot n_routed is the
+// shared expert.
+struct MatSet {
+    const uint8_t* base;
+    int64_t stride;
+    const int32_t* ids;
+    int32_t n_routed;
+    int32_t E;
+    const uint8_t* shared;
+};
+
+struct GemvArgs {
+    MatSet m;
+    int32_t slot0;            // first slot handled by the launch (blockIdx.y offset)
+    int32_t rows, in;
+    int32_t tiles_per_wave;
+    const uint32_t* xop;      // activation operands [slot][in/64][XOP_DW]
+    int64_t xop_slot_stride;  // dwords between slots (0 = shared by all slots)
+    float* y;                 // outputs [slot][rows]
+    int64_t y_slot_stride;    // floats
+    int32_t* status;
+};
+
+struct GateUpArgs {
+    MatSet gate, up;
+    int32_t slot0;
+    int32_t rows, in;
+    int32_t tiles_per_wave;
+    const uint32_t* xop;      // operands of the (common) gate/up type, shared by all slots
+    float* act;               // SwiGLU output [slot][act_slot_stride]
+    int64_t act_slot_stride;
+    int32_t* status;
+};
+
+// Activation-operand preparation: for `nslots` slots, segments of type t over
+// an `in`-long vector.  mode 0: v = src[slot*src_stride + col];
+// mode 1: v = silu(g) * u with g = src, u = src2 (also stored to act_out).
+struct XPrepArgs {
+    int32_t mode, nslots, in;
+    const float* src;
+    const float* src2;
+    int64_t src_stride;
+    uint32_t* out;
+    int64_t out_stride;       // dwords between slots
+    float* act_out;
+    int64_t act_stride;
+};
+
+struct CombineArgs {
+    const float* ypart;       // [K(+1)][H]
+    int64_t y_stride;
+    const float* w;           // [K] routing weights
+    const int32_t* ids;       // [K] (checked against E)
+    int32_t K, E, H;
+    int32_t has_shared;
+    const float* sh_gate;     // scalar or NULL
+    float* out;
+};
+
+// Launchers (return hipError_t as int; 0 = success).
+int launch_router_logits(const float* x, const float* W, int H, int E, float* logits, hipStream_t s);
+int launch_topk(const float* logits, int E, int K, int32_t* ids, float* w, uint32_t* hits, int32_t* status,
+                hipStream_t s);
+int launch_xprep(int t, const XPrepArgs& a, hipStream_t s);
+int launch_gemv(int t, const GemvArgs& a, int nslots, hipStream_t s);
+int launch_gateup(int t, const GateUpArgs& a, int nslots, hipStream_t s);
+int launch_combine(const CombineArgs& a, hipStream_t s);
+int launch_shgate(const float* x, const float* g, int H, float* out, hipStream_t s);
+int launch_dequant(int t, const void* blocks, int64_t nblocks, float* out, hipStream_t s);
+int launch_quantize(int t, const float* x, int64_t nblocks, void* out, hipStream_t s);
+int launch_fill_i32(int32_t* p, int32_t v, int64_t n, hipStream_t s);
+int launch_axpy(float* acc, const float* y, float w, int n, hipStream_t s);
+
+// Geometry of the segment mapping for a row of `in` weights.
+struct Geo {
+    int lpr, rpt, active;
+    int64_t row_bytes, tile_bytes;
+};
+WM_HD Geo geometry(int t, int in) {
+    Geo g;
+    g.lpr = in / SEG;
+    g.rpt = g.lpr > 0 ? SEG / g.lpr : 0;
+    g.active = g.rpt * g.lpr;
+    g.row_bytes = matrix_bytes(t, 1, in);
+    g.tile_bytes = g.row_bytes * g.rpt;
+    return g;
+}
+// Shapes the segment kernels accept: in a multiple of the block size and of
+// 64, in/64 a power of two dividing 64 (in = 64 .. 4096).
+WM_HD bool gemv_shape_ok(int t, int in) {
+    if (!supported(t) || in <= 0 || in % block_elems(t) || in % SEG || in > 4096) return false;
+    int lpr = in / SEG;
+    return (lpr & (lpr - 1)) == 0;
+}
+
+}  // namespace wm

@@ -1,0 +1,280 @@
+"""PyTorch-ROCm host API of the MoE expert-layer path.
+
+Mirrors the reference's entry points on device tensors:
+
+* ``router_topk``      engine/runtime/transformer.h:107-152 (+ verify_router.py:71-84)
+* ``quant_matvec``     engine/runtime/transformer.h:157-194
+* ``dequantize`` / ``dequant_q8_0_row`` / ``dequant_q4k_block``
+                       q8_dequant.h:116-126, validate_l0.py:32-45, verify_expert.py:55-88 (ggml order)
+* ``expert_ffn``       expert_ffn.h:48-74, gpu_expert_ffn_fused (gpu_offload.cu:718-751)
+* ``MoELayer.decode``  the MoE block of winmoe_inference.c:1684-2027 for one token
+* ``MoELayer.prefill`` the same block for a batch of prompt tokens
+
+Torch is used only for device memory and streams; every computation runs in
+libwinmoe_hip.so.  Tensors must live on the current HIP device.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib
+from ._lib import BLOCK_BYTES, BLOCK_ELEMS, LayerDesc, check, load
+
+
+def _stream(stream=None) -> C.c_void_p:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+def _p(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _need(t: torch.Tensor, dtype, name: str) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise ValueError(f"{name} must be a CUDA (HIP) tensor")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t
+
+
+def matrix_bytes(qtype: int, rows: int, cols: int) -> int:
+    return rows * (cols // BLOCK_ELEMS[qtype]) * BLOCK_BYTES[qtype]
+
+
+def _ws(nbytes: int, device) -> torch.Tensor:
+    # 256-byte aligned (the caching allocator hands out >= 512-byte aligned blocks)
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+# ------------------------------------------------------------------ block ops
+
+def dequantize(blocks: torch.Tensor, qtype: int, stream=None) -> torch.Tensor:
+    """fp32 weights of raw blocks (uint8, whole blocks).  Bit-exact with the oracle."""
+    _need(blocks, torch.uint8, "blocks")
+    bs = BLOCK_BYTES[qtype]
+    if blocks.numel() % bs:
+        raise ValueError("blocks must hold whole blocks")
+    nb = blocks.numel() // bs
+    out = torch.empty(nb * BLOCK_ELEMS[qtype], dtype=torch.float32, device=blocks.device)
+    check(load().wm_dequant(qtype, _p(blocks), nb, _p(out), _stream(stream)), "wm_dequant")
+    return out
+
+
+def dequant_q8_0_row(data: torch.Tensor, offset: int, n_elements: int) -> torch.Tensor:
+    """validate_l0.py:32-45 on device: one Q8_0 row of n_elements starting at byte offset."""
+    nb = n_elements // 32
+    return dequantize(data[offset:offset + nb * 34], _lib.Q8_0)
+
+
+def dequant_q4k_block(data: torch.Tensor, offset: int) -> torch.Tensor:
+    """One Q4_K block in the ggml order (q4k_dequant.h:129-155), not verify_expert.py's order."""
+    return dequantize(data[offset:offset + 144], _lib.Q4_K)
+
+
+def quantize(x: torch.Tensor, qtype: int, stream=None) -> torch.Tensor:
+    """Quantise fp32 values (length a multiple of the block size) into raw blocks."""
+    _need(x, torch.float32, "x")
+    n = x.numel()
+    if n % BLOCK_ELEMS[qtype]:
+        raise ValueError("length must be a multiple of the block size")
+    out = torch.empty(n // BLOCK_ELEMS[qtype] * BLOCK_BYTES[qtype], dtype=torch.uint8, device=x.device)
+    check(load().wm_quantize(qtype, _p(x), n, _p(out), _stream(stream)), "wm_quantize")
+    return out
+
+
+def quantize_into(x: torch.Tensor, qtype: int, out: torch.Tensor, stream=None) -> None:
+    _need(x, torch.float32, "x")
+    n = x.numel()
+    if out.numel() != n // BLOCK_ELEMS[qtype] * BLOCK_BYTES[qtype]:
+        raise ValueError("output size mismatch")
+    check(load().wm_quantize(qtype, _p(x), n, _p(out), _stream(stream)), "wm_quantize")
+
+
+def quant_matvec(W: torch.Tensor, x: torch.Tensor, out_dim: int, in_dim: int, qtype: int,
+                 stream=None) -> torch.Tensor:
+    """y = W x for one raw quantised matrix [out_dim][in_dim/QK] (transformer.h:157-194)."""
+    _need(W, torch.uint8, "W")
+    _need(x, torch.float32, "x")
+    if W.numel() < matrix_bytes(qtype, out_dim, in_dim) or x.numel() != in_dim:
+        raise ValueError("shape mismatch")
+    y = torch.empty(out_dim, dtype=torch.float32, device=x.device)
+    ws = _ws((in_dim // 64) * 160, x.device)
+    check(load().wm_quant_matvec(qtype, _p(W), _p(x), out_dim, in_dim, _p(y), _p(ws), ws.numel(),
+                                 _stream(stream)), "wm_quant_matvec")
+    return y
+
+
+def q8_0_matvec(W: torch.Tensor, x: torch.Tensor, out_dim: int, in_dim: int) -> torch.Tensor:
+    """verify_3layers.py:85-101 on device."""
+    return quant_matvec(W, x, out_dim, in_dim, _lib.Q8_0)
+
+
+def router_logits(hidden: torch.Tensor, gate_weights: torch.Tensor, stream=None) -> torch.Tensor:
+    """fp32 router logits [E] in the reference's accumulation order (gpu_router on device)."""
+    _need(hidden, torch.float32, "hidden")
+    _need(gate_weights, torch.float32, "gate_weights")
+    E, H = gate_weights.shape
+    out = torch.empty(E, dtype=torch.float32, device=hidden.device)
+    check(load().wm_router_logits(_p(hidden), _p(gate_weights), H, E, _p(out), _stream(stream)), "wm_router_logits")
+    return out
+
+
+def router_topk(hidden: torch.Tensor, gate_weights: torch.Tensor, K: int, stream=None):
+    """Reference-order fp32 router logits, top-K ids (desc logit, ties to the lower
+    index) and softmax weights over the K picks.  gate_weights is [E][H] fp32."""
+    _need(hidden, torch.float32, "hidden")
+    _need(gate_weights, torch.float32, "gate_weights")
+    E, H = gate_weights.shape
+    if hidden.numel() != H:
+        raise ValueError("hidden size mismatch")
+    L = load()
+    ids = torch.empty(K, dtype=torch.int32, device=hidden.device)
+    w = torch.empty(K, dtype=torch.float32, device=hidden.device)
+    ws = _ws(L.wm_router_workspace_size(E), hidden.device)
+    check(L.wm_router_topk(_p(hidden), _p(gate_weights), H, E, K, _p(ids), _p(w), _p(ws), ws.numel(),
+                           _stream(stream)), "wm_router_topk")
+    return ids, w
+
+
+def expert_ffn(gate: torch.Tensor, up: torch.Tensor, down: torch.Tensor, x: torch.Tensor, H: int, I: int,
+               types: Sequence[int], stream=None) -> torch.Tensor:
+    """down(SwiGLU(gate x, up x)) for one expert's raw blocks (any supported types)."""
+    for t, n in ((gate, "gate"), (up, "up"), (down, "down")):
+        _need(t, torch.uint8, n)
+    _need(x, torch.float32, "x")
+    L = load()
+    out = torch.empty(H, dtype=torch.float32, device=x.device)
+    ws = _ws(L.wm_expert_workspace_size(H, I), x.device)
+    gt, ut, dt = types
+    check(L.wm_expert_ffn(_p(gate), gt, _p(up), ut, _p(down), dt, _p(x), H, I, _p(out), _p(ws), ws.numel(),
+                          _stream(stream)), "wm_expert_ffn")
+    return out
+
+
+# ------------------------------------------------------------------ layer
+
+@dataclass
+class SharedExpert:
+    gate: torch.Tensor
+    up: torch.Tensor
+    down: torch.Tensor
+    types: tuple
+    gate_inp: Optional[torch.Tensor] = None   # fp32 [H] sigmoid gate, or None
+    inter: int = 0                            # 0 = routed intermediate
+
+
+class MoELayer:
+    """One MoE layer over raw GGUF expert tensors resident in HBM.
+
+    gate_exps / up_exps: uint8, stacked [E][I rows][H/QK blocks]; down_exps:
+    [E][H rows][I/QK blocks] -- the per-expert slicing of the reference
+    (winmoe_inference.c:467-489).  ``strides`` overrides the per-expert byte
+    stride (e.g. a GGUF tensor's data_size / E).  The workspace (routing trace
+    of ``max_tokens`` entries, hit counters, scratch) is allocated once.
+    """
+
+    def __init__(self, H: int, I: int, E: int, K: int, router: Optional[torch.Tensor], gate_exps: torch.Tensor,
+                 up_exps: torch.Tensor, down_exps: torch.Tensor, types: Sequence[int],
+                 shared: Optional[SharedExpert] = None, max_tokens: int = 256, strides=(0, 0, 0)):
+        self.H, self.I, self.E, self.K = H, I, E, K
+        self.types = tuple(types)
+        self.max_tokens = max_tokens
+        self.router = None if router is None else _need(router, torch.float32, "router")
+        self.gate_exps = _need(gate_exps, torch.uint8, "gate_exps")
+        self.up_exps = _need(up_exps, torch.uint8, "up_exps")
+        self.down_exps = _need(down_exps, torch.uint8, "down_exps")
+        self.shared = shared
+        d = LayerDesc()
+        d.hidden, d.inter, d.n_experts, d.top_k = H, I, E, K
+        d.gate_type, d.up_type, d.down_type = self.types
+        d.router = _p(self.router)
+        d.gate_exps, d.up_exps, d.down_exps = _p(gate_exps), _p(up_exps), _p(down_exps)
+        d.gate_stride, d.up_stride, d.down_stride = strides
+        if shared is not None:
+            for t, n in ((shared.gate, "shared.gate"), (shared.up, "shared.up"), (shared.down, "shared.down")):
+                _need(t, torch.uint8, n)
+            d.sh_gate, d.sh_up, d.sh_down = _p(shared.gate), _p(shared.up), _p(shared.down)
+            d.sh_gate_type, d.sh_up_type, d.sh_down_type = shared.types
+            d.inter_shared = shared.inter
+            if shared.gate_inp is not None:
+                d.sh_gate_inp = _p(_need(shared.gate_inp, torch.float32, "shared.gate_inp"))
+        self.desc = d
+        L = load()
+        nbytes = L.wm_workspace_size(C.byref(d), max_tokens)
+        if nbytes < 0:
+            raise ValueError("invalid layer descriptor")
+        self.ws = _ws(nbytes, gate_exps.device)
+        self.step = 0
+        self.reset()
+        io, wo, ho = C.c_int64(), C.c_int64(), C.c_int64()
+        check(L.wm_workspace_trace(C.byref(d), max_tokens, C.byref(io), C.byref(wo), C.byref(ho)), "trace")
+        self._trace_off = (io.value, wo.value, ho.value)
+
+    def reset(self, stream=None) -> None:
+        """Clear the routing trace, hit counters and status bits."""
+        check(load().wm_workspace_reset(C.byref(self.desc), self.max_tokens, _p(self.ws), self.ws.numel(),
+                                        _stream(stream)), "wm_workspace_reset")
+        self.step = 0
+
+    def decode(self, x: torch.Tensor, out: Optional[torch.Tensor] = None, step: Optional[int] = None,
+               stream=None) -> torch.Tensor:
+        """moe_out (before the residual add) of one token; routing recorded in the trace."""
+        _need(x, torch.float32, "x")
+        if out is None:
+            out = torch.empty(self.H, dtype=torch.float32, device=x.device)
+        st = self.step if step is None else step
+        check(load().wm_moe_decode(C.byref(self.desc), _p(x), _p(out), _p(self.ws), self.ws.numel(),
+                                   self.max_tokens, st, _stream(stream)), "wm_moe_decode")
+        self.step = st + 1
+        return out
+
+    def decode_forced(self, x: torch.Tensor, ids: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None,
+                      step: Optional[int] = None, stream=None) -> torch.Tensor:
+        """One token with caller-supplied routing (ids int32[K], w fp32[K] on device)."""
+        _need(x, torch.float32, "x")
+        _need(ids, torch.int32, "ids")
+        _need(w, torch.float32, "w")
+        if out is None:
+            out = torch.empty(self.H, dtype=torch.float32, device=x.device)
+        st = self.step if step is None else step
+        check(load().wm_moe_decode_forced(C.byref(self.desc), _p(x), _p(ids), _p(w), _p(out), _p(self.ws),
+                                          self.ws.numel(), self.max_tokens, st, _stream(stream)),
+              "wm_moe_decode_forced")
+        self.step = st + 1
+        return out
+
+    def prefill(self, x_bf16: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+        """moe_out for T prompt tokens (x bf16 [T][H]) -> fp32 [T][H]."""
+        _need(x_bf16, torch.bfloat16, "x")
+        T = x_bf16.shape[0]
+        if out is None:
+            out = torch.empty(T, self.H, dtype=torch.float32, device=x_bf16.device)
+        check(load().wm_moe_prefill(C.byref(self.desc), _p(x_bf16), T, _p(out), _p(self.ws), self.ws.numel(),
+                                    self.max_tokens, _stream(stream)), "wm_moe_prefill")
+        return out
+
+    # -- trace ---------------------------------------------------------------
+    def trace(self):
+        """(ids int32 [max_tokens][K], weights fp32 [max_tokens][K]) views of the device trace."""
+        io, wo, _ = self._trace_off
+        n = self.max_tokens * self.K * 4
+        ids = self.ws[io:io + n].view(torch.int32).view(self.max_tokens, self.K)
+        w = self.ws[wo:wo + n].view(torch.float32).view(self.max_tokens, self.K)
+        return ids, w
+
+    def hits(self) -> torch.Tensor:
+        """Per-expert selection counters (uint32 stored, returned as int32 view)."""
+        _, _, ho = self._trace_off
+        return self.ws[ho:ho + self.E * 4].view(torch.int32)
+
+    def status(self) -> int:
+        v = C.c_int32()
+        check(load().wm_workspace_status(_p(self.ws), self.ws.numel(), C.byref(v)), "wm_workspace_status")
+        return v.value
