@@ -121,6 +121,8 @@ def main():
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--multi-kernel", action="store_true",
+                    help="run each step as per-phase kernel launches instead of the single fused launch")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -139,7 +141,8 @@ def main():
     cfg = synth.CONFIGS[args.config]
     log(f"building {cfg.name} on {torch.cuda.get_device_name(0)}")
     t_build = time.perf_counter()
-    layers = [synth.build_layer(cfg, layer_index=i, max_tokens=cfg.tokens) for i in range(cfg.n_layers)]
+    layers = [synth.build_layer(cfg, layer_index=i, max_tokens=cfg.tokens, multi_kernel=args.multi_kernel)
+              for i in range(cfg.n_layers)]
     X = synth.make_hidden(cfg)
     routes = None
     if cfg.routing != "router":

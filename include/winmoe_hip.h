@@ -47,6 +47,16 @@ enum {
 #define WM_STATUS_DEGENERATE_ROUTING 1   /* a top-K pass found no logit > -1e30 */
 #define WM_STATUS_BAD_EXPERT_ID      2   /* forced routing named an id outside [0, E) */
 #define WM_STATUS_NONFINITE_WEIGHT   4   /* a routing weight was NaN/Inf */
+#define WM_STATUS_SPIN_TIMEOUT       8   /* a fused-step dependency wait hit its bound (results invalid;
+                                            call wm_workspace_reset before the next call) */
+
+/* wm_layer_desc.flags: run the decode step as a sequence of per-phase kernel
+ * launches instead of the single fused launch (same results, bit for bit). */
+#define WM_FLAG_MULTI_KERNEL 1
+/* wm_layer_desc.flags: the fused step also records, per work item, its start,
+ * dependency-satisfied and end times (device constant-rate clock) and its kind
+ * into the workspace (diagnostics; see wm_workspace_timeline). */
+#define WM_FLAG_TIMELINE 2
 
 /* One MoE layer.  Expert tensors are the raw GGUF blocks, stacked by expert:
  * gate/up expert e = [inter rows][hidden/QK blocks] at gate_exps + e*gate_stride,
@@ -62,7 +72,7 @@ typedef struct wm_layer_desc {
     int32_t top_k;           /* K, 1..16 (no silent clamp, unlike winmoe_inference.c:812) */
     int32_t gate_type, up_type, down_type;
     int32_t sh_gate_type, sh_up_type, sh_down_type;
-    int32_t reserved;
+    int32_t flags;           /* WM_FLAG_* */
     const float* router;     /* [E][H] fp32, row-major; NULL only for forced routing */
     const void* gate_exps;
     const void* up_exps;
@@ -119,6 +129,17 @@ int64_t wm_workspace_size(const wm_layer_desc* d, int max_tokens);
 
 /* Clears the trace, counters and status of a workspace (stream-ordered). */
 int wm_workspace_reset(const wm_layer_desc* d, int max_tokens, void* ws, int64_t ws_bytes, void* stream);
+
+/* Byte offset of the fused-step timeline in the workspace (valid when the
+ * descriptor has WM_FLAG_TIMELINE): uint64 [capacity][8] = start, dependencies
+ * met, main work done, end (device clock ticks, wm_device_clock_khz per ms),
+ * kind | HW_ID << 8 | XCC_ID << 40, then for router items the time their
+ * counter increment returned and, for the one that ran top-K, the time top-K
+ * finished (0 otherwise), and a zero word; kind 0 = shared gate / forced
+ * routing, 1 = router, 2 = shared gate/up, 3 = routed gate/up, 4 = down (+8
+ * when it also combined). */
+int wm_workspace_timeline(const wm_layer_desc* d, int max_tokens, int64_t* offset, int64_t* capacity);
+int64_t wm_device_clock_khz(void);
 
 /* Host-synchronous read of the workspace status bits (WM_STATUS_*). */
 int wm_workspace_status(void* ws, int64_t ws_bytes, int32_t* status_out);

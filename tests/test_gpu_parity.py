@@ -306,3 +306,33 @@ def test_legacy_expert_cache_and_ffn(wm, orc):
     assert L.gpu_expert_cache_count() == 1 and L.gpu_vram_used_mb() > 0
     L.gpu_shutdown()
     assert L.gpu_is_initialized() == 0
+
+
+# ------------------------------------------------------------------ fused step vs per-phase launches
+
+@pytest.mark.parametrize("name,E,tokens", [("c1", 64, 4), ("c2", 40, 6), ("c3", 24, 4), ("c4", 24, 4)])
+def test_fused_step_matches_multi_kernel(wm, name, E, tokens):
+    """One fused launch per token == the per-phase kernel sequence, bit for bit,
+    over several consecutive tokens (the counters reset between launches)."""
+    from winmoe_amd import synth
+    cfg = synth.CONFIGS[name]
+    sl = synth.build_layer(cfg, E=E, max_tokens=8)
+    multi = synth.twin_layer(sl, multi_kernel=True)
+    X = synth.make_hidden(cfg, tokens=tokens)
+    routes = synth.forced_routes(cfg, E=E, tokens=tokens) if cfg.routing != "router" else None
+    for t in range(tokens):
+        case(f"fused vs multi {name} E={E} token={t}")
+        if routes is None:
+            a = host(sl.layer.decode(X[t]))
+            b = host(multi.decode(X[t]))
+        else:
+            ids, w = dev(routes[0][t]), dev(routes[1][t])
+            a = host(sl.layer.decode_forced(X[t], ids, w))
+            b = host(multi.decode_forced(X[t], ids, w))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), t
+    ta, wa = sl.layer.trace()
+    tb, wb = multi.trace()
+    assert np.array_equal(host(ta[:tokens]), host(tb[:tokens]))
+    assert np.array_equal(host(wa[:tokens]).view(np.uint32), host(wb[:tokens]).view(np.uint32))
+    assert np.array_equal(host(sl.layer.hits()), host(multi.hits()))
+    assert sl.layer.status() == 0 and multi.status() == 0

@@ -23,6 +23,9 @@ QUANT_TYPES = (Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K)
 STATUS_DEGENERATE_ROUTING = 1
 STATUS_BAD_EXPERT_ID = 2
 STATUS_NONFINITE_WEIGHT = 4
+STATUS_SPIN_TIMEOUT = 8
+FLAG_MULTI_KERNEL = 1
+FLAG_TIMELINE = 2
 
 _vp, _i64 = C.c_void_p, C.c_int64
 
@@ -33,7 +36,7 @@ class LayerDesc(C.Structure):
         ("hidden", C.c_int32), ("inter", C.c_int32), ("inter_shared", C.c_int32), ("n_experts", C.c_int32),
         ("top_k", C.c_int32), ("gate_type", C.c_int32), ("up_type", C.c_int32), ("down_type", C.c_int32),
         ("sh_gate_type", C.c_int32), ("sh_up_type", C.c_int32), ("sh_down_type", C.c_int32),
-        ("reserved", C.c_int32),
+        ("flags", C.c_int32),
         ("router", _vp), ("gate_exps", _vp), ("up_exps", _vp), ("down_exps", _vp),
         ("gate_stride", _i64), ("up_stride", _i64), ("down_stride", _i64),
         ("sh_gate", _vp), ("sh_up", _vp), ("sh_down", _vp), ("sh_gate_inp", _vp),
@@ -56,6 +59,8 @@ SIGNATURES = {
     "wm_workspace_size": (_i64, [C.POINTER(LayerDesc), C.c_int]),
     "wm_workspace_reset": (C.c_int, [C.POINTER(LayerDesc), C.c_int, _vp, _i64, _vp]),
     "wm_workspace_status": (C.c_int, [_vp, _i64, C.POINTER(C.c_int32)]),
+    "wm_workspace_timeline": (C.c_int, [C.POINTER(LayerDesc), C.c_int, C.POINTER(_i64), C.POINTER(_i64)]),
+    "wm_device_clock_khz": (_i64, []),
     "wm_workspace_trace": (C.c_int, [C.POINTER(LayerDesc), C.c_int, C.POINTER(_i64), C.POINTER(_i64),
                                      C.POINTER(_i64)]),
     "wm_moe_decode": (C.c_int, [C.POINTER(LayerDesc), _vp, _vp, _vp, _i64, C.c_int, C.c_int, _vp]),

@@ -11,8 +11,10 @@
 #include <vector>
 
 #include "../../include/winmoe_hip.h"
+#include "wm_decode.h"
 #include "wm_launch.h"
 #include "wm_quant.h"
+#include "wm_wave.h"
 
 using namespace wm;
 
@@ -41,9 +43,9 @@ static bool g_dev_ready = false;
 
 // ------------------------------------------------------------------ phase profiler
 namespace {
-enum Phase { PH_ROUTER = 0, PH_TOPK, PH_XPREP, PH_GATEUP, PH_ACTPREP, PH_DOWN, PH_COMBINE, PH_STEP };
-const char* kPhaseNames[WM_PROF_NPHASE] = {"router_logits", "topk", "x_operand", "gate_up_swiglu",
-                                           "act_operand", "down", "combine", "step"};
+enum Phase { PH_ROUTER = 0, PH_TOPK, PH_SHGATE, PH_GATEUP, PH_SWIGLU, PH_DOWN, PH_COMBINE, PH_STEP };
+const char* kPhaseNames[WM_PROF_NPHASE] = {"router_logits", "topk", "shared_gate", "gate_up_swiglu",
+                                           "swiglu", "down", "combine", "step"};
 struct Prof {
     bool on = false;
     std::vector<hipEvent_t> pool;                 // free events
@@ -176,6 +178,15 @@ static int check_matrix(int t, const void* W, int in) {
 
 static int64_t xop_bytes(int in) { return (int64_t)(in / SEG) * XOP_DW * 4; }
 
+// Input vectors are read as b128 vectors: one that is not 16-byte aligned is
+// first copied to an aligned workspace buffer of at least n floats.
+static int aligned_input(const float*& x, int64_t n, float* scratch, hipStream_t s) {
+    if (al(x, 16)) return WM_OK;
+    WM_FAIL_HIP(hipMemcpyAsync(scratch, x, (size_t)n * 4, hipMemcpyDeviceToDevice, s));
+    x = scratch;
+    return WM_OK;
+}
+
 extern "C" int wm_quant_matvec(int t, const void* W, const float* x, int rows, int in, float* y, void* ws,
                                int64_t ws_bytes, void* stream) {
     WM_CHECK_ARG(supported(t) && W && x && y && rows >= 0);
@@ -184,15 +195,13 @@ extern "C" int wm_quant_matvec(int t, const void* W, const float* x, int rows, i
     if (rows == 0) return WM_OK;
     if (wm_init()) return WM_ERR;
     hipStream_t s = S(stream);
-    uint32_t* xop = (uint32_t*)ws;
-    XPrepArgs xp = {0, 1, in, x, nullptr, 0, xop, 0, nullptr, 0};
-    WM_FAIL_HIP(launch_xprep(t, xp, s));
+    if (int rc = aligned_input(x, in, (float*)ws, s)) return rc;
     GemvArgs g = {};
     g.m = MatSet{(const uint8_t*)W, 0, nullptr, 1, 1, nullptr};
     g.slot0 = 0;
     g.rows = rows;
     g.in = in;
-    g.xop = xop;
+    g.x = x;
     g.y = y;
     WM_FAIL_HIP(launch_gemv(t, g, 1, s));
     return WM_OK;
@@ -202,7 +211,7 @@ extern "C" int64_t wm_router_workspace_size(int E) { return E > 0 ? up256((int64
 
 extern "C" int wm_router_logits(const float* x, const float* W, int H, int E, float* logits, void* stream) {
     WM_CHECK_ARG(x && W && logits && H > 0 && E > 0);
-    WM_CHECK_ARG(2 * (int64_t)H * 4 <= 65536);
+    WM_CHECK_ARG(router_rows_per_wg(H, false) > 0);
     if (wm_init()) return WM_ERR;
     WM_FAIL_HIP(launch_router_logits(x, W, H, E, logits, S(stream)));
     return WM_OK;
@@ -211,7 +220,7 @@ extern "C" int wm_router_logits(const float* x, const float* W, int H, int E, fl
 extern "C" int wm_router_topk(const float* x, const float* W, int H, int E, int K, int32_t* ids, float* w, void* ws,
                               int64_t ws_bytes, void* stream) {
     WM_CHECK_ARG(x && W && ids && w && H > 0 && E > 0 && E <= 1024 && K >= 1 && K <= 16 && K <= E);
-    WM_CHECK_ARG(2 * (int64_t)H * 4 <= 65536);
+    WM_CHECK_ARG(router_rows_per_wg(H, false) > 0);
     WM_CHECK_ARG(ws && al(ws, 256) && ws_bytes >= wm_router_workspace_size(E));
     if (wm_init()) return WM_ERR;
     hipStream_t s = S(stream);
@@ -225,7 +234,7 @@ extern "C" int wm_router_topk(const float* x, const float* W, int H, int E, int 
 // ------------------------------------------------------------------ layer descriptor + workspace
 
 struct WsLayout {
-    int64_t status, logits, tr_ids, tr_w, hits, shgate, xop, gbuf, ubuf, act, actop, ypart, total;
+    int64_t status, ctr, logits, tr_ids, tr_w, hits, shgate, xin, gbuf, ubuf, act, ypart, timeline, total;
     int K1, Imax, Is;
 };
 
@@ -244,7 +253,7 @@ static int validate_desc(const wm_layer_desc* d, bool need_router) {
     WM_CHECK_ARG(d->gate_stride % 16 == 0 && d->up_stride % 16 == 0 && d->down_stride % 16 == 0);
     if (need_router) {
         WM_CHECK_ARG(d->router != nullptr);
-        WM_CHECK_ARG(2 * (int64_t)d->hidden * 4 <= 65536);
+        WM_CHECK_ARG(router_rows_per_wg(d->hidden, false) > 0);
     }
     if (has_shared(d)) {
         int Is = Ishared(d);
@@ -265,17 +274,19 @@ static WsLayout layout(const wm_layer_desc* d, int max_tokens) {
     L.Imax = std::max(d->inter, L.Is);
     int64_t o = 0;
     L.status = o; o += 256;
+    L.ctr = o; o += (int64_t)C_TOTAL * CTR_STRIDE * 4;
     L.logits = o; o += up256((int64_t)E * 4);
     L.tr_ids = o; o += up256((int64_t)max_tokens * K * 4);
     L.tr_w = o; o += up256((int64_t)max_tokens * K * 4);
     L.hits = o; o += up256((int64_t)E * 4);
     L.shgate = o; o += 256;
-    L.xop = o; o += 4 * up256(xop_bytes(H));
+    L.xin = o; o += up256((int64_t)H * 4);
     L.gbuf = o; o += up256((int64_t)L.K1 * L.Imax * 4);
     L.ubuf = o; o += up256((int64_t)L.K1 * L.Imax * 4);
     L.act = o; o += up256((int64_t)L.K1 * L.Imax * 4);
-    L.actop = o; o += up256((int64_t)L.K1 * xop_bytes(L.Imax));
     L.ypart = o; o += up256((int64_t)L.K1 * H * 4);
+    L.timeline = o;
+    if (d->flags & WM_FLAG_TIMELINE) o += up256((int64_t)TIMELINE_CAP * 8 * 8);
     L.total = o;
     return L;
 }
@@ -304,6 +315,22 @@ extern "C" int wm_workspace_reset(const wm_layer_desc* d, int max_tokens, void* 
     return WM_OK;
 }
 
+extern "C" int wm_workspace_timeline(const wm_layer_desc* d, int max_tokens, int64_t* offset, int64_t* capacity) {
+    WM_CHECK_ARG(d && max_tokens > 0 && d->top_k > 0 && d->n_experts > 0 && (d->flags & WM_FLAG_TIMELINE));
+    WsLayout L = layout(d, max_tokens);
+    if (offset) *offset = L.timeline;
+    if (capacity) *capacity = TIMELINE_CAP;
+    return WM_OK;
+}
+
+extern "C" int64_t wm_device_clock_khz(void) {
+    if (wm_init()) return WM_ERR;
+    int dev = 0, khz = 0;
+    WM_FAIL_HIP(hipGetDevice(&dev));
+    WM_FAIL_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
+    return khz;
+}
+
 extern "C" int wm_workspace_status(void* ws, int64_t ws_bytes, int32_t* status_out) {
     WM_CHECK_ARG(ws && status_out && ws_bytes >= 4);
     if (wm_init()) return WM_ERR;
@@ -313,7 +340,7 @@ extern "C" int wm_workspace_status(void* ws, int64_t ws_bytes, int32_t* status_o
 }
 
 // The expert part of one decode token, given routing already in the trace
-// entry (ids_d / w_d): gate/up + SwiGLU, activation operands, down, combine.
+// entry (ids_d / w_d): gate/up + SwiGLU, down, combine.
 static int run_experts(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, const float* x, const int32_t* ids_d,
                        const float* w_d, float* out, hipStream_t s) {
     const int H = d->hidden, I = d->inter, K = d->top_k, E = d->n_experts, Is = L.Is;
@@ -322,27 +349,12 @@ static int run_experts(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
     float* act = (float*)(ws + L.act);
     float* gbuf = (float*)(ws + L.gbuf);
     float* ubuf = (float*)(ws + L.ubuf);
-    uint32_t* actop = (uint32_t*)(ws + L.actop);
     float* ypart = (float*)(ws + L.ypart);
-    const int64_t act_stride = L.Imax, actop_stride = xop_bytes(L.Imax) / 4;
-
-    // activation operands of x, one per distinct input type
-    int types[4] = {d->gate_type, d->up_type, sh ? d->sh_gate_type : -1, sh ? d->sh_up_type : -1};
-    int tslot[16];
-    for (int i = 0; i < 16; i++) tslot[i] = -1;
-    int nts = 0;
-    uint32_t* xop = (uint32_t*)(ws + L.xop);
-    const int64_t xop_slot = up256(xop_bytes(H)) / 4;
-    {
-        PhaseTimer pt(PH_XPREP, s);
-        for (int i = 0; i < 4; i++) {
-            int t = types[i];
-            if (t < 0 || tslot[t] >= 0) continue;
-            tslot[t] = nts++;
-            XPrepArgs xp = {0, 1, H, x, nullptr, 0, xop + tslot[t] * xop_slot, 0, nullptr, 0};
-            WM_FAIL_HIP(launch_xprep(t, xp, s));
-        }
-        if (sh && d->sh_gate_inp) WM_FAIL_HIP(launch_shgate(x, d->sh_gate_inp, H, (float*)(ws + L.shgate), s));
+    const int64_t act_stride = L.Imax;
+    if (int rc = aligned_input(x, H, (float*)(ws + L.xin), s)) return rc;
+    if (sh && d->sh_gate_inp) {
+        PhaseTimer pt(PH_SHGATE, s);
+        WM_FAIL_HIP(launch_shgate(x, d->sh_gate_inp, H, (float*)(ws + L.shgate), s));
     }
 
     MatSet mg = {(const uint8_t*)d->gate_exps, d->gate_stride ? d->gate_stride : matrix_bytes(d->gate_type, I, H),
@@ -352,40 +364,31 @@ static int run_experts(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
     MatSet md = {(const uint8_t*)d->down_exps, d->down_stride ? d->down_stride : matrix_bytes(d->down_type, H, I),
                  ids_d, K, E, (const uint8_t*)d->sh_down};
 
-    // gate/up (+ SwiGLU) for the routed slots [0, K) and the shared slot K
+    // gate/up (+ SwiGLU) for slots [slot0, slot0 + nslots): one fused launch
+    // when gate and up share a type, else two GEMVs and an elementwise SwiGLU
     auto gate_up = [&](int slot0, int nslots, int gt, int ut, int rows) -> int {
         if (gt == ut) {
             GateUpArgs a = {};
             a.gate = mg; a.up = mu;
             a.slot0 = slot0; a.rows = rows; a.in = H;
-            a.xop = xop + tslot[gt] * xop_slot;
+            a.x = x;
             a.act = act; a.act_slot_stride = act_stride; a.status = status;
             return launch_gateup(gt, a, nslots, s);
         }
         GemvArgs a = {};
         a.slot0 = slot0; a.rows = rows; a.in = H; a.status = status;
-        a.m = mg; a.xop = xop + tslot[gt] * xop_slot; a.y = gbuf; a.y_slot_stride = act_stride;
+        a.m = mg; a.x = x; a.y = gbuf; a.y_slot_stride = act_stride;
         if (int e = launch_gemv(gt, a, nslots, s)) return e;
-        a.m = mu; a.xop = xop + tslot[ut] * xop_slot; a.y = ubuf;
-        return launch_gemv(ut, a, nslots, s);
-    };
-    // activation operands of the SwiGLU output in the down type's layout
-    auto act_prep = [&](int slot0, int nslots, int gt, int ut, int dt, int rows) -> int {
-        XPrepArgs xp = {};
-        xp.nslots = nslots; xp.in = rows;
-        xp.out = actop + slot0 * actop_stride; xp.out_stride = actop_stride;
-        xp.src_stride = act_stride;
-        if (gt == ut) { xp.mode = 0; xp.src = act + slot0 * act_stride; }
-        else {
-            xp.mode = 1; xp.src = gbuf + slot0 * act_stride; xp.src2 = ubuf + slot0 * act_stride;
-            xp.act_out = act + slot0 * act_stride; xp.act_stride = act_stride;
-        }
-        return launch_xprep(dt, xp, s);
+        a.m = mu; a.y = ubuf;
+        if (int e = launch_gemv(ut, a, nslots, s)) return e;
+        PhaseTimer pt(PH_SWIGLU, s);
+        return launch_swiglu(gbuf + slot0 * act_stride, ubuf + slot0 * act_stride, act + slot0 * act_stride, rows,
+                             nslots, act_stride, s);
     };
     auto down = [&](int slot0, int nslots, int dt, int in) -> int {
         GemvArgs a = {};
         a.m = md; a.slot0 = slot0; a.rows = H; a.in = in; a.status = status;
-        a.xop = actop; a.xop_slot_stride = actop_stride; a.y = ypart; a.y_slot_stride = H;
+        a.x = act; a.x_slot_stride = act_stride; a.y = ypart; a.y_slot_stride = H;
         return launch_gemv(dt, a, nslots, s);
     };
 
@@ -396,11 +399,6 @@ static int run_experts(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
         PhaseTimer pt(PH_GATEUP, s);
         WM_FAIL_HIP(gate_up(0, n_main, d->gate_type, d->up_type, I));
         if (sh && !merge) WM_FAIL_HIP(gate_up(K, 1, d->sh_gate_type, d->sh_up_type, Is));
-    }
-    {
-        PhaseTimer pt(PH_ACTPREP, s);
-        WM_FAIL_HIP(act_prep(0, n_main, d->gate_type, d->up_type, d->down_type, I));
-        if (sh && !merge) WM_FAIL_HIP(act_prep(K, 1, d->sh_gate_type, d->sh_up_type, d->sh_down_type, Is));
     }
     {
         PhaseTimer pt(PH_DOWN, s);
@@ -418,6 +416,71 @@ static int run_experts(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
     return WM_OK;
 }
 
+static int rpt_of(int t, int in) { return geometry(t, in).rpt; }
+
+// One launch of the fused step kernel; returns 1 when the type combination has
+// no fused instantiation (the caller then runs the per-phase kernels).
+static int run_fused(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, const float* x, float* out,
+                     const int32_t* forced_ids, const float* forced_w, int32_t* ids, float* w, hipStream_t s) {
+    const bool sh = has_shared(d);
+    if (d->gate_type != d->up_type || (sh && d->sh_gate_type != d->sh_up_type)) return 1;
+    const int gut = d->gate_type, dt = d->down_type;
+    const int sgut = sh ? d->sh_gate_type : gut, sdt = sh ? d->sh_down_type : dt;
+    if (!decode_step_supported(gut, dt, sgut, sdt)) return 1;
+    const int H = d->hidden, I = d->inter, Is = L.Is, K = d->top_k, E = d->n_experts;
+    DecodeArgs a = {};
+    a.H = H; a.I = I; a.Is = Is; a.E = E; a.K = K; a.has_shared = sh ? 1 : 0;
+    a.forced = forced_ids ? 1 : 0;
+    if (int rc = aligned_input(x, H, (float*)(ws + L.xin), s)) return rc;
+    {
+        const bool aligned = (H % 4 == 0) && al(x, 16) && al(d->router, 16);
+        // two rows per item: the item count is what hides the router's latency
+        a.rr = std::min(2, router_rows_per_wg(H, aligned));
+        a.router_region = router_region(H, aligned);
+        if (a.rr <= 0) return 1;
+    }
+    a.x = x; a.out = out; a.router = d->router;
+    a.gate = (const uint8_t*)d->gate_exps; a.up = (const uint8_t*)d->up_exps; a.down = (const uint8_t*)d->down_exps;
+    a.gstride = d->gate_stride ? d->gate_stride : matrix_bytes(gut, I, H);
+    a.ustride = d->up_stride ? d->up_stride : matrix_bytes(gut, I, H);
+    a.dstride = d->down_stride ? d->down_stride : matrix_bytes(dt, H, I);
+    a.sh_gate = (const uint8_t*)d->sh_gate; a.sh_up = (const uint8_t*)d->sh_up; a.sh_down = (const uint8_t*)d->sh_down;
+    a.sh_gate_inp = sh ? d->sh_gate_inp : nullptr;
+    a.forced_ids = forced_ids; a.forced_w = forced_w;
+    a.logits = (float*)(ws + L.logits); a.ids = ids; a.w = w;
+    a.hits = (uint32_t*)(ws + L.hits); a.status = (int32_t*)(ws + L.status);
+    a.act = (float*)(ws + L.act); a.act_stride = L.Imax;
+    a.ypart = (float*)(ws + L.ypart); a.shgate = (float*)(ws + L.shgate); a.ctr = (uint32_t*)(ws + L.ctr);
+    // work split: gate/up items of 2 x tpw_gu tiles of gate and of up (at most
+    // GU_ROWS_MAX rows); down items of rows_dn_item rows (4 waves, a whole
+    // number of tiles each, for the routed and the shared down type alike)
+    const int rpt_gu = rpt_of(gut, H);
+    a.tpw_gu = std::max(1, std::min(8, GU_ROWS_MAX / (2 * rpt_gu)));
+    const int rows_gu = 2 * a.tpw_gu * rpt_gu;
+    a.n_gu_slot = (I + rows_gu - 1) / rows_gu;
+    a.n_sgu = sh ? (Is + rows_gu - 1) / rows_gu : 0;
+    int unit = WAVES * rpt_of(dt, I);
+    if (sh) unit = std::max(unit, WAVES * rpt_of(sdt, Is));      // powers of two: the max is the lcm
+    int rows_dn = std::max(unit, 128);
+    while ((H + rows_dn - 1) / rows_dn > C_MAX_RANGES) rows_dn *= 2;
+    a.rows_dn_item = rows_dn;
+    a.n_dn_slot = (H + rows_dn - 1) / rows_dn;
+    a.it_router = 1;
+    a.n_router = a.forced ? 0 : (E + a.rr - 1) / a.rr;
+    a.it_sgu = a.it_router + a.n_router;
+    a.it_sdn = a.it_sgu + a.n_sgu;
+    a.it_gu = a.it_sdn + (sh ? a.n_dn_slot : 0);
+    a.it_dn = a.it_gu + K * a.n_gu_slot;
+    a.n_items = a.it_dn + K * a.n_dn_slot;
+    if (d->flags & WM_FLAG_TIMELINE) {
+        a.timeline = (uint64_t*)(ws + L.timeline);
+        a.timeline_cap = TIMELINE_CAP;
+    }
+    PhaseTimer pt(PH_STEP, s);
+    WM_FAIL_HIP(launch_decode_step(a, gut, dt, sgut, sdt, s));
+    return WM_OK;
+}
+
 extern "C" int wm_moe_decode(const wm_layer_desc* d, const float* x, float* out, void* ws, int64_t ws_bytes,
                              int max_tokens, int step, void* stream) {
     if (int rc = validate_desc(d, true)) return rc;
@@ -431,6 +494,10 @@ extern "C" int wm_moe_decode(const wm_layer_desc* d, const float* x, float* out,
     int32_t* ids = (int32_t*)(w8 + L.tr_ids) + (int64_t)slot * d->top_k;
     float* wts = (float*)(w8 + L.tr_w) + (int64_t)slot * d->top_k;
     float* logits = (float*)(w8 + L.logits);
+    if (!(d->flags & WM_FLAG_MULTI_KERNEL)) {
+        int rc = run_fused(d, L, w8, x, out, nullptr, nullptr, ids, wts, s);
+        if (rc <= 0) return rc;
+    }
     PhaseTimer step_timer(PH_STEP, s);
     {
         PhaseTimer pt(PH_ROUTER, s);
@@ -456,9 +523,14 @@ extern "C" int wm_moe_decode_forced(const wm_layer_desc* d, const float* x, cons
     int slot = step % max_tokens;
     int32_t* ids = (int32_t*)(w8 + L.tr_ids) + (int64_t)slot * d->top_k;
     float* wts = (float*)(w8 + L.tr_w) + (int64_t)slot * d->top_k;
+    if (!(d->flags & WM_FLAG_MULTI_KERNEL)) {
+        int rc = run_fused(d, L, w8, x, out, ids_in, w_in, ids, wts, s);
+        if (rc <= 0) return rc;
+    }
     PhaseTimer step_timer(PH_STEP, s);
     WM_FAIL_HIP(hipMemcpyAsync(ids, ids_in, (size_t)d->top_k * 4, hipMemcpyDeviceToDevice, s));
     WM_FAIL_HIP(hipMemcpyAsync(wts, w_in, (size_t)d->top_k * 4, hipMemcpyDeviceToDevice, s));
+    WM_FAIL_HIP(launch_count_hits(ids, d->top_k, d->n_experts, (uint32_t*)(w8 + L.hits), (int32_t*)(w8 + L.status), s));
     return run_experts(d, L, w8, x, ids, wts, out, s);
 }
 
@@ -479,36 +551,28 @@ extern "C" int wm_expert_ffn(const void* gate, int gt, const void* up, int ut, c
     uint8_t* w8 = (uint8_t*)ws;
     int32_t* status = (int32_t*)w8;
     int64_t o = 256;
-    uint32_t* xop_g = (uint32_t*)(w8 + o); o += up256(xop_bytes(H));
-    uint32_t* xop_u = (uint32_t*)(w8 + o); o += up256(xop_bytes(H));
+    float* xin = (float*)(w8 + o); o += 2 * up256(xop_bytes(H));
     float* gb = (float*)(w8 + o); o += up256((int64_t)I * 4);
     float* ub = (float*)(w8 + o); o += up256((int64_t)I * 4);
-    float* act = (float*)(w8 + o); o += up256((int64_t)I * 4);
-    uint32_t* actop = (uint32_t*)(w8 + o);
+    float* act = (float*)(w8 + o);
+    if (int rc = aligned_input(x, H, xin, s)) return rc;
     MatSet mg = {(const uint8_t*)gate, 0, nullptr, 1, 1, nullptr};
     MatSet mu = {(const uint8_t*)up, 0, nullptr, 1, 1, nullptr};
     MatSet md = {(const uint8_t*)down, 0, nullptr, 1, 1, nullptr};
-    XPrepArgs xp = {0, 1, H, x, nullptr, 0, xop_g, 0, nullptr, 0};
-    WM_FAIL_HIP(launch_xprep(gt, xp, s));
     if (gt == ut) {
         GateUpArgs a = {};
-        a.gate = mg; a.up = mu; a.rows = I; a.in = H; a.xop = xop_g; a.act = act; a.status = status;
+        a.gate = mg; a.up = mu; a.rows = I; a.in = H; a.x = x; a.act = act; a.status = status;
         WM_FAIL_HIP(launch_gateup(gt, a, 1, s));
-        XPrepArgs ap = {0, 1, I, act, nullptr, 0, actop, 0, nullptr, 0};
-        WM_FAIL_HIP(launch_xprep(dt, ap, s));
     } else {
         GemvArgs a = {};
-        a.m = mg; a.rows = I; a.in = H; a.xop = xop_g; a.y = gb; a.status = status;
+        a.m = mg; a.rows = I; a.in = H; a.x = x; a.y = gb; a.status = status;
         WM_FAIL_HIP(launch_gemv(gt, a, 1, s));
-        XPrepArgs xu = {0, 1, H, x, nullptr, 0, xop_u, 0, nullptr, 0};
-        WM_FAIL_HIP(launch_xprep(ut, xu, s));
-        a.m = mu; a.xop = xop_u; a.y = ub;
+        a.m = mu; a.y = ub;
         WM_FAIL_HIP(launch_gemv(ut, a, 1, s));
-        XPrepArgs ap = {1, 1, I, gb, ub, 0, actop, 0, act, 0};
-        WM_FAIL_HIP(launch_xprep(dt, ap, s));
+        WM_FAIL_HIP(launch_swiglu(gb, ub, act, I, 1, 0, s));
     }
     GemvArgs dn = {};
-    dn.m = md; dn.rows = H; dn.in = I; dn.xop = actop; dn.y = out; dn.status = status;
+    dn.m = md; dn.rows = H; dn.in = I; dn.x = act; dn.y = out; dn.status = status;
     WM_FAIL_HIP(launch_gemv(dt, dn, 1, s));
     return WM_OK;
 }
@@ -643,7 +707,7 @@ extern "C" int gpu_upload_router(int layer, const float* weights, int hidden_dim
 extern "C" int gpu_router(int layer, const float* normed, int hidden_dim, float* logits_out, int num_experts) {
     if (!G.init || layer < 0 || layer >= 64 || !G.router[layer]) return -1;
     if (G.router_dims[layer][0] != hidden_dim || G.router_dims[layer][1] != num_experts) return -1;
-    if (2 * (int64_t)hidden_dim * 4 > 65536) return -1;
+    if (router_rows_per_wg(hidden_dim, false) <= 0) return -1;
     if (ensure_ws(hidden_dim, std::max(num_experts, 64))) return -1;
     float* dx = G.dio;
     float* dl = G.dio + ((hidden_dim + 255) & ~255);

@@ -266,8 +266,15 @@ struct XOp {
     float s;
 };
 
-// Build the operand of 64 values v[j] (segment order) for type T.
-template <int T> WM_DEV void build_xop(const float* v, uint32_t* out /* XOP_DW dwords */) {
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Operand of 64 values v[j] (segment order) for type T: two signed 8-bit
+// digits per value, x_j ~= s * (256*hi + lo) with |256*hi + lo| <= 32639
+// (round to nearest even), packed in the byte order of the segment's
+// quantised values (Q8_0: after each block's 2-byte scale), the exact integer
+// run sums, and s = amax / 32639 (NaN when a value is not finite, which makes
+// every dot product with the segment NaN).
+template <int T> WM_DEV void xop_core(const float* v, uint32_t* hi, uint32_t* lo, int* sum, float& s) {
     constexpr bool Q8 = (T == Q8_0);
     constexpr int RUNLEN = (T == Q8_0 || T == Q4_K || T == Q5_K) ? 32 : 16;
     float amax = 0.0f;
@@ -278,10 +285,10 @@ template <int T> WM_DEV void build_xop(const float* v, uint32_t* out /* XOP_DW d
         finite = finite && isfinite(v[j]);
     }
     float inv = amax > 0.0f ? 32639.0f / amax : 0.0f;
-    uint32_t hi[17], lo[17];
-    int sum[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int k = 0; k < 17; k++) hi[k] = lo[k] = 0u;
+#pragma unroll
+    for (int r = 0; r < 4; r++) sum[r] = 0;
 #pragma unroll
     for (int j = 0; j < 64; j++) {
         int xi = finite ? (int)rintf(v[j] * inv) : 0;
@@ -293,31 +300,40 @@ template <int T> WM_DEV void build_xop(const float* v, uint32_t* out /* XOP_DW d
         lo[p >> 2] |= ((uint32_t)l & 0xFFu) << (8 * (p & 3));
         sum[j / RUNLEN] += xi;
     }
-#pragma unroll
-    for (int k = 0; k < 17; k++) {
-        out[XOP_HI + k] = hi[k];
-        out[XOP_LO + k] = lo[k];
-    }
-#pragma unroll
-    for (int r = 0; r < 4; r++) out[XOP_SUM + r] = (uint32_t)sum[r];
-    float s = finite ? amax / 32639.0f : __builtin_nanf("");
-    out[XOP_S] = __builtin_bit_cast(uint32_t, s);
-    out[XOP_S + 1] = 0u;
+    s = finite ? amax / 32639.0f : __builtin_nanf("");
 }
 
-WM_DEV void load_xop(const uint32_t* src, XOp& x) {
-    const uint4* p = (const uint4*)src;
-    uint32_t t[40];
+// The 64 values of segment `seg` of a 16-byte aligned fp32 vector: four runs
+// of 16 consecutive floats (seg_col), fetched as 16 b128 loads.
+template <int T> WM_DEV void xop_fetch(const float* src, int seg, f32x4 (&r)[16]) {
 #pragma unroll
-    for (int k = 0; k < 10; k++) {
-        uint4 v = p[k];
-        t[4 * k] = v.x; t[4 * k + 1] = v.y; t[4 * k + 2] = v.z; t[4 * k + 3] = v.w;
+    for (int g = 0; g < 4; g++) {
+        const f32x4* p = (const f32x4*)(src + seg_col(T, seg, 16 * g));
+#pragma unroll
+        for (int q = 0; q < 4; q++) r[4 * g + q] = p[q];
     }
+}
+
+template <int T> WM_DEV void xop_make(const f32x4 (&r)[16], XOp& x) {
+    float v[64];
 #pragma unroll
-    for (int k = 0; k < 17; k++) { x.hi[k] = t[XOP_HI + k]; x.lo[k] = t[XOP_LO + k]; }
-#pragma unroll
-    for (int r = 0; r < 4; r++) x.sum[r] = (int)t[XOP_SUM + r];
-    x.s = __builtin_bit_cast(float, t[XOP_S]);
+    for (int i = 0; i < 16; i++) {
+        v[4 * i] = r[i].x; v[4 * i + 1] = r[i].y; v[4 * i + 2] = r[i].z; v[4 * i + 3] = r[i].w;
+    }
+    xop_core<T>(v, x.hi, x.lo, x.sum, x.s);
+}
+
+// Device-coherent access for data handed between workgroups inside one
+// launch (COH = true): relaxed agent-scope atomics, i.e. loads / stores with
+// the device-scope cache policy (sc1), which bypass the per-XCD L2's
+// non-coherent copies without whole-cache writeback or invalidation.
+template <bool COH, typename V> WM_DEV void gst(V* p, V v) {
+    if constexpr (COH) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *p = v;
+}
+template <bool COH, typename V> WM_DEV V gld(const V* p) {
+    if constexpr (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else return *p;
 }
 
 // Segment partial dot product: sum_j w_j * x_j of the lane's 64 weights.
@@ -345,10 +361,66 @@ template <int T> WM_DEV float seg_dot(const Seg<T>& s, const XOp& x) {
     }
 }
 
-// Sum over the `lpr` consecutive lanes of a row (lpr a power of two <= 64).
+// DPP lane moves (gfx9 encodings): quad permutes, mirrors within 8 and 16
+// lanes, rotations within a row of 16, and the row broadcasts of lane 15 /
+// lane 31.  A lane whose row is masked off, or whose source is off, gets 0.
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+constexpr int DPP_ROR1 = 0x121, DPP_ROR2 = 0x122, DPP_ROR4 = 0x124, DPP_ROR8 = 0x128;
+constexpr int DPP_BCAST15 = 0x142, DPP_BCAST31 = 0x143;
+template <int CTRL, int ROW_MASK = 0xF> WM_DEV uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xF, false);
+}
+template <int CTRL, int ROW_MASK = 0xF> WM_DEV float dpp_f32(float v) {
+    return __builtin_bit_cast(float, dpp_u32<CTRL, ROW_MASK>(__builtin_bit_cast(uint32_t, v)));
+}
+template <int CTRL> WM_DEV uint64_t dpp_u64(uint64_t v) {
+    return ((uint64_t)dpp_u32<CTRL>((uint32_t)(v >> 32)) << 32) | dpp_u32<CTRL>((uint32_t)v);
+}
+WM_DEV uint64_t readlane_u64(uint64_t v, int lane) {
+    return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), lane) << 32) |
+           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+}
+
+// Sum over groups of `lpr` consecutive lanes (lpr a power of two <= 64), with
+// DPP moves; the sum is complete in the group's last lane (in every lane of
+// the group when lpr <= 16).  Called with all 64 lanes active.
 WM_DEV float row_reduce(float v, int lpr) {
-    for (int m = lpr >> 1; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    if (lpr >= 2) v += dpp_f32<DPP_XOR1>(v);
+    if (lpr >= 4) v += dpp_f32<DPP_XOR2>(v);
+    if (lpr >= 8) v += dpp_f32<DPP_HALF_MIRROR>(v);
+    if (lpr >= 16) v += dpp_f32<DPP_MIRROR>(v);
+    if (lpr >= 32) v += dpp_f32<DPP_BCAST15, 0xA>(v);
+    if (lpr >= 64) v += dpp_f32<DPP_BCAST31, 0xC>(v);
     return v;
+}
+
+// Maximum of a 32-bit value over the wave (all 64 lanes active), uniform result.
+WM_DEV uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_u32<DPP_XOR1>(v));
+    v = max(v, dpp_u32<DPP_XOR2>(v));
+    v = max(v, dpp_u32<DPP_HALF_MIRROR>(v));
+    v = max(v, dpp_u32<DPP_MIRROR>(v));
+    // every lane of a row of 16 now holds the row's maximum
+    uint32_t m = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+    m = max(m, (uint32_t)__builtin_amdgcn_readlane((int)v, 16));
+    m = max(m, (uint32_t)__builtin_amdgcn_readlane((int)v, 32));
+    m = max(m, (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
+    return m;
+}
+
+// Maximum of a 64-bit key over the wave (all 64 lanes active), uniform result.
+WM_DEV uint64_t wave_max_u64(uint64_t v) {
+    uint64_t o;
+    o = dpp_u64<DPP_XOR1>(v); v = o > v ? o : v;
+    o = dpp_u64<DPP_XOR2>(v); v = o > v ? o : v;
+    o = dpp_u64<DPP_HALF_MIRROR>(v); v = o > v ? o : v;
+    o = dpp_u64<DPP_MIRROR>(v); v = o > v ? o : v;
+    // every lane of a row of 16 now holds the row's maximum
+    uint64_t m = readlane_u64(v, 0);
+    o = readlane_u64(v, 16); m = o > m ? o : m;
+    o = readlane_u64(v, 32); m = o > m ? o : m;
+    o = readlane_u64(v, 48); m = o > m ? o : m;
+    return m;
 }
 
 // s_waitcnt with vmcnt only (gfx9 encoding: vmcnt[3:0] | vmcnt[5:4] << 14,

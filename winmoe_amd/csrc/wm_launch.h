@@ -25,8 +25,8 @@ struct GemvArgs {
     int32_t slot0;            // first slot handled by the launch (blockIdx.y offset)
     int32_t rows, in;
     int32_t tiles_per_wave;
-    const uint32_t* xop;      // activation operands [slot][in/64][XOP_DW]
-    int64_t xop_slot_stride;  // dwords between slots (0 = shared by all slots)
+    const float* x;           // input vectors [slot][x_slot_stride], 16-byte aligned
+    int64_t x_slot_stride;    // floats between slots (0 = shared by all slots)
     float* y;                 // outputs [slot][rows]
     int64_t y_slot_stride;    // floats
     int32_t* status;
@@ -37,24 +37,10 @@ struct GateUpArgs {
     int32_t slot0;
     int32_t rows, in;
     int32_t tiles_per_wave;
-    const uint32_t* xop;      // operands of the (common) gate/up type, shared by all slots
+    const float* x;           // input vector shared by all slots, 16-byte aligned
     float* act;               // SwiGLU output [slot][act_slot_stride]
     int64_t act_slot_stride;
     int32_t* status;
-};
-
-// Activation-operand preparation: for `nslots` slots, segments of type t over
-// an `in`-long vector.  mode 0: v = src[slot*src_stride + col];
-// mode 1: v = silu(g) * u with g = src, u = src2 (also stored to act_out).
-struct XPrepArgs {
-    int32_t mode, nslots, in;
-    const float* src;
-    const float* src2;
-    int64_t src_stride;
-    uint32_t* out;
-    int64_t out_stride;       // dwords between slots
-    float* act_out;
-    int64_t act_stride;
 };
 
 struct CombineArgs {
@@ -72,7 +58,7 @@ struct CombineArgs {
 int launch_router_logits(const float* x, const float* W, int H, int E, float* logits, hipStream_t s);
 int launch_topk(const float* logits, int E, int K, int32_t* ids, float* w, uint32_t* hits, int32_t* status,
                 hipStream_t s);
-int launch_xprep(int t, const XPrepArgs& a, hipStream_t s);
+int launch_swiglu(const float* g, const float* u, float* act, int n, int nslots, int64_t stride, hipStream_t s);
 int launch_gemv(int t, const GemvArgs& a, int nslots, hipStream_t s);
 int launch_gateup(int t, const GateUpArgs& a, int nslots, hipStream_t s);
 int launch_combine(const CombineArgs& a, hipStream_t s);
@@ -80,6 +66,7 @@ int launch_shgate(const float* x, const float* g, int H, float* out, hipStream_t
 int launch_dequant(int t, const void* blocks, int64_t nblocks, float* out, hipStream_t s);
 int launch_quantize(int t, const float* x, int64_t nblocks, void* out, hipStream_t s);
 int launch_fill_i32(int32_t* p, int32_t v, int64_t n, hipStream_t s);
+int launch_count_hits(const int32_t* ids, int K, int E, uint32_t* hits, int32_t* status, hipStream_t s);
 int launch_axpy(float* acc, const float* y, float w, int n, hipStream_t s);
 
 // Geometry of the segment mapping for a row of `in` weights.

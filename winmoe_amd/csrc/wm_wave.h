@@ -1,0 +1,431 @@
+// wm_wave.h -- wave- and workgroup-level building blocks shared by the
+// standalone kernels (wm_kernels.hip) and the fused decode-step kernel
+// (wm_decode.hip).  Workgroups are 256 threads (4 wave64s).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/winmoe_hip.h"
+#include "wm_device.h"
+#include "wm_launch.h"
+
+namespace wm {
+
+constexpr int WAVES = 4;               // waves per workgroup
+constexpr int TILE_LDS = 4416;         // max tile (64 x 68 B) + 16 B alignment shift + 48 B over-read pad
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+WM_DEV const uint8_t* slot_matrix(const MatSet& m, int slot, int32_t* status) {
+    if (slot < m.n_routed) {
+        int e = m.ids ? m.ids[slot] : slot;
+        if (e < 0 || e >= m.E) {
+            if (status) atomicOr(status, WM_STATUS_BAD_EXPERT_ID);
+            return nullptr;
+        }
+        return m.base + (int64_t)e * m.stride;
+    }
+    return m.shared;
+}
+
+// Coalesced 16-byte loads of one tile: bytes [off, off + nbytes) of W, read
+// from the 16-byte aligned granules that contain them (a granule never
+// crosses a page, so the over-read stays inside the allocation).
+struct TileLoad {
+    u32x4 r[5];
+    uint32_t shift;
+    int nch;
+};
+WM_DEV void tile_issue(const uint8_t* W, int64_t off, int64_t nbytes, int lane, TileLoad& tl) {
+    uintptr_t G = (uintptr_t)(W + off);
+    uintptr_t A = G & ~(uintptr_t)15;
+    tl.shift = (uint32_t)(G - A);
+    tl.nch = (int)((tl.shift + nbytes + 15) >> 4);
+    const u32x4* p = (const u32x4*)A;
+#pragma unroll
+    for (int k = 0; k < 5; k++) {
+        int i = lane + 64 * k;
+        if (i < tl.nch) tl.r[k] = __builtin_nontemporal_load(p + i);
+    }
+}
+WM_DEV void tile_store(lds8_t* lt, const TileLoad& tl, int lane) {
+    lds32_t* d = (lds32_t*)lt;
+#pragma unroll
+    for (int k = 0; k < 5; k++) {
+        int i = lane + 64 * k;
+        if (i < tl.nch) {
+            lds32_t* q = d + 4 * i;
+            q[0] = tl.r[k].x; q[1] = tl.r[k].y; q[2] = tl.r[k].z; q[3] = tl.r[k].w;
+        }
+    }
+}
+
+WM_DEV float silu_mul(float g, float u) {
+    // g * sigmoid(g) * u with the branch-stable sigmoid of deltanet_impl.h:108-115
+    float sg;
+    if (g >= 0.0f) sg = 1.0f / (1.0f + expf(-g));
+    else { float z = expf(g); sg = z / (1.0f + z); }
+    return g * sg * u;
+}
+
+WM_DEV float sigmoid_stable(float v) {
+    if (v >= 0.0f) return 1.0f / (1.0f + expf(-v));
+    float z = expf(v);
+    return z / (1.0f + z);
+}
+
+WM_DEV int64_t tile_nbytes(const Geo& g, int rows, int t) {
+    int64_t rows_left = rows - (int64_t)t * g.rpt;
+    return (rows_left >= g.rpt ? g.rpt : rows_left) * g.row_bytes;
+}
+
+// ---------------------------------------------------------------- tile streaming
+// A wave streams its tiles through a ring of S LDS buffers filled by
+// global_load_lds_dwordx4 (each instruction: 64 lanes x 16 B = 1 KB of
+// consecutive bytes, written to LDS in lane order), so S tiles are in flight
+// per wave with no register staging.  Every tile is exactly NI instructions
+// (lanes past the tile end reload its last granule), so "tile t has landed"
+// is s_waitcnt vmcnt(#instructions issued after it).
+
+template <int T> WM_HD constexpr int tile_ni() {
+    return T == Q8_0 ? 5 : (T == Q6_K ? 4 : ((T == Q4_K || T == Q5_K) ? 3 : 2));
+}
+template <int T> WM_HD constexpr int tile_buf() { return tile_ni<T>() * 1024; }
+
+// Issue the NI DMA loads of bytes [off, off + nbytes) of W (16-byte granules
+// containing them) into dst.
+template <int NI>
+WM_DEV void tile_dma(const uint8_t* W, int64_t off, int64_t nbytes, int lane, lds8_t* dst) {
+    const uintptr_t G = (uintptr_t)(W + off);
+    const uintptr_t A = G & ~(uintptr_t)15;
+    const int nch = (int)(((G - A) + (uintptr_t)nbytes + 15) >> 4);
+#pragma unroll
+    for (int k = 0; k < NI; k++) {
+        int i = lane + 64 * k;
+        i = i < nch ? i : nch - 1;
+        __builtin_amdgcn_global_load_lds((const void*)(A + 16 * (uintptr_t)i),
+                                         (__attribute__((address_space(3))) void*)(dst + 1024 * k), 16, 0, 0);
+    }
+}
+
+// s_waitcnt vmcnt(ahead * NI) for ahead in [0, S).
+template <int NI, int S> WM_DEV void wait_tiles(int ahead) {
+    static_assert((S - 1) * NI <= 63, "vmcnt range");
+    if (ahead <= 0) WM_WAIT_VMCNT(0);
+    else if (ahead == 1) WM_WAIT_VMCNT(NI);
+    else if (S > 2 && ahead == 2) WM_WAIT_VMCNT(2 * NI);
+    else WM_WAIT_VMCNT(3 * NI < 64 ? 3 * NI : 63);
+}
+
+// One wave: row sums W[row] . x over tiles [t0, t1) (t0 < t1) of a
+// [rows][in] matrix.  x is the fp32 input vector (16-byte aligned); each
+// lane builds the integer-dot operand of its segment in registers while the
+// first S tiles are in flight.  Row results go to gout[row] (global,
+// device-coherent when COH) and/or lout[row - lrow0] (LDS).  ring holds
+// S * tile_buf<T>() bytes.
+template <int T, int S, bool COH>
+WM_DEV void wave_stream(const uint8_t* W, int rows, const Geo& g, int t0, int t1, const float* xsrc, lds8_t* ring,
+                        float* gout, __attribute__((address_space(3))) float* lout, int lrow0, int lane) {
+    constexpr int NI = tile_ni<T>(), BUF = tile_buf<T>();
+    const int rig = lane / g.lpr, sub = lane % g.lpr;
+    f32x4 xr[16];
+    xop_fetch<T>(xsrc, sub, xr);
+    // The prologue always issues S tiles (repeating the last one when the
+    // wave has fewer), so exactly S * NI loads follow the operand fetch.
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        const int t = min(t0 + s, t1 - 1);
+        tile_dma<NI>(W, (int64_t)t * g.tile_bytes, tile_nbytes(g, rows, t), lane, ring + s * BUF);
+    }
+    // keep the operand arithmetic (which waits for the operand loads) after
+    // the tile loads have been issued
+    __builtin_amdgcn_sched_barrier(0);
+    XOp x;
+    xop_make<T>(xr, x);
+    for (int t = t0; t < t1; t++) {
+        const int s = (t - t0) % S;
+        wait_tiles<NI, S>(min(S - 1, t1 - 1 - t));
+        const uint32_t shift = (uint32_t)(((uintptr_t)W + (uintptr_t)((int64_t)t * g.tile_bytes)) & 15u);
+        Seg<T> sg;
+        sg.load(ring + s * BUF + shift, lane < g.active ? lane : 0);
+        float p = lane < g.active ? seg_dot<T>(sg, x) : 0.0f;
+        p = row_reduce(p, g.lpr);
+        wave_lds_sync();           // every lane's reads of this buffer are done before it is refilled
+        if (t + S < t1) tile_dma<NI>(W, (int64_t)(t + S) * g.tile_bytes, tile_nbytes(g, rows, t + S), lane, ring + s * BUF);
+        const int row = t * g.rpt + rig;
+        if (sub == g.lpr - 1 && rig < g.rpt && row < rows) {
+            if (gout) gst<COH>(gout + row, p);
+            if (lout) lout[row - lrow0] = p;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- workgroup items
+// COH: the item's outputs are read by other workgroups of the same launch
+// (device-coherent stores).  The input vector is always read with ordinary
+// cached loads, even when another workgroup of the launch wrote it: its
+// writer stores it device-coherently and raises a flag after the stores
+// completed, nobody reads it before that flag, and caches hold nothing of it
+// from earlier launches (each launch starts with invalidated caches), so no
+// cache can return a stale copy.  Device-coherent loads would send every
+// item's reads of the same few KB past L2 and congest the channels holding them.
+constexpr int RING_S = 3;            // tiles in flight per wave
+constexpr int GU_ROWS_MAX = 512;     // rows of one gate/up item (LDS row sums)
+
+// Dynamic LDS of a 4-wave streaming workgroup: one ring per wave + gate/up row sums.
+WM_HD constexpr int wg_stream_lds_bytes(int max_tile_buf) { return WAVES * RING_S * max_tile_buf + 2 * GU_ROWS_MAX * 4; }
+
+// Gate/up + SwiGLU over tiles [tb, tb + 2*tpw) of one slot: waves 0-1 stream
+// gate, waves 2-3 stream up (tpw tiles each), row sums meet in LDS, and
+// act[row] = silu(g) * u.  A null matrix (bad expert id) yields zeros.
+template <int T, bool COH>
+WM_DEV void wg_gateup_item(const uint8_t* Wg, const uint8_t* Wu, int rows, int in, int tb, int tpw, const float* x,
+                           float* act, uint8_t* lds) {
+    typedef __attribute__((address_space(3))) float lf;
+    constexpr int BUF = tile_buf<T>();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const Geo g = geometry(T, in);
+    const int ntiles = (rows + g.rpt - 1) / g.rpt;
+    lf* garr = (lf*)(lds + WAVES * RING_S * BUF);
+    lf* uarr = garr + GU_ROWS_MAX;
+    const int r0 = tb * g.rpt;
+    const int r1 = min(rows, (tb + 2 * tpw) * g.rpt);
+    const int t0 = tb + (wave & 1) * tpw, t1 = min(t0 + tpw, ntiles);
+    const uint8_t* W = wave < 2 ? Wg : Wu;
+    if (Wg && Wu && t0 < t1)
+        wave_stream<T, RING_S, COH>(W, rows, g, t0, t1, x, (lds8_t*)(lds + wave * RING_S * BUF), nullptr,
+                                    wave < 2 ? garr : uarr, r0, lane);
+    __syncthreads();
+    for (int r = threadIdx.x; r < r1 - r0; r += 256) gst<COH>(act + r0 + r, (Wg && Wu) ? silu_mul(garr[r], uarr[r]) : 0.0f);
+    __syncthreads();
+}
+
+// y[row] = W[row] . x over tiles [tb, tb + 4*tpw) (tpw per wave).
+template <int T, bool COH>
+WM_DEV void wg_gemv_item(const uint8_t* W, int rows, int in, int tb, int tpw, const float* x, float* y, uint8_t* lds) {
+    constexpr int BUF = tile_buf<T>();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const Geo g = geometry(T, in);
+    const int ntiles = (rows + g.rpt - 1) / g.rpt;
+    const int t0 = tb + wave * tpw, t1 = min(t0 + tpw, ntiles);
+    if (t0 >= t1) return;
+    if (!W) {
+        const int rig = lane / g.lpr, sub = lane % g.lpr;
+        for (int t = t0; t < t1; t++) {
+            int row = t * g.rpt + rig;
+            if (sub == 0 && rig < g.rpt && row < rows) gst<COH>(y + row, 0.0f);
+        }
+        return;
+    }
+    wave_stream<T, RING_S, COH>(W, rows, g, t0, t1, x, (lds8_t*)(lds + wave * RING_S * BUF), y, nullptr, 0, lane);
+}
+
+// ---------------------------------------------------------------- router
+constexpr int ROUTER_LDS = 65536;    // LDS of a router workgroup (x + rows)
+
+// LDS bytes of one router operand (x or one weight row): H floats plus the
+// 16-byte alignment shift of an unaligned source, in whole 1 KB DMA units.
+WM_HD int router_region(int H, bool aligned) { return ((H * 4 + (aligned ? 0 : 16) + 1023) / 1024) * 1024; }
+// Rows per router workgroup (1..4), or 0 when x and one row do not fit.
+WM_HD int router_rows_per_wg(int H, bool aligned) {
+    int n = ROUTER_LDS / router_region(H, aligned) - 1;
+    return n < 1 ? 0 : (n > 4 ? 4 : n);
+}
+
+// Router logits of rows [r0, r0 + nr), nr <= 4, in the reference order
+// (transformer.h:172-191): lane l of a row keeps the running fp32 FMA over
+// columns l, l+16, ...; the 16 lanes then reduce with the xor tree 8, 4, 2, 1
+// (= _mm512_reduce_add_ps) and lane 0 adds the scalar tail.  x and the rows
+// are pulled into LDS regions of `region` bytes at once (LDS-DMA, 1 KB per
+// wave instruction, all in flight together); wave r then runs the 16 chains
+// of row r.  Called by all 256 threads.
+template <bool COH>
+WM_DEV void wg_router_rows(const float* __restrict__ x, const float* __restrict__ W, int H, int r0, int nr, int region,
+                           lds8_t* lds, float* __restrict__ logits) {
+    typedef __attribute__((address_space(3))) float lf;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t nbytes = (int64_t)H * 4;
+    // DMA units per operand: enough for H floats plus a possible 16 B shift,
+    // never past the region (the host sizes the region for the actual shift)
+    const int units = min((int)((nbytes + 16 + 1023) >> 10), region >> 10);
+    // operand q: 0 = x, 1..nr = rows; its DMA units go round-robin over the waves
+    for (int u = wave; u < (nr + 1) * units; u += WAVES) {
+        const int q = u / units, k = u % units;
+        const float* src = q == 0 ? x : W + (int64_t)(r0 + q - 1) * H;
+        const uintptr_t G = (uintptr_t)src, A = G & ~(uintptr_t)15;
+        const int nch = (int)(((G - A) + (uintptr_t)nbytes + 15) >> 4);
+        int i = lane + 64 * k;
+        i = i < nch ? i : nch - 1;
+        __builtin_amdgcn_global_load_lds((const void*)(A + 16 * (uintptr_t)i),
+                                         (__attribute__((address_space(3))) void*)(lds + q * region + 1024 * k), 16, 0,
+                                         0);
+    }
+    WM_WAIT_VMCNT(0);
+    __syncthreads();
+    if (wave < nr && lane < 16) {
+        const lf* xr = (const lf*)(lds + (((uintptr_t)x) & 15));
+        const float* wsrc = W + (int64_t)(r0 + wave) * H;
+        const lf* wr = (const lf*)(lds + (wave + 1) * region + (((uintptr_t)wsrc) & 15));
+        const int H16 = H - (H & 15), nsteps = H16 / 16;
+        float acc = 0.0f;
+        int s = 0;
+        for (; s + 16 <= nsteps; s += 16) {
+            float wv[16], xv[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                wv[j] = wr[lane + 16 * (s + j)];
+                xv[j] = xr[lane + 16 * (s + j)];
+            }
+#pragma unroll
+            for (int j = 0; j < 16; j++) acc = fmaf(wv[j], xv[j], acc);
+        }
+        for (; s < nsteps; s++) acc = fmaf(wr[lane + 16 * s], xr[lane + 16 * s], acc);
+        // xor tree 8, 4, 2, 1 over the 16 lanes as row rotations: after the
+        // step of distance d the partial sums repeat with period d, so the
+        // lane d places on is the xor partner up to that repetition
+        acc += dpp_f32<DPP_ROR8>(acc);
+        acc += dpp_f32<DPP_ROR4>(acc);
+        acc += dpp_f32<DPP_ROR2>(acc);
+        acc += dpp_f32<DPP_ROR1>(acc);
+        if (lane == 0) {
+            for (int c = H16; c < H; c++) acc = fmaf(wr[c], xr[c], acc);
+            gst<COH>(logits + r0 + wave, acc);
+        }
+    }
+    __syncthreads();
+}
+
+// K-pass arg-max (transformer.h:117-139: strict '>' from -1e30, skip picked,
+// equal values to the lower index, NaN never picked, nothing valid -> index 0)
+WM_DEV uint64_t topk_key(float v, int e) {
+    if (!(v > -1e30f)) return 0ull;              // NaN / -inf / <= -1e30 never selected
+    if (v == 0.0f) v = 0.0f;                     // -0 == +0 for the comparison
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)u << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)e);
+}
+
+// Per-lane sort of N keys, descending (bitonic network, unrolled).
+template <int N> WM_DEV void sort_desc(uint64_t (&k)[N]) {
+#pragma unroll
+    for (int size = 2; size <= N; size <<= 1)
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1)
+#pragma unroll
+            for (int i = 0; i < N; i++) {
+                const int l = i ^ stride;
+                if (l > i) {
+                    const bool desc = (i & size) == 0;
+                    const uint64_t a = k[i], b = k[l];
+                    const bool swap = desc ? (a < b) : (a > b);
+                    k[i] = swap ? b : a;
+                    k[l] = swap ? a : b;
+                }
+            }
+}
+
+// One wave: top-K of E <= 1024 logits and the softmax over the picks
+// (transformer.h:142-149); lane 0 writes ids / w, bumps the hit counters
+// and reports degenerate / non-finite routing in *status.  Each lane sorts
+// its keys once; a pass then takes the wave maximum of the lane heads (value
+// bits first, the index only on a value tie) and the winning lane drops its head.
+template <int MAXV, bool COH>
+WM_DEV void wave_topk_n(const float* logits, int E, int K, int32_t* ids, float* w, uint32_t* hits, int32_t* status,
+                        int lane) {
+    uint64_t key[MAXV];
+    float lv[MAXV];
+    // all loads unconditional (index clamped) so they are in flight together
+#pragma unroll
+    for (int i = 0; i < MAXV; i++) lv[i] = gld<COH>(logits + min(lane + 64 * i, E - 1));
+    const float v0 = lv[0];                           // logits[0] (lane 0): the value of a degenerate pick
+#pragma unroll
+    for (int i = 0; i < MAXV; i++) {
+        int e = lane + 64 * i;
+        key[i] = e < E ? topk_key(lv[i], e) : 0ull;
+    }
+    sort_desc<MAXV>(key);
+    int my_id[16];
+    float my_v[16];
+    bool degenerate = false;
+    for (int k = 0; k < K; k++) {
+        const uint32_t hi = (uint32_t)(key[0] >> 32), lo = (uint32_t)key[0];
+        const uint32_t vmax = wave_max_u32(hi);
+        const uint64_t tie = __builtin_amdgcn_ballot_w64(hi == vmax);
+        uint32_t lmax;
+        if (__builtin_popcountll(tie) == 1) lmax = (uint32_t)__builtin_amdgcn_readlane((int)lo, (int)__builtin_ctzll(tie));
+        else lmax = wave_max_u32(hi == vmax ? lo : 0u);
+        const uint64_t best = ((uint64_t)vmax << 32) | lmax;
+        int e = 0;
+        float v = v0;
+        if (best == 0ull) degenerate = true;
+        else {
+            e = (int)(0xFFFFFFFFu - lmax);
+            if ((e & 63) == lane) {
+#pragma unroll
+                for (int i = 0; i + 1 < MAXV; i++) key[i] = key[i + 1];
+                key[MAXV - 1] = 0ull;
+            }
+            // the value back from its order key (-0 comes back as +0, which
+            // changes no difference or exponential below)
+            v = __builtin_bit_cast(float, (vmax & 0x80000000u) ? (vmax & 0x7FFFFFFFu) : ~vmax);
+        }
+        my_id[k] = e;
+        my_v[k] = v;
+    }
+    if (lane == 0) {
+        float wl[16];
+        for (int k = 0; k < K; k++) wl[k] = my_v[k];
+        float wmax = wl[0];
+        for (int k = 1; k < K; k++) if (wl[k] > wmax) wmax = wl[k];
+        float wsum = 0.0f;
+        for (int k = 0; k < K; k++) { wl[k] = expf(wl[k] - wmax); wsum += wl[k]; }
+        if (wsum > 0.0f) for (int k = 0; k < K; k++) wl[k] /= wsum;
+        bool nonfinite = false;
+        for (int k = 0; k < K; k++) {
+            gst<COH>(ids + k, (int32_t)my_id[k]);
+            gst<COH>(w + k, wl[k]);
+            nonfinite = nonfinite || !isfinite(wl[k]);
+            if (hits) atomicAdd(hits + my_id[k], 1u);
+        }
+        int st = (degenerate ? WM_STATUS_DEGENERATE_ROUTING : 0) | (nonfinite ? WM_STATUS_NONFINITE_WEIGHT : 0);
+        if (st && status) atomicOr(status, st);
+    }
+}
+
+template <bool COH = false>
+WM_DEV void wave_topk(const float* logits, int E, int K, int32_t* ids, float* w, uint32_t* hits, int32_t* status,
+                      int lane) {
+    if (E <= 512) wave_topk_n<8, COH>(logits, E, K, ids, w, hits, status, lane);
+    else wave_topk_n<16, COH>(logits, E, K, ids, w, hits, status, lane);
+}
+
+// Shared-expert gate: sigmoid_stable((float) sum_h g[h] * x[h]) with the dot
+// in fp64 (winmoe_inference.c:2005-2009); fixed-order tree reduction.  All
+// 256 threads call it; thread 0 writes *out.
+template <bool COH = false>
+WM_DEV void wg_shgate(const float* __restrict__ x, const float* __restrict__ g, int H, float* __restrict__ out) {
+    __shared__ double s_part[256];
+    double acc = 0.0;
+    for (int base = 0; base < H; base += 256 * 16) {
+        float gv[16], xv[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {              // clamped, unconditional: all loads in flight together
+            const int h = min(base + (int)threadIdx.x + 256 * i, H - 1);
+            gv[i] = g[h];
+            xv[i] = x[h];
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            if (base + (int)threadIdx.x + 256 * i < H) acc += (double)gv[i] * (double)xv[i];
+    }
+    s_part[threadIdx.x] = acc;
+    __syncthreads();
+    for (int m = 128; m >= 1; m >>= 1) {
+        if ((int)threadIdx.x < m) s_part[threadIdx.x] += s_part[threadIdx.x + m];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) gst<COH>(out, sigmoid_stable((float)s_part[0]));
+    __syncthreads();
+}
+
+}  // namespace wm

@@ -178,11 +178,14 @@ class MoELayer:
     (winmoe_inference.c:467-489).  ``strides`` overrides the per-expert byte
     stride (e.g. a GGUF tensor's data_size / E).  The workspace (routing trace
     of ``max_tokens`` entries, hit counters, scratch) is allocated once.
+    A decode step is one fused kernel launch; ``multi_kernel=True`` runs the
+    same step as per-phase launches (bit-identical, used as a cross-check).
     """
 
     def __init__(self, H: int, I: int, E: int, K: int, router: Optional[torch.Tensor], gate_exps: torch.Tensor,
                  up_exps: torch.Tensor, down_exps: torch.Tensor, types: Sequence[int],
-                 shared: Optional[SharedExpert] = None, max_tokens: int = 256, strides=(0, 0, 0)):
+                 shared: Optional[SharedExpert] = None, max_tokens: int = 256, strides=(0, 0, 0),
+                 multi_kernel: bool = False, timeline: bool = False):
         self.H, self.I, self.E, self.K = H, I, E, K
         self.types = tuple(types)
         self.max_tokens = max_tokens
@@ -197,6 +200,7 @@ class MoELayer:
         d.router = _p(self.router)
         d.gate_exps, d.up_exps, d.down_exps = _p(gate_exps), _p(up_exps), _p(down_exps)
         d.gate_stride, d.up_stride, d.down_stride = strides
+        d.flags = (_lib.FLAG_MULTI_KERNEL if multi_kernel else 0) | (_lib.FLAG_TIMELINE if timeline else 0)
         if shared is not None:
             for t, n in ((shared.gate, "shared.gate"), (shared.up, "shared.up"), (shared.down, "shared.down")):
                 _need(t, torch.uint8, n)
@@ -273,6 +277,16 @@ class MoELayer:
         """Per-expert selection counters (uint32 stored, returned as int32 view)."""
         _, _, ho = self._trace_off
         return self.ws[ho:ho + self.E * 4].view(torch.int32)
+
+    def timeline(self):
+        """Per-work-item timeline of the last fused step: uint64 [items][8]
+        (start, dependencies met, main work done, end in device clock ticks;
+        kind | hw ids; three zero words)."""
+        off, cap = C.c_int64(), C.c_int64()
+        check(load().wm_workspace_timeline(C.byref(self.desc), self.max_tokens, C.byref(off), C.byref(cap)),
+              "wm_workspace_timeline")
+        n = cap.value * 8 * 8
+        return self.ws[off.value:off.value + n].view(torch.int64).view(cap.value, 8)
 
     def status(self) -> int:
         v = C.c_int32()

@@ -95,7 +95,7 @@ class SynthLayer:
 
 
 def build_layer(cfg: LayerConfig, device="cuda", layer_index: int = 0, max_tokens: Optional[int] = None,
-                E: Optional[int] = None) -> SynthLayer:
+                E: Optional[int] = None, multi_kernel: bool = False) -> SynthLayer:
     """Generate one layer of cfg on device.  E may shrink the expert count for tests."""
     E = E or cfg.E
     g = torch.Generator(device=device)
@@ -125,8 +125,15 @@ def build_layer(cfg: LayerConfig, device="cuda", layer_index: int = 0, max_token
             gi = torch.randn(cfg.H, generator=g, device=device, dtype=torch.float32).mul_(0.02)
         shared = SharedExpert(sg, su, sd, tuple(cfg.shared_types), gi, Is)
     layer = MoELayer(cfg.H, cfg.I, E, cfg.K, router, gate, up, down, cfg.types, shared=shared,
-                     max_tokens=max_tokens or max(cfg.tokens, 1))
+                     max_tokens=max_tokens or max(cfg.tokens, 1), multi_kernel=multi_kernel)
     return SynthLayer(cfg, layer, router, gate, up, down, shared)
+
+
+def twin_layer(sl: SynthLayer, multi_kernel: bool) -> MoELayer:
+    """A second MoELayer over the same device tensors (own workspace)."""
+    c = sl.cfg
+    return MoELayer(c.H, c.I, sl.layer.E, c.K, sl.router, sl.gate, sl.up, sl.down, c.types, shared=sl.shared,
+                    max_tokens=sl.layer.max_tokens, multi_kernel=multi_kernel)
 
 
 def make_hidden(cfg: LayerConfig, device="cuda", tokens: Optional[int] = None, seed_offset: int = 0) -> torch.Tensor:
