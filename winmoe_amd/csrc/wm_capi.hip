@@ -418,6 +418,20 @@ static int run_experts(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
 
 static int rpt_of(int t, int in) { return geometry(t, in).rpt; }
 
+// Workgroups of the fused step resident on the current device at once: two
+// per CU (each holds a 64 KB LDS ring set).
+static int resident_slots() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
+    if (!cached[dev]) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+        cached[dev] = 2 * cus;
+    }
+    return cached[dev];
+}
+
 // One launch of the fused step kernel; returns 1 when the type combination has
 // no fused instantiation (the caller then runs the per-phase kernels).
 static int run_fused(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, const float* x, float* out,
@@ -434,7 +448,8 @@ static int run_fused(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, con
     if (int rc = aligned_input(x, H, (float*)(ws + L.xin), s)) return rc;
     {
         const bool aligned = (H % 4 == 0) && al(x, 16) && al(d->router, 16);
-        // two rows per item: the item count is what hides the router's latency
+        // two rows per item: with the shared gate/up items the router
+        // items fill the device at the start
         a.rr = std::min(2, router_rows_per_wg(H, aligned));
         a.router_region = router_region(H, aligned);
         if (a.rr <= 0) return 1;
@@ -451,22 +466,35 @@ static int run_fused(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, con
     a.hits = (uint32_t*)(ws + L.hits); a.status = (int32_t*)(ws + L.status);
     a.act = (float*)(ws + L.act); a.act_stride = L.Imax;
     a.ypart = (float*)(ws + L.ypart); a.shgate = (float*)(ws + L.shgate); a.ctr = (uint32_t*)(ws + L.ctr);
-    // work split: gate/up items of 2 x tpw_gu tiles of gate and of up (at most
-    // GU_ROWS_MAX rows); down items of rows_dn_item rows (4 waves, a whole
-    // number of tiles each, for the routed and the shared down type alike)
+    // Work split.  The device holds `slots` decode-step workgroups at once
+    // (2 per CU by LDS); items are sized so that each phase fits one wave of
+    // them: the shared gate/up next to the router items, all routed gate/up
+    // items together, all down items together.  Gate/up items are 2 x tpw
+    // tiles of gate and of up (at most GU_ROWS_MAX rows); down items are
+    // rows_dn_item rows, a whole number of tiles per wave for the routed and
+    // the shared down type alike.
+    const int slots = resident_slots();
     const int rpt_gu = rpt_of(gut, H);
-    a.tpw_gu = std::max(1, std::min(8, GU_ROWS_MAX / (2 * rpt_gu)));
-    const int rows_gu = 2 * a.tpw_gu * rpt_gu;
-    a.n_gu_slot = (I + rows_gu - 1) / rows_gu;
-    a.n_sgu = sh ? (Is + rows_gu - 1) / rows_gu : 0;
+    auto gu_tpw = [&](int rows, int items) {
+        const int per = (rows + std::max(items, 1) - 1) / std::max(items, 1);
+        return std::max(1, std::min((per + 2 * rpt_gu - 1) / (2 * rpt_gu), GU_ROWS_MAX / (2 * rpt_gu)));
+    };
     int unit = WAVES * rpt_of(dt, I);
     if (sh) unit = std::max(unit, WAVES * rpt_of(sdt, Is));      // powers of two: the max is the lcm
-    int rows_dn = std::max(unit, 128);
+    const int K1 = K + (sh ? 1 : 0);
+    const int ranges_want = std::max(1, slots / K1);
+    int rows_dn = ((H + ranges_want - 1) / ranges_want + unit - 1) / unit * unit;
     while ((H + rows_dn - 1) / rows_dn > C_MAX_RANGES) rows_dn *= 2;
     a.rows_dn_item = rows_dn;
     a.n_dn_slot = (H + rows_dn - 1) / rows_dn;
-    a.it_router = 1;
     a.n_router = a.forced ? 0 : (E + a.rr - 1) / a.rr;
+    a.tpw_sgu = sh ? gu_tpw(Is, slots - 1 - a.n_router) : 1;
+    a.n_sgu = sh ? (Is + 2 * a.tpw_sgu * rpt_gu - 1) / (2 * a.tpw_sgu * rpt_gu) : 0;
+    a.tpw_gu = gu_tpw(I, (slots - (sh ? a.n_dn_slot : 0)) / K);
+    a.n_gu_slot = (I + 2 * a.tpw_gu * rpt_gu - 1) / (2 * a.tpw_gu * rpt_gu);
+    a.it_router = 1;
+    a.n_rgroups = (a.n_router + RGROUP - 1) / RGROUP;
+    if (a.n_rgroups > C_MAX_RGROUPS) return 1;
     a.it_sgu = a.it_router + a.n_router;
     a.it_sdn = a.it_sgu + a.n_sgu;
     a.it_gu = a.it_sdn + (sh ? a.n_dn_slot : 0);

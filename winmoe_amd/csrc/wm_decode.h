@@ -12,15 +12,19 @@ namespace wm {
 // while atomics on distinct lines proceed in parallel.  All zero between
 // launches.
 constexpr int CTR_STRIDE = 64;    // dwords between counters
+constexpr int RGROUP = 16;        // router items per group counter
 enum : int {
-    C_ROUTER = 0,      // router items finished
+    C_RTOP = 0,        // router groups finished: every logit is written
     C_TOPK = 1,        // routing of this step is in the trace
     C_AUX = 2,         // shared-expert gate (and forced routing) written
     C_COMBINED = 3,    // row ranges combined
-    C_GU = 4,          // + slot: gate/up items finished for the slot
-    C_RANGE = 36,      // + range: down items finished for the row range
+    C_SLOTEID = 4,     // not a counter: dword s = expert id of routed slot s
+    C_GU = 5,          // + slot: gate/up items finished for the slot
+    C_RGROUP = 37,     // + group: router items finished in the group
+    C_MAX_RGROUPS = 64,
+    C_RANGE = C_RGROUP + C_MAX_RGROUPS,   // + range: down items finished for the row range
     C_MAX_RANGES = 256,
-    C_TOTAL = C_RANGE + C_MAX_RANGES,   // counters (lines)
+    C_TOTAL = C_RANGE + C_MAX_RANGES,     // counters (lines)
 };
 
 struct DecodeArgs {
@@ -48,8 +52,8 @@ struct DecodeArgs {
     float* ypart;
     float* shgate;
     uint32_t* ctr;
-    int32_t n_items, it_router, n_router, it_sgu, n_sgu, it_sdn, it_gu, n_gu_slot, it_dn, n_dn_slot;
-    int32_t tpw_gu, rows_dn_item, router_region;
+    int32_t n_items, it_router, n_router, n_rgroups, it_sgu, n_sgu, it_sdn, it_gu, n_gu_slot, it_dn, n_dn_slot;
+    int32_t tpw_gu, tpw_sgu, rows_dn_item, router_region;
     uint64_t* timeline;    // NULL, or [n_items][8]: start, dependencies met, work done, end (device clock), kind | hw ids
     int32_t timeline_cap;
 };

@@ -92,20 +92,20 @@ WM_DEV void wg_flag(uint32_t* ctr) {
     if (threadIdx.x == 0) st_relaxed(ctr, 1u);
 }
 
-// Gate/up + SwiGLU item j of a slot: 2 * tpw_gu tiles of gate and of up.
+// Gate/up + SwiGLU item j of a slot: 2 * tpw tiles of gate and of up.
 template <int T>
-WM_DEV void item_gateup(const DecodeArgs& a, const uint8_t* Wg, const uint8_t* Wu, int rows, int j, float* act,
-                        uint8_t* smem) {
-    wg_gateup_item<T, true>(Wg, Wu, rows, a.H, j * 2 * a.tpw_gu, a.tpw_gu, a.x, act, smem);
+WM_DEV void item_gateup(const DecodeArgs& a, const uint8_t* Wg, const uint8_t* Wu, int rows, int j, int tpw,
+                        float* act, uint8_t* smem) {
+    wg_gateup_item<T, true>(Wg, Wu, rows, a.H, j * 2 * tpw, tpw, a.x, act, smem);
 }
 
 // Down-projection rows [range * rows_dn_item, ...) of one slot, 4 waves.
 template <int T>
 WM_DEV void item_down(const DecodeArgs& a, const uint8_t* W, int in, int range, const float* act, float* y,
-                      uint8_t* smem) {
+                      uint8_t* smem, const float* scale = nullptr) {
     const Geo g = geometry(T, in);
     const int tpw = a.rows_dn_item / (WAVES * g.rpt);
-    wg_gemv_item<T, true>(W, a.H, in, range * WAVES * tpw, tpw, act, y, smem);
+    wg_gemv_item<T, true>(W, a.H, in, range * WAVES * tpw, tpw, act, y, smem, scale);
 }
 
 WM_DEV uint32_t* ctr(const DecodeArgs& a, int i) { return a.ctr + (int64_t)i * CTR_STRIDE; }
@@ -141,33 +141,53 @@ __global__ __launch_bounds__(256) void k_decode_step(DecodeArgs a) {
         wg_flag(ctr(a, C_AUX));
         if (a.forced && threadIdx.x == 0) st_relaxed(ctr(a, C_TOPK), 1u);
     } else if (item < a.it_sgu) {
-        // ---- router rows; the last router item runs top-K
-        const int r0 = (item - a.it_router) * a.rr;
+        // ---- router rows.  The last item of each group of RGROUP bumps the
+        // top counter (all logits are in once it reaches n_rgroups); the last
+        // of those writes the trace: top-K, softmax weights, hit counts.
+        const int j = item - a.it_router;
+        const int r0 = j * a.rr, g = j / RGROUP;
         kind = 1;
         wg_router_rows<true>(a.x, a.router, a.H, r0, min(a.rr, a.E - r0), a.router_region, (lds8_t*)smem, a.logits);
         t_work = __builtin_amdgcn_s_memrealtime();
-        uint32_t old = wg_signal(ctr(a, C_ROUTER));
-        t_x1 = __builtin_amdgcn_s_memrealtime();
-        if (old == (uint32_t)(a.n_router - 1)) {
-            if (threadIdx.x < 64) wave_topk<true>(a.logits, a.E, K, a.ids, a.w, a.hits, a.status, threadIdx.x);
-            t_x2 = __builtin_amdgcn_s_memrealtime();
-            wg_flag(ctr(a, C_TOPK));
+        const uint32_t gsize = (uint32_t)min(RGROUP, a.n_router - g * RGROUP);
+        if (wg_signal(ctr(a, C_RGROUP + g)) == gsize - 1) {
+            t_x1 = __builtin_amdgcn_s_memrealtime();
+            if (wg_signal(ctr(a, C_RTOP)) == (uint32_t)(a.n_rgroups - 1)) {
+                if (threadIdx.x < 64) wave_topk<true>(a.logits, a.E, K, a.ids, a.w, a.hits, a.status, threadIdx.x);
+                t_x2 = __builtin_amdgcn_s_memrealtime();
+                wg_flag(ctr(a, C_TOPK));
+            }
         }
     } else if (item < a.it_sdn) {
         // ---- shared expert gate/up + SwiGLU (needs no routing)
         kind = 2;
-        item_gateup<SGUT>(a, a.sh_gate, a.sh_up, a.Is, item - a.it_sgu, a.act + (int64_t)K * a.act_stride, smem);
+        item_gateup<SGUT>(a, a.sh_gate, a.sh_up, a.Is, item - a.it_sgu, a.tpw_sgu, a.act + (int64_t)K * a.act_stride,
+                          smem);
         t_work = __builtin_amdgcn_s_memrealtime();
         wg_post(ctr(a, C_GU + K));
     } else if (item >= a.it_gu && item < a.it_dn) {
-        // ---- routed gate/up + SwiGLU
+        // ---- routed gate/up + SwiGLU.  The item finds its slot's expert
+        // itself (slot + 1 picks over the logits), so it does not wait for the
+        // whole top-K; the slot's first item publishes the id for the down items.
+        // (the last slot first: its pick takes the most passes)
         const int j = item - a.it_gu;
-        const int slot = j / a.n_gu_slot, jj = j % a.n_gu_slot;
-        wg_wait(ctr(a, C_TOPK), 1u, a.status);
+        const int slot = K - 1 - j / a.n_gu_slot, jj = j % a.n_gu_slot;
+        int e;
+        float v = 0.0f;
+        if (a.forced) {
+            wg_wait(ctr(a, C_TOPK), 1u, a.status);
+            e = gld<true>(a.ids + slot);
+        } else {
+            wg_wait(ctr(a, C_RTOP), (uint32_t)a.n_rgroups, a.status);
+            e = wave_pick(a.logits, a.E, slot, threadIdx.x & 63, v);
+        }
         t_ready = __builtin_amdgcn_s_memrealtime();
         kind = 3;
-        const int e = gld<true>(a.ids + slot);
-        item_gateup<GUT>(a, routed(a.gate, a.gstride, e, a.E), routed(a.up, a.ustride, e, a.E), a.I, jj,
+        if (jj == 0 && threadIdx.x == 0) {
+            gst<true>((int32_t*)ctr(a, C_SLOTEID) + slot, (int32_t)e);
+            gst<true>((float*)ctr(a, C_SLOTEID) + MAX_TOPK + slot, v);
+        }
+        item_gateup<GUT>(a, routed(a.gate, a.gstride, e, a.E), routed(a.up, a.ustride, e, a.E), a.I, jj, a.tpw_gu,
                          a.act + (int64_t)slot * a.act_stride, smem);
         t_work = __builtin_amdgcn_s_memrealtime();
         wg_post(ctr(a, C_GU + slot));
@@ -181,25 +201,42 @@ __global__ __launch_bounds__(256) void k_decode_step(DecodeArgs a) {
         kind = 4;
         const float* act = a.act + (int64_t)slot * a.act_stride;
         float* y = a.ypart + (int64_t)slot * a.H;
-        if (slot == K) item_down<SDT>(a, a.sh_down, a.Is, range, act, y, smem);
-        else item_down<DT>(a, routed(a.down, a.dstride, gld<true>(a.ids + slot), a.E), a.I, range, act, y, smem);
+        if (slot == K) {
+            // the shared-expert gate multiplies the shared rows here (the
+            // same product the combine would form)
+            __shared__ float s_gate;
+            const bool gated = a.sh_gate_inp != nullptr;
+            if (gated) {
+                wg_wait(ctr(a, C_AUX), 1u, a.status);
+                if (threadIdx.x == 0) s_gate = gld<true>(a.shgate);
+                __syncthreads();
+            }
+            item_down<SDT>(a, a.sh_down, a.Is, range, act, y, smem, gated ? &s_gate : nullptr);
+        }
+        else item_down<DT>(a, routed(a.down, a.dstride, gld<true>((const int32_t*)ctr(a, C_SLOTEID) + slot), a.E),
+                           a.I, range, act, y, smem);
         t_work = __builtin_amdgcn_s_memrealtime();
         uint32_t old = wg_signal(ctr(a, C_RANGE + range));
         if (old == (uint32_t)(K1 - 1)) {
             // out[h] = sum_k w_k y_k[h] (k order, invalid ids skipped) + gate * y_shared[h]
             kind |= 8;
-            __shared__ float s_w[MAX_TOPK + 1];
+            __shared__ float s_w[MAX_TOPK];
             __shared__ int s_valid[MAX_TOPK];
-            if (a.has_shared && a.sh_gate_inp) wg_wait(ctr(a, C_AUX), 1u, a.status);
             if ((int)threadIdx.x < K) {
-                const int e = gld<true>(a.ids + threadIdx.x);
-                const float wk = gld<true>(a.w + threadIdx.x);
-                s_valid[threadIdx.x] = (e >= 0 && e < a.E) ? 1 : 0;
-                s_w[threadIdx.x] = (e >= 0 && e < a.E) ? wk : 0.0f;
-            }
-            if (threadIdx.x == 0) {
-                const float sg = gld<true>(a.shgate);
-                s_w[MAX_TOPK] = (a.has_shared && a.sh_gate_inp) ? sg : 1.0f;
+                const int k = threadIdx.x;
+                const int e = gld<true>((const int32_t*)ctr(a, C_SLOTEID) + k);
+                float wk;
+                if (a.forced) wk = gld<true>(a.w + k);
+                else {
+                    // the softmax weight from the K published pick logits
+                    float v[MAX_TOPK];
+#pragma unroll
+                    for (int i = 0; i < MAX_TOPK; i++)      // clamped, unconditional: loads in flight together
+                        v[i] = gld<true>((const float*)ctr(a, C_SLOTEID) + MAX_TOPK + min(i, K - 1));
+                    wk = pick_weight(v, K, k);
+                }
+                s_valid[k] = (e >= 0 && e < a.E) ? 1 : 0;
+                s_w[k] = (e >= 0 && e < a.E) ? wk : 0.0f;
             }
             __syncthreads();
             const int h0 = range * a.rows_dn_item, h1 = min(a.H, h0 + a.rows_dn_item);
@@ -212,20 +249,17 @@ __global__ __launch_bounds__(256) void k_decode_step(DecodeArgs a) {
 #pragma unroll
                 for (int k = 0; k < MAX_TOPK; k++)
                     if (k < K && s_valid[k]) acc = fmaf(s_w[k], yv[k], acc);
-                if (a.has_shared) {
-                    float ys = yv[K];
-                    if (a.sh_gate_inp) ys *= s_w[MAX_TOPK];
-                    acc = acc + ys;
-                }
+                if (a.has_shared) acc = acc + yv[K];            // gate already applied
                 a.out[h] = acc;
             }
             // The last combined range ends the step: every other item has
             // already made its last counter access (each one feeds a range,
-            // and item 0 was awaited above or feeds nothing that is read, in
-            // which case it is awaited here), so the counters go back to zero.
-            if (!(a.has_shared && a.sh_gate_inp)) wg_wait(ctr(a, C_AUX), 1u, a.status);
+            // and item 0 and the trace writer are awaited here), so the
+            // counters go back to zero.
             uint32_t done = wg_signal(ctr(a, C_COMBINED));
             if (done == (uint32_t)(a.n_dn_slot - 1)) {
+                wg_wait(ctr(a, C_TOPK), 1u, a.status);
+                wg_wait(ctr(a, C_AUX), 1u, a.status);
                 for (int i = threadIdx.x; i < C_TOTAL; i += 256) st_relaxed(a.ctr + (int64_t)i * CTR_STRIDE, 0u);
             }
         }

@@ -376,10 +376,6 @@ template <int CTRL, int ROW_MASK = 0xF> WM_DEV float dpp_f32(float v) {
 template <int CTRL> WM_DEV uint64_t dpp_u64(uint64_t v) {
     return ((uint64_t)dpp_u32<CTRL>((uint32_t)(v >> 32)) << 32) | dpp_u32<CTRL>((uint32_t)v);
 }
-WM_DEV uint64_t readlane_u64(uint64_t v, int lane) {
-    return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), lane) << 32) |
-           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
-}
 
 // Sum over groups of `lpr` consecutive lanes (lpr a power of two <= 64), with
 // DPP moves; the sum is complete in the group's last lane (in every lane of
@@ -394,33 +390,33 @@ WM_DEV float row_reduce(float v, int lpr) {
     return v;
 }
 
-// Maximum of a 32-bit value over the wave (all 64 lanes active), uniform result.
-WM_DEV uint32_t wave_max_u32(uint32_t v) {
-    v = max(v, dpp_u32<DPP_XOR1>(v));
-    v = max(v, dpp_u32<DPP_XOR2>(v));
-    v = max(v, dpp_u32<DPP_HALF_MIRROR>(v));
-    v = max(v, dpp_u32<DPP_MIRROR>(v));
-    // every lane of a row of 16 now holds the row's maximum
-    uint32_t m = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
-    m = max(m, (uint32_t)__builtin_amdgcn_readlane((int)v, 16));
-    m = max(m, (uint32_t)__builtin_amdgcn_readlane((int)v, 32));
-    m = max(m, (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
-    return m;
+WM_DEV uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// gfx950 cross-row lane swaps with both operands v: permlane16_swap pairs row
+// r (16 lanes) with row r^1, permlane32_swap lane i with lane i^32; .first
+// and .second of the result are the two members of each pair.
+WM_DEV uint64_t swap_max_u64_rows(uint64_t v) {
+    const uint32_t hi = (uint32_t)(v >> 32), lo = (uint32_t)v;
+    const auto h = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    const auto l = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    return max_u64(((uint64_t)h[0] << 32) | l[0], ((uint64_t)h[1] << 32) | l[1]);
+}
+WM_DEV uint64_t swap_max_u64_halves(uint64_t v) {
+    const uint32_t hi = (uint32_t)(v >> 32), lo = (uint32_t)v;
+    const auto h = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    const auto l = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    return max_u64(((uint64_t)h[0] << 32) | l[0], ((uint64_t)h[1] << 32) | l[1]);
 }
 
-// Maximum of a 64-bit key over the wave (all 64 lanes active), uniform result.
+// Maximum of a 64-bit key over the wave (all 64 lanes active), in every lane:
+// DPP within rows of 16, then the two cross-row swaps; no scalar round trips.
 WM_DEV uint64_t wave_max_u64(uint64_t v) {
-    uint64_t o;
-    o = dpp_u64<DPP_XOR1>(v); v = o > v ? o : v;
-    o = dpp_u64<DPP_XOR2>(v); v = o > v ? o : v;
-    o = dpp_u64<DPP_HALF_MIRROR>(v); v = o > v ? o : v;
-    o = dpp_u64<DPP_MIRROR>(v); v = o > v ? o : v;
-    // every lane of a row of 16 now holds the row's maximum
-    uint64_t m = readlane_u64(v, 0);
-    o = readlane_u64(v, 16); m = o > m ? o : m;
-    o = readlane_u64(v, 32); m = o > m ? o : m;
-    o = readlane_u64(v, 48); m = o > m ? o : m;
-    return m;
+    v = max_u64(v, dpp_u64<DPP_XOR1>(v));
+    v = max_u64(v, dpp_u64<DPP_XOR2>(v));
+    v = max_u64(v, dpp_u64<DPP_HALF_MIRROR>(v));
+    v = max_u64(v, dpp_u64<DPP_MIRROR>(v));
+    v = swap_max_u64_rows(v);
+    return swap_max_u64_halves(v);
 }
 
 // s_waitcnt with vmcnt only (gfx9 encoding: vmcnt[3:0] | vmcnt[5:4] << 14,

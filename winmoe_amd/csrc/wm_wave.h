@@ -125,7 +125,8 @@ template <int NI, int S> WM_DEV void wait_tiles(int ahead) {
 // S * tile_buf<T>() bytes.
 template <int T, int S, bool COH>
 WM_DEV void wave_stream(const uint8_t* W, int rows, const Geo& g, int t0, int t1, const float* xsrc, lds8_t* ring,
-                        float* gout, __attribute__((address_space(3))) float* lout, int lrow0, int lane) {
+                        float* gout, __attribute__((address_space(3))) float* lout, int lrow0, int lane,
+                        float gscale = 1.0f, bool scaled = false) {
     constexpr int NI = tile_ni<T>(), BUF = tile_buf<T>();
     const int rig = lane / g.lpr, sub = lane % g.lpr;
     f32x4 xr[16];
@@ -154,7 +155,7 @@ WM_DEV void wave_stream(const uint8_t* W, int rows, const Geo& g, int t0, int t1
         if (t + S < t1) tile_dma<NI>(W, (int64_t)(t + S) * g.tile_bytes, tile_nbytes(g, rows, t + S), lane, ring + s * BUF);
         const int row = t * g.rpt + rig;
         if (sub == g.lpr - 1 && rig < g.rpt && row < rows) {
-            if (gout) gst<COH>(gout + row, p);
+            if (gout) gst<COH>(gout + row, scaled ? p * gscale : p);
             if (lout) lout[row - lrow0] = p;
         }
     }
@@ -200,9 +201,11 @@ WM_DEV void wg_gateup_item(const uint8_t* Wg, const uint8_t* Wu, int rows, int i
     __syncthreads();
 }
 
-// y[row] = W[row] . x over tiles [tb, tb + 4*tpw) (tpw per wave).
+// y[row] = W[row] . x over tiles [tb, tb + 4*tpw) (tpw per wave), times
+// *scale when scale is not null.
 template <int T, bool COH>
-WM_DEV void wg_gemv_item(const uint8_t* W, int rows, int in, int tb, int tpw, const float* x, float* y, uint8_t* lds) {
+WM_DEV void wg_gemv_item(const uint8_t* W, int rows, int in, int tb, int tpw, const float* x, float* y, uint8_t* lds,
+                         const float* scale = nullptr) {
     constexpr int BUF = tile_buf<T>();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const Geo g = geometry(T, in);
@@ -217,7 +220,8 @@ WM_DEV void wg_gemv_item(const uint8_t* W, int rows, int in, int tb, int tpw, co
         }
         return;
     }
-    wave_stream<T, RING_S, COH>(W, rows, g, t0, t1, x, (lds8_t*)(lds + wave * RING_S * BUF), y, nullptr, 0, lane);
+    wave_stream<T, RING_S, COH>(W, rows, g, t0, t1, x, (lds8_t*)(lds + wave * RING_S * BUF), y, nullptr, 0, lane,
+                                scale ? *scale : 1.0f, scale != nullptr);
 }
 
 // ---------------------------------------------------------------- router
@@ -305,91 +309,126 @@ WM_DEV uint64_t topk_key(float v, int e) {
     return ((uint64_t)u << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)e);
 }
 
-// Per-lane sort of N keys, descending (bitonic network, unrolled).
-template <int N> WM_DEV void sort_desc(uint64_t (&k)[N]) {
+// Maximum of N keys of one lane (tree).
+template <int N> WM_DEV uint64_t lane_max(const uint64_t (&k)[N]) {
+    uint64_t m[N];
 #pragma unroll
-    for (int size = 2; size <= N; size <<= 1)
+    for (int i = 0; i < N; i++) m[i] = k[i];
 #pragma unroll
-        for (int stride = size >> 1; stride > 0; stride >>= 1)
+    for (int w = N / 2; w >= 1; w >>= 1)
 #pragma unroll
-            for (int i = 0; i < N; i++) {
-                const int l = i ^ stride;
-                if (l > i) {
-                    const bool desc = (i & size) == 0;
-                    const uint64_t a = k[i], b = k[l];
-                    const bool swap = desc ? (a < b) : (a > b);
-                    k[i] = swap ? b : a;
-                    k[l] = swap ? a : b;
-                }
-            }
+        for (int i = 0; i < w; i++) m[i] = max_u64(m[i], m[i + w]);
+    return m[0];
 }
 
-// One wave: top-K of E <= 1024 logits and the softmax over the picks
-// (transformer.h:142-149); lane 0 writes ids / w, bumps the hit counters
-// and reports degenerate / non-finite routing in *status.  Each lane sorts
-// its keys once; a pass then takes the wave maximum of the lane heads (value
-// bits first, the index only on a value tie) and the winning lane drops its head.
+// K-pass arg-max state of one wave over E <= 64 * MAXV logits: every lane
+// keeps the order keys of logits lane, lane + 64, ... and the maximum of
+// them; a pick takes the wave maximum of those, and the lane that owned it
+// clears it and recomputes its maximum.
+template <int MAXV> struct Picker {
+    uint64_t key[MAXV];
+    uint64_t head;
+    float v0;                                        // logits[0]: the value of a degenerate pick (index 0)
+
+    template <bool COH> WM_DEV void init(const float* logits, int E, int lane) {
+        float lv[MAXV];
+        // all loads unconditional (index clamped) so they are in flight together
+#pragma unroll
+        for (int i = 0; i < MAXV; i++) lv[i] = gld<COH>(logits + min(lane + 64 * i, E - 1));
+        v0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lv[0]), 0));
+#pragma unroll
+        for (int i = 0; i < MAXV; i++) key[i] = (lane + 64 * i) < E ? topk_key(lv[i], lane + 64 * i) : 0ull;
+        head = lane_max<MAXV>(key);
+    }
+    // Next pick: its key (0 = degenerate, nothing valid left) in every lane.
+    WM_DEV uint64_t next() {
+        const uint64_t best = wave_max_u64(head);
+        if (best != 0ull && head == best) {
+#pragma unroll
+            for (int i = 0; i < MAXV; i++) key[i] = key[i] == best ? 0ull : key[i];
+            head = lane_max<MAXV>(key);
+        }
+        return best;
+    }
+    WM_DEV static int id_of(uint64_t best) { return best ? (int)(0xFFFFFFFFu - (uint32_t)best) : 0; }
+    // the value back from its order key (-0 comes back as +0, which changes
+    // no difference or exponential of the softmax)
+    WM_DEV float value_of(uint64_t best) const {
+        if (!best) return v0;
+        const uint32_t u = (uint32_t)(best >> 32);
+        return __builtin_bit_cast(float, (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
+    }
+};
+
+// One wave: top-K (K <= 16) of E <= 64 * MAXV logits and the softmax over
+// the picks (transformer.h:142-149).  Lane k keeps pick k, writes ids[k] /
+// w[k] and bumps the pick's hit counter; degenerate / non-finite routing is
+// reported in *status.  The softmax matches the sequential form: wmax starts
+// from pick 0 and takes later picks that compare greater, the exponentials
+// are summed in k order.
 template <int MAXV, bool COH>
 WM_DEV void wave_topk_n(const float* logits, int E, int K, int32_t* ids, float* w, uint32_t* hits, int32_t* status,
                         int lane) {
-    uint64_t key[MAXV];
-    float lv[MAXV];
-    // all loads unconditional (index clamped) so they are in flight together
-#pragma unroll
-    for (int i = 0; i < MAXV; i++) lv[i] = gld<COH>(logits + min(lane + 64 * i, E - 1));
-    const float v0 = lv[0];                           // logits[0] (lane 0): the value of a degenerate pick
-#pragma unroll
-    for (int i = 0; i < MAXV; i++) {
-        int e = lane + 64 * i;
-        key[i] = e < E ? topk_key(lv[i], e) : 0ull;
-    }
-    sort_desc<MAXV>(key);
-    int my_id[16];
-    float my_v[16];
+    Picker<MAXV> pk;
+    pk.template init<COH>(logits, E, lane);
+    int my_e = 0;
+    float my_v = 0.0f;
     bool degenerate = false;
     for (int k = 0; k < K; k++) {
-        const uint32_t hi = (uint32_t)(key[0] >> 32), lo = (uint32_t)key[0];
-        const uint32_t vmax = wave_max_u32(hi);
-        const uint64_t tie = __builtin_amdgcn_ballot_w64(hi == vmax);
-        uint32_t lmax;
-        if (__builtin_popcountll(tie) == 1) lmax = (uint32_t)__builtin_amdgcn_readlane((int)lo, (int)__builtin_ctzll(tie));
-        else lmax = wave_max_u32(hi == vmax ? lo : 0u);
-        const uint64_t best = ((uint64_t)vmax << 32) | lmax;
-        int e = 0;
-        float v = v0;
-        if (best == 0ull) degenerate = true;
-        else {
-            e = (int)(0xFFFFFFFFu - lmax);
-            if ((e & 63) == lane) {
-#pragma unroll
-                for (int i = 0; i + 1 < MAXV; i++) key[i] = key[i + 1];
-                key[MAXV - 1] = 0ull;
-            }
-            // the value back from its order key (-0 comes back as +0, which
-            // changes no difference or exponential below)
-            v = __builtin_bit_cast(float, (vmax & 0x80000000u) ? (vmax & 0x7FFFFFFFu) : ~vmax);
-        }
-        my_id[k] = e;
-        my_v[k] = v;
+        const uint64_t best = pk.next();
+        degenerate = degenerate || best == 0ull;
+        if (lane == k) { my_e = Picker<MAXV>::id_of(best); my_v = pk.value_of(best); }
+    }
+    const bool mine = lane < K;
+    float wmax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_v), 0));
+    for (int k = 1; k < K; k++) {
+        const float vk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_v), k));
+        if (vk > wmax) wmax = vk;
+    }
+    const float ex = mine ? expf(my_v - wmax) : 0.0f;
+    float wsum = 0.0f;
+    for (int k = 0; k < K; k++) wsum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), k));
+    const float wk = wsum > 0.0f ? ex / wsum : ex;
+    const bool nonfinite = __builtin_amdgcn_ballot_w64(mine && !isfinite(wk)) != 0ull;
+    if (mine) {
+        gst<COH>(ids + lane, (int32_t)my_e);
+        gst<COH>(w + lane, wk);
+        if (hits) atomicAdd(hits + my_e, 1u);
     }
     if (lane == 0) {
-        float wl[16];
-        for (int k = 0; k < K; k++) wl[k] = my_v[k];
-        float wmax = wl[0];
-        for (int k = 1; k < K; k++) if (wl[k] > wmax) wmax = wl[k];
-        float wsum = 0.0f;
-        for (int k = 0; k < K; k++) { wl[k] = expf(wl[k] - wmax); wsum += wl[k]; }
-        if (wsum > 0.0f) for (int k = 0; k < K; k++) wl[k] /= wsum;
-        bool nonfinite = false;
-        for (int k = 0; k < K; k++) {
-            gst<COH>(ids + k, (int32_t)my_id[k]);
-            gst<COH>(w + k, wl[k]);
-            nonfinite = nonfinite || !isfinite(wl[k]);
-            if (hits) atomicAdd(hits + my_id[k], 1u);
-        }
         int st = (degenerate ? WM_STATUS_DEGENERATE_ROUTING : 0) | (nonfinite ? WM_STATUS_NONFINITE_WEIGHT : 0);
         if (st && status) atomicOr(status, st);
     }
+}
+
+// Expert id and logit of routing slot `slot` (pick slot + 1 of the K-pass
+// arg-max), computed by one wave from the logits (ordinary loads).
+WM_DEV int wave_pick(const float* logits, int E, int slot, int lane, float& value) {
+    uint64_t best = 0ull;
+    if (E <= 512) {
+        Picker<8> pk;
+        pk.template init<false>(logits, E, lane);
+        for (int k = 0; k <= slot; k++) best = pk.next();
+        value = pk.value_of(best);
+    } else {
+        Picker<16> pk;
+        pk.template init<false>(logits, E, lane);
+        for (int k = 0; k <= slot; k++) best = pk.next();
+        value = pk.value_of(best);
+    }
+    return Picker<8>::id_of(best);
+}
+
+// Softmax weight of pick k from the K pick logits, exactly as wave_topk_n
+// computes it (wmax from pick 0 raised by later picks that compare greater,
+// exponentials summed in k order).
+WM_DEV float pick_weight(const float* v, int K, int k) {
+    float wmax = v[0];
+    for (int i = 1; i < K; i++) if (v[i] > wmax) wmax = v[i];
+    float wsum = 0.0f;
+    for (int i = 0; i < K; i++) wsum += expf(v[i] - wmax);
+    const float ex = expf(v[k] - wmax);
+    return wsum > 0.0f ? ex / wsum : ex;
 }
 
 template <bool COH = false>
