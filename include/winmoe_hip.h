@@ -135,7 +135,8 @@ int wm_workspace_reset(const wm_layer_desc* d, int max_tokens, void* ws, int64_t
  * met, main work done, end (device clock ticks, wm_device_clock_khz per ms),
  * kind | HW_ID << 8 | XCC_ID << 40, then for router items the time their
  * counter increment returned and, for the one that ran top-K, the time top-K
- * finished (0 otherwise), and a zero word; kind 0 = shared gate / forced
+ * finished (0 otherwise), and the time its weight rows had landed in LDS
+ * (router items only); kind 0 = shared gate / forced
  * routing, 1 = router, 2 = shared gate/up, 3 = routed gate/up, 4 = down (+8
  * when it also combined). */
 int wm_workspace_timeline(const wm_layer_desc* d, int max_tokens, int64_t* offset, int64_t* capacity);

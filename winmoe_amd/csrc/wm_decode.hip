@@ -123,7 +123,7 @@ __global__ __launch_bounds__(256) void k_decode_step(DecodeArgs a) {
     // are bounded in any case).
     const int item = (int)blockIdx.x;
     const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
-    uint64_t t_ready = t_start, t_work = 0, t_x1 = 0, t_x2 = 0;
+    uint64_t t_ready = t_start, t_work = 0, t_x1 = 0, t_x2 = 0, t_x3 = 0;
     int kind = 0;
     const int K = a.K, K1 = a.K + (a.has_shared ? 1 : 0);
 
@@ -147,7 +147,8 @@ __global__ __launch_bounds__(256) void k_decode_step(DecodeArgs a) {
         const int j = item - a.it_router;
         const int r0 = j * a.rr, g = j / RGROUP;
         kind = 1;
-        wg_router_rows<true>(a.x, a.router, a.H, r0, min(a.rr, a.E - r0), a.router_region, (lds8_t*)smem, a.logits);
+        wg_router_rows<true>(a.x, a.router, a.H, r0, min(a.rr, a.E - r0), a.router_region, (lds8_t*)smem, a.logits,
+                             &t_x3);
         t_work = __builtin_amdgcn_s_memrealtime();
         const uint32_t gsize = (uint32_t)min(RGROUP, a.n_router - g * RGROUP);
         if (wg_signal(ctr(a, C_RGROUP + g)) == gsize - 1) {
@@ -276,7 +277,7 @@ __global__ __launch_bounds__(256) void k_decode_step(DecodeArgs a) {
         r[4] = (uint64_t)kind | (hw << 8) | (xcc << 40);
         r[5] = t_x1;
         r[6] = t_x2;
-        r[7] = 0;
+        r[7] = t_x3;
     }
 }
 

@@ -245,7 +245,7 @@ WM_HD int router_rows_per_wg(int H, bool aligned) {
 // of row r.  Called by all 256 threads.
 template <bool COH>
 WM_DEV void wg_router_rows(const float* __restrict__ x, const float* __restrict__ W, int H, int r0, int nr, int region,
-                           lds8_t* lds, float* __restrict__ logits) {
+                           lds8_t* lds, float* __restrict__ logits, uint64_t* t_landed = nullptr) {
     typedef __attribute__((address_space(3))) float lf;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t nbytes = (int64_t)H * 4;
@@ -266,6 +266,7 @@ WM_DEV void wg_router_rows(const float* __restrict__ x, const float* __restrict_
     }
     WM_WAIT_VMCNT(0);
     __syncthreads();
+    if (t_landed) *t_landed = __builtin_amdgcn_s_memrealtime();
     if (wave < nr && lane < 16) {
         const lf* xr = (const lf*)(lds + (((uintptr_t)x) & 15));
         const float* wsrc = W + (int64_t)(r0 + wave) * H;
