@@ -56,6 +56,27 @@ def step_bytes(cfg) -> int:
     return b * cfg.n_layers
 
 
+def prefill_bytes(cfg, ids) -> int:
+    """Algorithmic bytes of one prefill batch: every expert touched once,
+    the shared expert, x (bf16) in, out (fp32) out, the router when it routes."""
+    uniq = len(np.unique(ids[(ids >= 0) & (ids < cfg.E)]))
+    b = uniq * cfg.expert_bytes() + cfg.shared_bytes() + cfg.tokens * cfg.H * (2 + 4)
+    if cfg.routing == "router":
+        b += cfg.E * cfg.H * 4
+    return b
+
+
+def prefill_gateup_bytes(cfg, ids) -> int:
+    """Algorithmic bytes of the prefill gate/up launch: gate and up of every
+    expert touched (and the shared one), x rows read once, SwiGLU rows written."""
+    from winmoe_amd.moe import matrix_bytes
+    gt, ut, _ = cfg.types
+    uniq = len(np.unique(ids[(ids >= 0) & (ids < cfg.E)]))
+    b = uniq * (matrix_bytes(gt, cfg.I, cfg.H) + matrix_bytes(ut, cfg.I, cfg.H))
+    b += cfg.tokens * cfg.H * 2 + ids.size * cfg.I * 4
+    return b
+
+
 def gateup_bytes(cfg) -> int:
     """Algorithmic bytes of one launch of the gate/up + SwiGLU kernel (weights + act out)."""
     from winmoe_amd.moe import matrix_bytes
@@ -130,7 +151,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2048)
     ap.add_argument("--warmup", type=int, default=64)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--multi-kernel", action="store_true",
@@ -169,7 +190,16 @@ def main():
     torch.cuda.synchronize()
     log(f"built in {time.perf_counter() - t_build:.1f} s")
 
+    prefill = cfg.x_dtype == "bf16" and cfg.tokens > 1     # one step = the whole batch through the layer
+
     def step(i):
+        if prefill:
+            for li, sl in enumerate(layers):
+                if routes is None:
+                    sl.layer.prefill(X, out=outs)
+                else:
+                    sl.layer.prefill_forced(X, routes[li][2], routes[li][3], out=outs)
+            return
         t = i % cfg.tokens
         x = X[t]
         for li, sl in enumerate(layers):
@@ -222,13 +252,23 @@ def main():
         if cnt_arr[p]:
             phases[L.wm_profile_phase_name(p).decode()] = {"avg_us": round(1000.0 * ms_arr[p] / cnt_arr[p], 3),
                                                            "launches": int(cnt_arr[p])}
-    st = max(sl.layer.status() for sl in layers)
+    st = max(sl.layer.prefill_status() if prefill else sl.layer.status() for sl in layers)
     ms_per_step = ev_ms / args.steps
-    tokens_per_s = args.steps / (ev_ms / 1000.0)
-    sbytes = step_bytes(cfg)
+    tokens_per_s = args.steps * (cfg.tokens if prefill else 1) / (ev_ms / 1000.0)
+    sbytes = prefill_bytes(cfg, routes[0][0]) * cfg.n_layers if prefill else step_bytes(cfg)
     step_gbps = sbytes / (ms_per_step * 1e-3) / 1e9
     roofline = None
-    if not args.multi_kernel:
+    if prefill and "gate_up_swiglu" in phases:
+        gu = phases["gate_up_swiglu"]
+        per_launch = prefill_gateup_bytes(cfg, routes[0][0])
+        ach = per_launch / (gu["avg_us"] * 1e-6) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                    "frac": round(ach / PEAK_HBM_GBPS, 4), "traffic": None,
+                    "kernel": "k_pf_gateup (prefill gate+up+SwiGLU, bf16 MFMA over Q8_0 blocks)",
+                    "bytes_per_launch": per_launch, "avg_launch_us": round(gu["avg_us"], 2)}
+    elif prefill:
+        pass
+    elif not args.multi_kernel:
         # one fused launch per layer per token moves the whole step's bytes;
         # its average duration is the timed region's event time over the
         # launches in it (they run back to back on this stream)
@@ -256,8 +296,9 @@ def main():
         "config": {"workload": cfg.name, "experts": cfg.E, "top_k": cfg.K, "hidden": cfg.H, "inter": cfg.I,
                    "types": [wm.TYPE_NAMES[t] for t in cfg.types],
                    "shared_types": [wm.TYPE_NAMES[t] for t in cfg.shared_types] if cfg.shared_types else None,
-                   "layers": cfg.n_layers, "routing": cfg.routing, "batch": 1, "distinct_tokens": cfg.tokens,
-                   "path": "multi-kernel" if args.multi_kernel else "fused"},
+                   "layers": cfg.n_layers, "routing": cfg.routing, "batch": cfg.tokens if prefill else 1,
+                   "distinct_tokens": cfg.tokens,
+                   "path": "prefill" if prefill else ("multi-kernel" if args.multi_kernel else "fused")},
         "roofline": roofline,
         "step_algorithmic_bytes": sbytes, "step_GBps": round(step_gbps, 1),
         "step_hbm_frac": round(step_gbps / PEAK_HBM_GBPS, 4),

@@ -163,11 +163,30 @@ int wm_moe_decode(const wm_layer_desc* d, const float* x, float* out, void* ws, 
 int wm_moe_decode_forced(const wm_layer_desc* d, const float* x, const int32_t* ids, const float* w,
                          float* out, void* ws, int64_t ws_bytes, int max_tokens, int step, void* stream);
 
-/* Batched prefill of T tokens: x bf16 [T][H], out fp32 [T][H].  Routes every
- * token, sorts (token, slot) pairs by expert in the workspace, runs grouped
- * expert GEMMs on MFMA and a weighted gather-combine.  T <= max_tokens. */
+/* Batched prefill of T tokens through the layer: x bf16 [T][H] -> out fp32
+ * [T][H] (moe_out of every token).  The reference has no batched path: its
+ * prompt tokens go one at a time through the decode loop
+ * (winmoe_inference.c:1079,2286-2288), each with router_topk
+ * (transformer.h:107-152) and the expert loop (:1684-2027); the result per
+ * token is the same mathematics.  Here all T tokens are routed, the (token,
+ * slot) pairs are grouped by expert in the workspace, each expert's matrices
+ * are streamed once for all of its tokens on MFMA, and a weighted combine
+ * gathers the outputs.  T <= max_tokens; the workspace (one per layer and
+ * stream) holds wm_prefill_workspace_size(d, max_tokens) bytes, 256-byte
+ * aligned.  Expert matrices (routed and shared) must be Q8_0 and H, I,
+ * inter_shared multiples of 128; otherwise WM_EINVAL. */
+int64_t wm_prefill_workspace_size(const wm_layer_desc* d, int max_tokens);
 int wm_moe_prefill(const wm_layer_desc* d, const uint16_t* x_bf16, int T, float* out, void* ws,
                    int64_t ws_bytes, int max_tokens, void* stream);
+/* Same with routing supplied by the caller: ids int32 [T][K], w fp32 [T][K]
+ * (device).  Ids outside [0, E) are skipped and set WM_STATUS_BAD_EXPERT_ID. */
+int wm_moe_prefill_forced(const wm_layer_desc* d, const uint16_t* x_bf16, int T, const int32_t* ids,
+                          const float* w, float* out, void* ws, int64_t ws_bytes, int max_tokens, void* stream);
+/* Byte offsets in a prefill workspace of the last call's routing: ids int32
+ * [T][K], weights fp32 [T][K], per-expert pick counts uint32 [E] (cumulative
+ * over calls until wm_workspace_reset-style clearing by the caller). */
+int wm_prefill_workspace_routing(const wm_layer_desc* d, int max_tokens, int64_t* ids_off, int64_t* w_off,
+                                 int64_t* hits_off);
 
 /* One expert FFN: out = down(SwiGLU(gate x, up x)) (gpu_expert_ffn_fused's
  * maths on device pointers, any supported types). */

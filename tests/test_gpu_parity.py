@@ -336,3 +336,81 @@ def test_fused_step_matches_multi_kernel(wm, name, E, tokens):
     assert np.array_equal(host(wa[:tokens]).view(np.uint32), host(wb[:tokens]).view(np.uint32))
     assert np.array_equal(host(sl.layer.hits()), host(multi.hits()))
     assert sl.layer.status() == 0 and multi.status() == 0
+
+
+# ------------------------------------------------------------------ prefill
+
+def _pf_cfg(E, K, H, I, shared=False, routing="router"):
+    from winmoe_amd import synth
+    return synth.LayerConfig(f"pf_e{E}_k{K}_h{H}_i{I}", E=E, K=K, H=H, I=I, types=(Q8_0, Q8_0, Q8_0),
+                             shared_types=(Q8_0, Q8_0, Q8_0) if shared else None, shared_inter=I if shared else 0,
+                             shared_gate_inp=shared, tokens=1, routing=routing, x_dtype="bf16", seed=3)
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_prefill_router_matches_oracle(wm, orc, shared):
+    """Batched prefill routed by the router == the oracle token by token: ids
+    exact, weights within 2 ulp, outputs within the layer bar."""
+    from winmoe_amd import synth
+    cfg = _pf_cfg(E=48, K=4, H=1024, I=512, shared=shared)
+    T = 40
+    sl = synth.build_layer(cfg, max_tokens=T)
+    X = synth.make_hidden(cfg, tokens=T)
+    case(f"prefill router shared={shared} T={T}")
+    out = host(sl.layer.prefill(X))
+    ids, w = (host(a) for a in sl.layer.prefill_routing(T))
+    for t in range(T):
+        oid, ow, ref = oracle_token(orc, sl, host(X[t].float()))
+        assert ids[t].tolist() == oid.tolist(), t
+        assert ulp_diff(w[t], ow).max() <= 2, t
+        assert rel_l2(out[t], ref) <= LAYER_TOL, (t, rel_l2(out[t], ref))
+    assert sl.layer.prefill_status() == 0
+
+
+def test_prefill_forced_multi_pass_and_bad_ids(wm, orc):
+    """Caller routing: one expert used by every token (more than one 64-pair
+    pass), one invalid id (skipped, reported)."""
+    from winmoe_amd import synth
+    cfg = _pf_cfg(E=16, K=4, H=512, I=256, routing="zipf")
+    T = 80
+    sl = synth.build_layer(cfg, max_tokens=T)
+    X = synth.make_hidden(cfg, tokens=T)
+    rng = np.random.default_rng(5)
+    ids = np.zeros((T, 4), np.int32)
+    for t in range(T):
+        ids[t, 1:] = rng.choice(np.arange(1, 16), 3, replace=False)
+    ids[7, 2] = 99                                        # invalid
+    w = rng.random((T, 4)).astype(np.float32)
+    case(f"prefill forced T={T}")
+    out = host(sl.layer.prefill_forced(X, dev(ids), dev(w)))
+    for t in range(T):
+        ok = (ids[t] >= 0) & (ids[t] < 16)
+        _, _, ref = oracle_token(orc, sl, host(X[t].float()), ids=ids[t][ok], w=w[t][ok])
+        assert rel_l2(out[t], ref) <= LAYER_TOL, (t, rel_l2(out[t], ref))
+    assert sl.layer.prefill_status() == 2                 # WM_STATUS_BAD_EXPERT_ID
+
+
+def test_prefill_c5_full(wm, orc):
+    """The 512-token, 512-expert, top-10 Q8_0 prefill with Zipf routing: a
+    sample of tokens against the oracle, every token against the decode path
+    with the same routing (a different route through the arithmetic)."""
+    from winmoe_amd import synth
+    cfg = synth.CONFIGS["c5"]
+    T = cfg.tokens
+    sl = synth.build_layer(cfg, max_tokens=T)
+    X = synth.make_hidden(cfg)
+    ids, w = synth.forced_routes(cfg)
+    case("prefill c5 full")
+    out = host(sl.layer.prefill_forced(X, dev(ids), dev(w)))
+    assert np.isfinite(out).all()
+    for t in (0, 1, 255, T - 1):
+        case(f"prefill c5 oracle token={t}")
+        _, _, ref = oracle_token(orc, sl, host(X[t].float()), ids=ids[t], w=w[t])
+        assert rel_l2(out[t], ref) <= LAYER_TOL, (t, rel_l2(out[t], ref))
+    case("prefill c5 vs decode, all tokens")
+    worst = 0.0
+    for t in range(T):
+        od = host(sl.layer.decode_forced(X[t].float(), dev(ids[t]), dev(w[t])))
+        worst = max(worst, rel_l2(out[t], od))
+    assert worst <= 1e-4, worst
+    assert sl.layer.prefill_status() == 0

@@ -66,7 +66,12 @@ SIGNATURES = {
     "wm_moe_decode": (C.c_int, [C.POINTER(LayerDesc), _vp, _vp, _vp, _i64, C.c_int, C.c_int, _vp]),
     "wm_moe_decode_forced": (C.c_int, [C.POINTER(LayerDesc), _vp, _vp, _vp, _vp, _vp, _i64, C.c_int, C.c_int,
                                        _vp]),
+    "wm_prefill_workspace_size": (_i64, [C.POINTER(LayerDesc), C.c_int]),
     "wm_moe_prefill": (C.c_int, [C.POINTER(LayerDesc), _vp, C.c_int, _vp, _vp, _i64, C.c_int, _vp]),
+    "wm_moe_prefill_forced": (C.c_int, [C.POINTER(LayerDesc), _vp, C.c_int, _vp, _vp, _vp, _vp, _i64, C.c_int,
+                                        _vp]),
+    "wm_prefill_workspace_routing": (C.c_int, [C.POINTER(LayerDesc), C.c_int, C.POINTER(_i64), C.POINTER(_i64),
+                                               C.POINTER(_i64)]),
     "wm_expert_ffn": (C.c_int, [_vp, C.c_int, _vp, C.c_int, _vp, C.c_int, _vp, C.c_int, C.c_int, _vp, _vp, _i64,
                                 _vp]),
     "wm_expert_workspace_size": (_i64, [C.c_int, C.c_int]),

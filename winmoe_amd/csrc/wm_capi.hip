@@ -13,6 +13,7 @@
 #include "../../include/winmoe_hip.h"
 #include "wm_decode.h"
 #include "wm_launch.h"
+#include "wm_prefill.h"
 #include "wm_quant.h"
 #include "wm_wave.h"
 
@@ -605,11 +606,109 @@ extern "C" int wm_expert_ffn(const void* gate, int gt, const void* up, int ut, c
     return WM_OK;
 }
 
+// ------------------------------------------------------------------ prefill
+
+struct PfLayout {
+    int64_t status, ids, w, logits, hits, offsets, sorted, sg, act, y, total;
+    int64_t act_stride;
+};
+
+static PfLayout pf_layout(const wm_layer_desc* d, int max_tokens) {
+    PfLayout L = {};
+    const int64_t T = max_tokens, K = d->top_k, E = d->n_experts, H = d->hidden;
+    const bool sh = has_shared(d);
+    const int64_t Imax = std::max<int64_t>(d->inter, sh ? Ishared(d) : 0);
+    const int64_t pairs = T * K + (sh ? T : 0);
+    int64_t o = 0;
+    L.status = o; o += 256;
+    L.ids = o; o += up256(T * K * 4);
+    L.w = o; o += up256(T * K * 4);
+    L.logits = o; o += up256(T * E * 4);
+    L.hits = o; o += up256(E * 4);
+    L.offsets = o; o += up256((E + 2) * 4);
+    L.sorted = o; o += up256(pairs * 4);
+    L.sg = o; o += up256(T * 4);
+    L.act_stride = Imax;
+    L.act = o; o += up256(pairs * Imax * 4);
+    L.y = o; o += up256(pairs * H * 4);
+    L.total = o;
+    return L;
+}
+
+extern "C" int64_t wm_prefill_workspace_size(const wm_layer_desc* d, int max_tokens) {
+    if (!d || max_tokens <= 0 || d->top_k <= 0 || d->n_experts <= 0 || d->hidden <= 0 || d->inter <= 0) return WM_EINVAL;
+    return pf_layout(d, max_tokens).total;
+}
+
+extern "C" int wm_prefill_workspace_routing(const wm_layer_desc* d, int max_tokens, int64_t* ids_off, int64_t* w_off,
+                                            int64_t* hits_off) {
+    WM_CHECK_ARG(d && max_tokens > 0 && d->top_k > 0 && d->n_experts > 0);
+    PfLayout L = pf_layout(d, max_tokens);
+    if (ids_off) *ids_off = L.ids;
+    if (w_off) *w_off = L.w;
+    if (hits_off) *hits_off = L.hits;
+    return WM_OK;
+}
+
+static int run_prefill(const wm_layer_desc* d, const uint16_t* x, int T, const int32_t* fids, const float* fw,
+                       float* out, void* ws, int64_t ws_bytes, int max_tokens, void* stream) {
+    if (int rc = validate_desc(d, fids == nullptr)) return rc;
+    WM_CHECK_ARG(x && out && ws && al(ws, 256) && al(x, 16) && T > 0 && T <= max_tokens);
+    PfLayout L = pf_layout(d, max_tokens);
+    WM_CHECK_ARG(ws_bytes >= L.total);
+    const bool sh = has_shared(d);
+    const bool q8 = d->gate_type == Q8_0 && d->up_type == Q8_0 && d->down_type == Q8_0 &&
+                    (!sh || (d->sh_gate_type == Q8_0 && d->sh_up_type == Q8_0 && d->sh_down_type == Q8_0));
+    const bool shapes = d->hidden % 128 == 0 && d->inter % 128 == 0 && (!sh || Ishared(d) % 128 == 0);
+    if (!q8 || !shapes) {
+        fprintf(stderr, "winmoe_hip: prefill needs Q8_0 expert matrices and H, I multiples of 128\n");
+        return WM_EINVAL;
+    }
+    if (wm_init()) return WM_ERR;
+    hipStream_t s = S(stream);
+    uint8_t* w8 = (uint8_t*)ws;
+    PrefillArgs a = {};
+    a.H = d->hidden; a.I = d->inter; a.Is = Ishared(d); a.E = d->n_experts; a.K = d->top_k; a.T = T;
+    a.has_shared = sh ? 1 : 0;
+    a.x = x; a.router = d->router;
+    a.gate = (const uint8_t*)d->gate_exps; a.up = (const uint8_t*)d->up_exps; a.down = (const uint8_t*)d->down_exps;
+    a.gstride = d->gate_stride ? d->gate_stride : matrix_bytes(d->gate_type, d->inter, d->hidden);
+    a.ustride = d->up_stride ? d->up_stride : matrix_bytes(d->up_type, d->inter, d->hidden);
+    a.dstride = d->down_stride ? d->down_stride : matrix_bytes(d->down_type, d->hidden, d->inter);
+    a.sh_gate = (const uint8_t*)d->sh_gate; a.sh_up = (const uint8_t*)d->sh_up; a.sh_down = (const uint8_t*)d->sh_down;
+    a.sh_gate_inp = sh ? d->sh_gate_inp : nullptr;
+    a.ids = (int32_t*)(w8 + L.ids); a.w = (float*)(w8 + L.w); a.logits = (float*)(w8 + L.logits);
+    a.hits = (uint32_t*)(w8 + L.hits); a.status = (int32_t*)(w8 + L.status);
+    a.offsets = (int32_t*)(w8 + L.offsets); a.sorted = (int32_t*)(w8 + L.sorted); a.sg = (float*)(w8 + L.sg);
+    a.act = (float*)(w8 + L.act); a.act_stride = L.act_stride; a.y = (float*)(w8 + L.y); a.out = out;
+    PhaseTimer step_timer(PH_STEP, s);
+    {
+        PhaseTimer pt(PH_ROUTER, s);
+        WM_FAIL_HIP(launch_prefill_route(a, fids, fw, s));
+    }
+    {
+        PhaseTimer pt(PH_GATEUP, s);
+        WM_FAIL_HIP(launch_prefill_gateup(a, s));
+    }
+    {
+        PhaseTimer pt(PH_DOWN, s);
+        WM_FAIL_HIP(launch_prefill_down(a, s));
+    }
+    PhaseTimer pt(PH_COMBINE, s);
+    WM_FAIL_HIP(launch_prefill_combine(a, s));
+    return WM_OK;
+}
+
 extern "C" int wm_moe_prefill(const wm_layer_desc* d, const uint16_t* x_bf16, int T, float* out, void* ws,
                               int64_t ws_bytes, int max_tokens, void* stream) {
-    (void)d; (void)x_bf16; (void)T; (void)out; (void)ws; (void)ws_bytes; (void)max_tokens; (void)stream;
-    fprintf(stderr, "winmoe_hip: wm_moe_prefill is not built yet\n");
-    return WM_ERR;
+    return run_prefill(d, x_bf16, T, nullptr, nullptr, out, ws, ws_bytes, max_tokens, stream);
+}
+
+extern "C" int wm_moe_prefill_forced(const wm_layer_desc* d, const uint16_t* x_bf16, int T, const int32_t* ids,
+                                     const float* w, float* out, void* ws, int64_t ws_bytes, int max_tokens,
+                                     void* stream) {
+    WM_CHECK_ARG(ids && w);
+    return run_prefill(d, x_bf16, T, ids, w, out, ws, ws_bytes, max_tokens, stream);
 }
 
 // ------------------------------------------------------------------ gpu_offload.h shims

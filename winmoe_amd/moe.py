@@ -254,15 +254,60 @@ class MoELayer:
         self.step = st + 1
         return out
 
+    def _prefill_ws(self, T: int) -> torch.Tensor:
+        """The prefill workspace (allocated on first use, sized for max(T, max_tokens))."""
+        need_tokens = max(T, self.max_tokens)
+        if getattr(self, "pf_ws", None) is None or self.pf_tokens < need_tokens:
+            nbytes = load().wm_prefill_workspace_size(C.byref(self.desc), need_tokens)
+            if nbytes < 0:
+                raise ValueError("invalid layer descriptor for prefill")
+            self.pf_ws = _ws(nbytes, self.gate_exps.device)
+            self.pf_ws.zero_()
+            self.pf_tokens = need_tokens
+        return self.pf_ws
+
     def prefill(self, x_bf16: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
-        """moe_out for T prompt tokens (x bf16 [T][H]) -> fp32 [T][H]."""
+        """moe_out for T prompt tokens (x bf16 [T][H]) -> fp32 [T][H], routed by the router."""
         _need(x_bf16, torch.bfloat16, "x")
         T = x_bf16.shape[0]
         if out is None:
             out = torch.empty(T, self.H, dtype=torch.float32, device=x_bf16.device)
-        check(load().wm_moe_prefill(C.byref(self.desc), _p(x_bf16), T, _p(out), _p(self.ws), self.ws.numel(),
-                                    self.max_tokens, _stream(stream)), "wm_moe_prefill")
+        ws = self._prefill_ws(T)
+        check(load().wm_moe_prefill(C.byref(self.desc), _p(x_bf16), T, _p(out), _p(ws), ws.numel(), self.pf_tokens,
+                                    _stream(stream)), "wm_moe_prefill")
         return out
+
+    def prefill_forced(self, x_bf16: torch.Tensor, ids: torch.Tensor, w: torch.Tensor,
+                       out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+        """Prefill with caller routing: ids int32 [T][K], w fp32 [T][K] on device."""
+        _need(x_bf16, torch.bfloat16, "x")
+        _need(ids, torch.int32, "ids")
+        _need(w, torch.float32, "w")
+        T = x_bf16.shape[0]
+        if ids.shape != (T, self.K) or w.shape != (T, self.K):
+            raise ValueError("ids / w must be [T][K]")
+        if out is None:
+            out = torch.empty(T, self.H, dtype=torch.float32, device=x_bf16.device)
+        ws = self._prefill_ws(T)
+        check(load().wm_moe_prefill_forced(C.byref(self.desc), _p(x_bf16), T, _p(ids), _p(w), _p(out), _p(ws),
+                                           ws.numel(), self.pf_tokens, _stream(stream)), "wm_moe_prefill_forced")
+        return out
+
+    def prefill_status(self) -> int:
+        """Status bits of the prefill workspace (synchronises the host)."""
+        v = C.c_int32()
+        check(load().wm_workspace_status(_p(self.pf_ws), self.pf_ws.numel(), C.byref(v)), "wm_workspace_status")
+        return v.value
+
+    def prefill_routing(self, T: int):
+        """(ids int32 [T][K], weights fp32 [T][K]) of the last prefill call."""
+        io, wo, ho = C.c_int64(), C.c_int64(), C.c_int64()
+        check(load().wm_prefill_workspace_routing(C.byref(self.desc), self.pf_tokens, C.byref(io), C.byref(wo),
+                                                  C.byref(ho)), "wm_prefill_workspace_routing")
+        n = T * self.K * 4
+        ids = self.pf_ws[io.value:io.value + n].view(torch.int32).view(T, self.K)
+        w = self.pf_ws[wo.value:wo.value + n].view(torch.float32).view(T, self.K)
+        return ids, w
 
     # -- trace ---------------------------------------------------------------
     def trace(self):
