@@ -367,9 +367,50 @@ def test_prefill_router_matches_oracle(wm, orc, shared):
     assert sl.layer.prefill_status() == 0
 
 
+def test_prefill_scales_and_narrow_shared(wm, orc):
+    """Tokens whose magnitudes span 1e-6 .. 1e4 (one all zero, one with a
+    single huge entry), a shared expert half as wide as the routed ones, an
+    odd token count; forced routing."""
+    import torch
+    from winmoe_amd import synth
+    cfg = synth.LayerConfig("pf_e24_k3_h1024_i512_s256", E=24, K=3, H=1024, I=512, types=(Q8_0, Q8_0, Q8_0),
+                            shared_types=(Q8_0, Q8_0, Q8_0), shared_inter=256, shared_gate_inp=True, tokens=1,
+                            routing="zipf", x_dtype="bf16", seed=11)
+    T = 37
+    sl = synth.build_layer(cfg, max_tokens=T)
+    X = synth.make_hidden(cfg, tokens=T).float()
+    scale = torch.logspace(-6, 4, T, device=X.device)
+    X = X * scale[:, None]
+    X[5] = 0.0
+    X[9, 100] = 3.0e4
+    X = X.to(torch.bfloat16)
+    rng = np.random.default_rng(7)
+    ids = np.stack([rng.choice(24, 3, replace=False) for _ in range(T)]).astype(np.int32)
+    w = rng.random((T, 3)).astype(np.float32)
+    case(f"prefill scales T={T}")
+    out = host(sl.layer.prefill_forced(X, dev(ids), dev(w)))
+    for t in range(T):
+        _, _, ref = oracle_token(orc, sl, host(X[t].float()), ids=ids[t], w=w[t])
+        if t == 5:
+            assert np.abs(out[t]).max() == 0.0
+            continue
+        assert rel_l2(out[t], ref) <= LAYER_TOL, (t, rel_l2(out[t], ref))
+    assert sl.layer.prefill_status() == 0
+
+
+def test_prefill_rejects_unsupported_widths(wm):
+    """Prefill needs H, I and the shared width to be multiples of 256."""
+    from winmoe_amd import synth
+    cfg = _pf_cfg(E=8, K=2, H=384, I=256)
+    sl = synth.build_layer(cfg, max_tokens=4)
+    X = synth.make_hidden(cfg, tokens=4)
+    with pytest.raises(Exception):
+        sl.layer.prefill(X)
+
+
 def test_prefill_forced_multi_pass_and_bad_ids(wm, orc):
-    """Caller routing: one expert used by every token (more than one 64-pair
-    pass), one invalid id (skipped, reported)."""
+    """Caller routing: one expert used by every token (three 32-pair passes),
+    one invalid id (skipped, reported)."""
     from winmoe_amd import synth
     cfg = _pf_cfg(E=16, K=4, H=512, I=256, routing="zipf")
     T = 80

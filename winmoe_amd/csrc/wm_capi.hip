@@ -419,19 +419,22 @@ static int run_experts(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
 
 static int rpt_of(int t, int in) { return geometry(t, in).rpt; }
 
-// Workgroups of the fused step resident on the current device at once: two
-// per CU (each holds a 64 KB LDS ring set).
-static int resident_slots() {
+// CUs of the current device (cached per device).
+static int cu_count() {
     static int cached[64] = {0};
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
     if (!cached[dev]) {
         int cus = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-        cached[dev] = 2 * cus;
+        cached[dev] = cus;
     }
     return cached[dev];
 }
+
+// Workgroups of the fused step resident on the current device at once: two
+// per CU (each holds a 64 KB LDS ring set).
+static int resident_slots() { return 2 * cu_count(); }
 
 // One launch of the fused step kernel; returns 1 when the type combination has
 // no fused instantiation (the caller then runs the per-phase kernels).
@@ -609,7 +612,8 @@ extern "C" int wm_expert_ffn(const void* gate, int gt, const void* up, int ut, c
 // ------------------------------------------------------------------ prefill
 
 struct PfLayout {
-    int64_t status, ids, w, logits, hits, offsets, sorted, sg, act, y, total;
+    int64_t status, ids, w, logits, hits, offsets, sorted, passes, pass_count, sg, x16, xexp, act_hi, act_lo, act_sc, y,
+        total;
     int64_t act_stride;
 };
 
@@ -627,9 +631,15 @@ static PfLayout pf_layout(const wm_layer_desc* d, int max_tokens) {
     L.hits = o; o += up256(E * 4);
     L.offsets = o; o += up256((E + 2) * 4);
     L.sorted = o; o += up256(pairs * 4);
+    L.passes = o; o += up256(prefill_max_passes(T, K, E) * 256);
+    L.pass_count = o; o += 256;
     L.sg = o; o += up256(T * 4);
-    L.act_stride = Imax;
-    L.act = o; o += up256(pairs * Imax * 4);
+    L.x16 = o; o += up256(T * H * 2);
+    L.xexp = o; o += up256(T * 4);
+    L.act_stride = (Imax + 255) / 256 * 256;
+    L.act_hi = o; o += up256(pairs * L.act_stride * 2);
+    L.act_lo = o; o += up256(pairs * L.act_stride * 2);
+    L.act_sc = o; o += up256(pairs * (L.act_stride / 128) * 4);
     L.y = o; o += up256(pairs * H * 4);
     L.total = o;
     return L;
@@ -659,9 +669,9 @@ static int run_prefill(const wm_layer_desc* d, const uint16_t* x, int T, const i
     const bool sh = has_shared(d);
     const bool q8 = d->gate_type == Q8_0 && d->up_type == Q8_0 && d->down_type == Q8_0 &&
                     (!sh || (d->sh_gate_type == Q8_0 && d->sh_up_type == Q8_0 && d->sh_down_type == Q8_0));
-    const bool shapes = d->hidden % 128 == 0 && d->inter % 128 == 0 && (!sh || Ishared(d) % 128 == 0);
+    const bool shapes = d->hidden % 256 == 0 && d->inter % 256 == 0 && (!sh || Ishared(d) % 256 == 0);
     if (!q8 || !shapes) {
-        fprintf(stderr, "winmoe_hip: prefill needs Q8_0 expert matrices and H, I multiples of 128\n");
+        fprintf(stderr, "winmoe_hip: prefill needs Q8_0 expert matrices and H, I multiples of 256\n");
         return WM_EINVAL;
     }
     if (wm_init()) return WM_ERR;
@@ -680,7 +690,14 @@ static int run_prefill(const wm_layer_desc* d, const uint16_t* x, int T, const i
     a.ids = (int32_t*)(w8 + L.ids); a.w = (float*)(w8 + L.w); a.logits = (float*)(w8 + L.logits);
     a.hits = (uint32_t*)(w8 + L.hits); a.status = (int32_t*)(w8 + L.status);
     a.offsets = (int32_t*)(w8 + L.offsets); a.sorted = (int32_t*)(w8 + L.sorted); a.sg = (float*)(w8 + L.sg);
-    a.act = (float*)(w8 + L.act); a.act_stride = L.act_stride; a.y = (float*)(w8 + L.y); a.out = out;
+    a.passes = (int32_t*)(w8 + L.passes); a.pass_count = (int32_t*)(w8 + L.pass_count);
+    a.x16 = (uint16_t*)(w8 + L.x16); a.xexp = (int32_t*)(w8 + L.xexp);
+    a.act_hi = (uint16_t*)(w8 + L.act_hi); a.act_lo = (uint16_t*)(w8 + L.act_lo); a.act_sc = (float*)(w8 + L.act_sc);
+    a.act_stride = L.act_stride; a.y = (float*)(w8 + L.y); a.out = out;
+    a.n_wg = cu_count();
+    // the expert GEMMs read 16-byte granules from row starts
+    WM_CHECK_ARG(al(a.gate, 16) && al(a.up, 16) && al(a.down, 16) && a.gstride % 16 == 0 && a.ustride % 16 == 0 &&
+                 a.dstride % 16 == 0 && (!sh || (al(a.sh_gate, 16) && al(a.sh_up, 16) && al(a.sh_down, 16))));
     PhaseTimer step_timer(PH_STEP, s);
     {
         PhaseTimer pt(PH_ROUTER, s);

@@ -27,16 +27,27 @@ struct PrefillArgs {
     int32_t* status;
     int32_t* offsets;           // [E + 2]: pairs of expert e are sorted[offsets[e] .. offsets[e + 1]); shared: [E] .. [E + 1]
     int32_t* sorted;            // [T * K + T] pair indices grouped by expert
-    float* act;                 // [pairs][act_stride] SwiGLU outputs
+    int32_t* passes;            // [prefill_max_passes][64] pass records (up to 32 pairs of one expert)
+    int32_t* pass_count;        // [2]: routed passes, shared passes
+    uint16_t* x16;              // fp16 [T][H]: x * 2^-e per token
+    int32_t* xexp;              // [T]: e
+    uint16_t* act_hi;           // fp16 [pairs][act_stride]: SwiGLU output = (hi + lo) * 2^e per (pair, 128 rows)
+    uint16_t* act_lo;
+    float* act_sc;              // [pairs][act_stride / 128]: 2^e
     int64_t act_stride;
     float* y;                   // [pairs][H] expert outputs
     float* sg;                  // [T] shared-expert gate
     float* out;                 // [T][H]
+    int32_t n_wg;               // workgroups of the persistent expert GEMMs (one per CU)
 };
 
+// Pass records a prefill of T tokens may need.
+inline int64_t prefill_max_passes(int64_t T, int64_t K, int64_t E) { return (T * K + 31) / 32 + E + (T + 31) / 32 + 1; }
+
 // The phases of a prefill, stream-ordered (the caller checks types: Q8_0
-// expert matrices, H, I, Is multiples of 128):
-//   routing: router + top-K, or the caller's ids / weights; grouping; shared gate
+// expert matrices, H, I, Is multiples of 256, expert strides multiples of 16):
+//   routing: router + top-K, or the caller's ids / weights; grouping; shared
+//   gate; fp16 copy of x
 //   gate/up + SwiGLU, down projection, combine.
 int launch_prefill_route(const PrefillArgs& a, const int32_t* forced_ids, const float* forced_w, hipStream_t s);
 int launch_prefill_gateup(const PrefillArgs& a, hipStream_t s);

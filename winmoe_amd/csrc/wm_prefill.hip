@@ -9,16 +9,19 @@
 //                  tokens x 16 experts, each lane one of the 16 FMA chains of
 //                  4 x 4 (token, expert) pairs)
 //   k_pf_topk      one wave per token: K-pass arg-max + softmax
-//   k_pf_group     counting sort of the pairs by expert
-//   k_pf_gateup    per (expert, 64 rows): gate and up on bf16 MFMA
-//                  (v_mfma_f32_16x16x32_bf16, one Q8_0 block per MFMA: the
-//                  int8 weights and the bf16 inputs are exact in bf16, the
-//                  block's fp16 scale multiplies the fp32 partial), SwiGLU
-//   k_pf_down      per (expert, 64 rows of H): down projection, the fp32
-//                  SwiGLU output split into bf16 hi + lo (two MFMAs)
+//   k_pf_group     counting sort of the pairs by expert; passes of <= 32
+//                  pairs of one expert
+//   k_pf_xpack     x as fp16 times a power of two per token
+//   k_pf_gemm<2,1> gate and up + SwiGLU on fp16 MFMA, persistent: one
+//                  workgroup per CU streams (pass, 128-row block) items
+//                  through an LDS-DMA ring; the SwiGLU output is stored as
+//                  fp16 hi + lo times a power of two per (pair, 128 rows)
+//   k_pf_gemm<1,2> down projection of the same form (hi and lo: two MFMAs)
 //   k_pf_combine   per token: sum_k w_k y_k in k order + gate * y_shared
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "../../include/winmoe_hip.h"
 #include "wm_device.h"
@@ -28,11 +31,30 @@
 
 namespace wm {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 WM_DEV float bf16f(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
 
 WM_DEV int pair_token(int p, int T, int K) { return p < T * K ? p / K : p - T * K; }
+
+// Exponent e with m * 2^-e in [2^14, 2^15) for a finite m > 0 (clamped to
+// e >= -126 so that 2^e and 2^-e are normal floats); 0 otherwise.  Values of
+// a group scaled by 2^-e fit fp16 with its full 11-bit precision down to
+// 2^-29 of the group maximum.
+WM_DEV int pf_exp(float m) {
+    if (!(m > 0.0f) || !(m <= 3.402823466e38f)) return 0;
+    int E;
+    frexpf(m, &E);                 // m in [2^(E-1), 2^E)
+    return max(E - 15, -126);
+}
+
+// Expert passes: a pass is up to GM_M pairs of one expert, described by a
+// record of GM_REC ints: expert (E = shared), pair count, 0, 0, GM_M pair ids
+// (positions past the count repeat the last id), then the x scale exponents
+// of the pairs' tokens, 4 signed bytes per int.
+constexpr int GM_M = 32;
+constexpr int GM_REC = 64;
 
 // ------------------------------------------------------------------ router
 
@@ -123,10 +145,17 @@ __global__ __launch_bounds__(256) void k_pf_forced(const int32_t* __restrict__ f
 }
 
 // One workgroup: pairs grouped by expert (order inside an expert is free:
-// every pair's output row is computed independently of the others).
+// every pair's output row is computed independently of the others), then
+// cut into pass records: routed passes first, in expert order, then the
+// shared expert's; pass_count = {routed passes, shared passes}.  A record
+// also carries the x scale of each pair's token.
 __global__ __launch_bounds__(1024) void k_pf_group(const int32_t* __restrict__ ids, int T, int K, int E, int has_shared,
-                                                   int32_t* __restrict__ offsets, int32_t* __restrict__ sorted) {
+                                                   int32_t* __restrict__ offsets, int32_t* __restrict__ sorted,
+                                                   int32_t* __restrict__ passes, int32_t* __restrict__ pass_count,
+                                                   const int32_t* __restrict__ xexp) {
     __shared__ int cnt[1024];
+    __shared__ int off[1026];
+    __shared__ int pbase[1026];
     __shared__ int s_total;
     const int tid = threadIdx.x, P = T * K;
     for (int e = tid; e < E; e += 1024) cnt[e] = 0;
@@ -141,12 +170,20 @@ __global__ __launch_bounds__(1024) void k_pf_group(const int32_t* __restrict__ i
         for (int e = 0; e < E; e++) {
             const int c = cnt[e];
             cnt[e] = run;
+            off[e] = run;
             offsets[e] = run;
             run += c;
         }
-        offsets[E] = run;
-        offsets[E + 1] = run + (has_shared ? T : 0);
+        off[E] = offsets[E] = run;
+        off[E + 1] = offsets[E + 1] = run + (has_shared ? T : 0);
         s_total = run;
+        int np = 0;
+        for (int e = 0; e <= E; e++) {
+            pbase[e] = np;
+            np += (off[e + 1] - off[e] + GM_M - 1) / GM_M;
+        }
+        pass_count[0] = pbase[E];
+        pass_count[1] = np - pbase[E];
     }
     __syncthreads();
     for (int p = tid; p < P; p += 1024) {
@@ -155,6 +192,72 @@ __global__ __launch_bounds__(1024) void k_pf_group(const int32_t* __restrict__ i
     }
     if (has_shared)
         for (int t = tid; t < T; t += 1024) sorted[s_total + t] = P + t;
+    __syncthreads();
+    for (int e = tid; e <= E; e += 1024) {
+        const int o = off[e], n = off[e + 1] - o;
+        for (int q = 0; q * GM_M < n; q++) {
+            int32_t* rec = passes + (int64_t)(pbase[e] + q) * GM_REC;
+            const int mn = min(GM_M, n - q * GM_M);
+            rec[0] = e;
+            rec[1] = mn;
+            rec[2] = 0;
+            rec[3] = 0;
+            uint32_t ex = 0;
+            for (int m = 0; m < GM_M; m++) {
+                const int pr = sorted[o + q * GM_M + min(m, mn - 1)];
+                rec[4 + m] = pr;
+                ex |= (uint32_t)(xexp[pair_token(pr, T, K)] & 0xFF) << (8 * (m & 3));
+                if ((m & 3) == 3) {
+                    rec[4 + GM_M + m / 4] = (int32_t)ex;
+                    ex = 0;
+                }
+            }
+        }
+    }
+}
+
+// x bf16 [T][H] -> x16 = fp16(x * 2^-e) with e per token (pf_exp of the
+// token's largest |x|), xexp[t] = e.  bf16 values are exact in fp16 at that
+// scale (8 significant bits, normal range down to 2^-29 of the maximum).
+__global__ __launch_bounds__(256) void k_pf_xpack(const uint16_t* __restrict__ x, int H, uint16_t* __restrict__ x16,
+                                                  int32_t* __restrict__ xexp) {
+    __shared__ float wmax[WAVES];
+    const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint16_t* xr = x + (int64_t)t * H;
+    float m = 0.0f;
+    for (int c0 = threadIdx.x * 8; c0 < H; c0 += 256 * 8) {
+        const u32x4 v = *(const u32x4*)(xr + c0);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            m = fmaxf(m, fmaxf(fabsf(__builtin_bit_cast(float, v[i] << 16)),
+                               fabsf(__builtin_bit_cast(float, v[i] & 0xFFFF0000u))));
+    }
+    m = fmaxf(m, dpp_f32<DPP_XOR1>(m));
+    m = fmaxf(m, dpp_f32<DPP_XOR2>(m));
+    m = fmaxf(m, dpp_f32<DPP_HALF_MIRROR>(m));
+    m = fmaxf(m, dpp_f32<DPP_MIRROR>(m));       // max of the 16 lanes of each row
+    float r = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m), 0));
+    r = fmaxf(r, __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m), 16)));
+    r = fmaxf(r, __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m), 32)));
+    r = fmaxf(r, __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m), 48)));
+    if (lane == 0) wmax[wave] = r;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const int e = pf_exp(M);
+    const float inv = ldexpf(1.0f, -e);
+    for (int c0 = threadIdx.x * 8; c0 < H; c0 += 256 * 8) {
+        const u32x4 v = *(const u32x4*)(xr + c0);
+        u32x4 o;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)(__builtin_bit_cast(float, v[i] << 16) * inv));
+            const uint32_t hi =
+                __builtin_bit_cast(uint16_t, (_Float16)(__builtin_bit_cast(float, v[i] & 0xFFFF0000u) * inv));
+            o[i] = lo | (hi << 16);
+        }
+        *(u32x4*)(x16 + (int64_t)t * H + c0) = o;
+    }
+    if (threadIdx.x == 0) xexp[t] = e;
 }
 
 // Shared-expert gate of every token: sigmoid_stable((float) sum_h g[h] x[h])
@@ -186,259 +289,493 @@ __global__ __launch_bounds__(256) void k_pf_shgate(const uint16_t* __restrict__ 
     if (threadIdx.x == 0) sg[t] = sigmoid_stable((float)part[0]);
 }
 
-// ------------------------------------------------------------------ grouped expert GEMMs (Q8_0)
+// ------------------------------------------------------------------ grouped expert GEMMs (Q8_0, fp16 MFMA)
+//
+// One workgroup per CU works through a static list of items: item j of a
+// launch is (pass, block of 128 matrix rows), and workgroup b takes items
+// b, b + grid, b + 2 grid, ...  For each item it streams the block's rows (of
+// gate and up, or of down) through an S-stage LDS ring, 128 columns = 4 Q8_0
+// blocks per stage, filled by global_load_lds:
+//   * weights: each row's 136-byte stage chunk as 9 granules of 16 B from
+//     the 16-byte boundary at or before it (the chunk starts 0 or 8 bytes
+//     into its first granule; the 9 granules never leave the row when the
+//     column count is a multiple of 256);
+//   * activations: the pass's 32 rows x 128 fp16, rows 272 bytes apart (a
+//     pad granule each), so the MFMA operand reads of 16 rows hit 16
+//     different 16-byte slots of a 256-byte bank cycle;
+//   * the activations' power-of-two scales of the stage (one dword each).
+// The ring runs across item boundaries: the next item's first stages are in
+// flight while the current one finishes.  Waves 0-7 issue the loads and do
+// the maths (16 rows each); wave 8 only writes results, because vector
+// stores count in vmcnt: issued by the compute waves they would hold up the
+// "stage landed" waits.
+//
+// Per (row, block) the 32 int8 weights become fp16 exactly (byte ^ 0x80
+// under the exponent byte 0x64 is 1152 + q; minus 1152), so
+// v_mfma_f32_16x16x32_f16 gives the block's dot product with the scaled fp16
+// activations; the block's fp16 scale d multiplies it, the activation scale
+// multiplies the stage's sum.
 
-constexpr int PG_N = 64;        // matrix rows per item (16 per wave)
-constexpr int PG_M = 64;        // pairs per pass (4 MFMA row tiles)
-constexpr int PG_SLOT = 160;    // LDS bytes per row chunk: 4 blocks (136 B) + alignment shift, whole granules
-constexpr int PG_XLD = 136;     // LDS row of an activation chunk, bf16 elements (128 + 8 pad)
+constexpr int GM_ROWS = 128;          // matrix rows per item
+constexpr int GM_RSLOT = 144;         // LDS bytes of a row's stage chunk (9 granules)
+constexpr int GM_CW = 8;              // compute waves
+constexpr int GM_THREADS = 64 * (GM_CW + 1);
+constexpr int GM_DESC = 8;            // pass records held in LDS
+constexpr int GM_ALD = 272;           // LDS bytes per activation row of a stage (256 + one pad granule)
+constexpr int GM_APART = 9 * 1024;    // one activation array of a stage: 32 rows x 272 B in 9 DMA units
 
-// 8 bytes at an arbitrary LDS byte offset.
-WM_DEV void lds_u64u(const uint8_t* base, uint32_t off, uint32_t& lo, uint32_t& hi) {
-    const uint32_t* p = (const uint32_t*)(base + (off & ~3u));
-    const uint32_t s = off & 3u;
-    const uint32_t w0 = p[0], w1 = p[1], w2 = p[2];
-    lo = alignbyte(w1, w0, s);
-    hi = alignbyte(w2, w1, s);
+template <int NMAT, int AHL> struct GmGeo {
+    static constexpr int S = NMAT == 2 ? 3 : 4;                        // ring stages
+    static constexpr int W_BYTES = NMAT * GM_ROWS * GM_RSLOT;
+    static constexpr int A_BYTES = AHL * GM_APART;
+    static constexpr int SLOT = W_BYTES + A_BYTES + 256;                // + 64 scale dwords
+    static constexpr int DESC = S * SLOT;
+    static constexpr int RED = DESC + GM_DESC * GM_REC * 4;             // [32 pairs][8 waves] maxima
+    static constexpr int STG = RED + (NMAT == 2 ? GM_M * GM_CW * 4 : 0);
+    // staging: gate/up 32 pairs x 128 rows of fp16 hi and lo + 32 scales;
+    // down 16 pairs x 128 rows of fp32 (the two halves pass through in turn)
+    static constexpr int LDS = STG + (NMAT == 2 ? GM_M * GM_ROWS * 4 + GM_M * 4 : 16 * GM_ROWS * 4);
+    static constexpr int NW = NMAT * GM_ROWS * 9 / 64;                // weight DMA instructions per stage
+    static constexpr int NWT = (NW + GM_CW - 1) / GM_CW;
+    static constexpr int NA = AHL * 9;                                // activation DMA instructions per stage
+    static constexpr int NAT = (NA + GM_CW - 1) / GM_CW;
+};
+static_assert(GmGeo<2, 1>::LDS <= 163840 && GmGeo<1, 2>::LDS <= 163840, "LDS per workgroup");
+static_assert(4 + GM_M + GM_M / 4 <= GM_REC, "pass record");
+
+struct PfGemm {
+    const uint8_t* w0;                 // routed matrices (gate, up) or (down, -): expert e at + e * st
+    const uint8_t* w1;
+    int64_t st0, st1;
+    const uint8_t* s0;                 // shared-expert matrices
+    const uint8_t* s1;
+    int64_t rb_r, rb_s;                // bytes per matrix row: routed, shared
+    int32_t mb_r, mb_s;                // bytes per matrix: routed, shared
+    const uint16_t* a_hi;              // activations, fp16 bits [rows][a_ld]
+    const uint16_t* a_lo;
+    int64_t a_ld;
+    const float* a_sc;                 // activation scales [rows][sc_ld], one per 128 columns
+    int64_t sc_ld;
+    int32_t a_bytes, sc_bytes;         // sizes of the activation and scale arrays
+    int32_t T, K, E, by_token;         // activation row: token of the pair (1) or the pair (0)
+    int32_t nrb_r, nrb_s, nkc_r, nkc_s;    // row blocks per pass and stages per item: routed, shared
+    const int32_t* recs;
+    const int32_t* npass;              // {routed passes, shared passes}
+    uint16_t* o_hi;                    // gate/up: SwiGLU output hi / lo [pair][o_ld], scales [pair][osc_ld]
+    uint16_t* o_lo;
+    float* o_sc;
+    int64_t o_ld, osc_ld;
+    float* y;                          // down: [pair][y_ld]
+    int64_t y_ld;
+};
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Raw buffer resource over [p, p + bytes) (gfx9 word 3: 32-bit data format).
+WM_DEV __amdgpu_buffer_rsrc_t gm_rsrc(const void* p, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
 }
 
-// 8 signed bytes -> 8 bf16 (exact).
-WM_DEV bf16x8 q8_bf16x8(uint32_t lo, uint32_t hi) {
-    bf16x8 r;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        r[j] = (__bf16)(float)(int8_t)(lo >> (8 * j));
-        r[4 + j] = (__bf16)(float)(int8_t)(hi >> (8 * j));
+// All waves of the workgroup meet; this wave's LDS accesses are complete.
+// (No fence: a fence would also wait for the ring's loads in flight.)
+WM_DEV void gm_bar() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform n (values past 15 wait for all).
+WM_DEV void gm_wait_vm(int n) {
+    switch (n) {
+#define WM_GM_CASE(k) \
+    case k: WM_WAIT_VMCNT(k); break;
+        WM_GM_CASE(1) WM_GM_CASE(2) WM_GM_CASE(3) WM_GM_CASE(4) WM_GM_CASE(5) WM_GM_CASE(6) WM_GM_CASE(7)
+        WM_GM_CASE(8) WM_GM_CASE(9) WM_GM_CASE(10) WM_GM_CASE(11) WM_GM_CASE(12) WM_GM_CASE(13) WM_GM_CASE(14)
+        WM_GM_CASE(15)
+#undef WM_GM_CASE
+        default: WM_WAIT_VMCNT(0); break;
     }
-    return r;
 }
 
-// Address of the 16-byte granule j of the 4-block chunk kc of row `row` of a
-// Q8_0 matrix, clamped to the chunk's last granule (no read past the chunk).
-WM_DEV const u32x4* chunk_granule(const uint8_t* W, int64_t row_bytes, int row, int kc, int j) {
-    const uintptr_t start = (uintptr_t)(W + (int64_t)row * row_bytes + (int64_t)kc * 136);
-    const uintptr_t A = start & ~(uintptr_t)15;
-    const int nch = (int)(((start - A) + 136 + 15) >> 4);
-    return (const u32x4*)(A + 16 * (uintptr_t)min(j, nch - 1));
-}
-WM_DEV uint32_t chunk_shift(const uint8_t* W, int64_t row_bytes, int row, int kc) {
-    return (uint32_t)(((uintptr_t)(W + (int64_t)row * row_bytes + (int64_t)kc * 136)) & 15u);
+// The 8 int8 weights k = 8g .. 8g+7 of block B of a row chunk as fp16
+// (exact).  rowp: the chunk's first byte in LDS (8-byte aligned).
+template <int B> WM_DEV f16x8 q8_f16x8(const uint8_t* rowp, int g) {
+    constexpr int off = 34 * B + 2;
+    const uint32_t* p = (const uint32_t*)(rowp + (off & ~3) + 8 * g);
+    const uint32_t K = 0x64646464u, X = 0x80808080u;
+    uint32_t h0, h1, h2, h3;
+    if constexpr ((off & 3) == 0) {
+        const uint32_t d0 = p[0] ^ X, d1 = p[1] ^ X;
+        h0 = __builtin_amdgcn_perm(K, d0, 0x04010400u);
+        h1 = __builtin_amdgcn_perm(K, d0, 0x04030402u);
+        h2 = __builtin_amdgcn_perm(K, d1, 0x04010400u);
+        h3 = __builtin_amdgcn_perm(K, d1, 0x04030402u);
+    } else {
+        const uint32_t d0 = p[0] ^ X, d1 = p[1] ^ X, d2 = p[2] ^ X;
+        h0 = __builtin_amdgcn_perm(K, d0, 0x04030402u);
+        h1 = __builtin_amdgcn_perm(K, d1, 0x04010400u);
+        h2 = __builtin_amdgcn_perm(K, d1, 0x04030402u);
+        h3 = __builtin_amdgcn_perm(K, d2, 0x04010400u);
+    }
+    const f16x2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const f16x2 v0 = __builtin_bit_cast(f16x2, h0) - bias, v1 = __builtin_bit_cast(f16x2, h1) - bias;
+    const f16x2 v2 = __builtin_bit_cast(f16x2, h2) - bias, v3 = __builtin_bit_cast(f16x2, h3) - bias;
+    return (f16x8){v0[0], v0[1], v1[0], v1[1], v2[0], v2[1], v3[0], v3[1]};
 }
 
-// Gate and up of one expert for rows [n0, n0 + 64) and all of its pairs:
-// act[pair][row] = silu(g) * u.
-__global__ __launch_bounds__(256) void k_pf_gateup(PrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t wl[2 * PG_N * PG_SLOT];
-    __shared__ __attribute__((aligned(16))) uint16_t xl[PG_M * PG_XLD];
-    const int eg = blockIdx.y;
-    const bool shared = eg == a.E;
-    const int rows = shared ? a.Is : a.I;
-    const int n0 = blockIdx.x * PG_N;
-    const int p0 = a.offsets[eg], np = a.offsets[eg + 1] - p0;
-    if (n0 >= rows || np <= 0) return;
-    const uint8_t* Wg = shared ? a.sh_gate : a.gate + (int64_t)eg * a.gstride;
-    const uint8_t* Wu = shared ? a.sh_up : a.up + (int64_t)eg * a.ustride;
-    const int H = a.H;
-    const int64_t row_bytes = (int64_t)(H / 32) * 34;
-    const int nkc = H / 128;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c = lane & 15;
-    const int rl = 16 * wave + c;                       // this lane's B row within the item
-    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+// NMAT = 2: gate and up of a pass (activations: the tokens' x, AHL = 1),
+// SwiGLU epilogue.  NMAT = 1: down (activations: the pairs' SwiGLU outputs as
+// hi + lo, AHL = 2), fp32 epilogue.
+template <int NMAT, int AHL>
+__global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
+#if defined(__HIP_DEVICE_COMPILE__)      // the host pass only needs the launch stub (buffer resources are device types)
+    typedef GmGeo<NMAT, AHL> G;
+    constexpr int S = G::S;
+    extern __shared__ __attribute__((aligned(16))) uint8_t gsm[];
+    // the wave index is uniform: readfirstlane lets the compiler keep what depends on it in SGPRs
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), g = lane >> 4, c = lane & 15;
+    const bool cw = wave < GM_CW;
+    const int n_rp = a.npass[0], n_sp = a.npass[1];
+    const int n_r = n_rp * a.nrb_r, n_items = n_r + n_sp * a.nrb_s;
+    if ((int)blockIdx.x >= n_items) return;
 
-    for (int mp = 0; mp < np; mp += PG_M) {
-        const int mn = min(PG_M, np - mp);
-        f32x4 acc[4][2];
+    auto item = [&](int i, int& pass, int& rb, int& nkc) -> bool {
+        const int j = (int)blockIdx.x + i * (int)gridDim.x;
+        if (j >= n_items) return false;
+        if (j < n_r) {
+            pass = j / a.nrb_r;
+            rb = j - pass * a.nrb_r;
+            nkc = a.nkc_r;
+        } else {
+            const int q = (j - n_r) / a.nrb_s;
+            rb = (j - n_r) - q * a.nrb_s;
+            pass = n_rp + q;
+            nkc = a.nkc_s;
+        }
+        return true;
+    };
+    const int32_t* desc = (const int32_t*)(gsm + G::DESC);
+    auto desc_dma = [&](int i, int pass) {
+        __builtin_amdgcn_global_load_lds((const void*)(a.recs + (int64_t)pass * GM_REC + lane),
+                                         (lds_void*)(gsm + G::DESC + (i % GM_DESC) * GM_REC * 4), 4, 0, 0);
+    };
+
+    // Down (NMAT = 1) activations carry a scale per (row, stage); gate/up
+    // activations (x) one per token, applied in the epilogue.
+    constexpr bool SCALED = NMAT == 1;
+    // DMA instructions per stage of this wave: weights, activations, scales
+    int n_w = AHL + (SCALED && wave == GM_CW - 1 ? 1 : 0);
 #pragma unroll
-        for (int mt = 0; mt < 4; mt++) acc[mt][0] = acc[mt][1] = zero;
-        u32x4 rw[5], rx[4];
-        // chunk loader: weights 2 x 64 rows x 10 granules, activations mn x 16 granules
-        auto load = [&](int kc) {
+    for (int t = 0; t < G::NWT; t++)
+        if (wave + GM_CW * t < G::NW) n_w++;
 #pragma unroll
-            for (int q = 0; q < 5; q++) {
-                const int i = tid + 256 * q;
-                const int mat = i / (PG_N * 10), r = (i % (PG_N * 10)) / 10, j = i % 10;
-                rw[q] = (u32x4){0u, 0u, 0u, 0u};
-                if (i < 2 * PG_N * 10 && n0 + r < rows) rw[q] = *chunk_granule(mat ? Wu : Wg, row_bytes, n0 + r, kc, j);
+    for (int t = 0; t < G::NAT; t++)
+        if (wave + GM_CW * t < G::NA) n_w++;
+    const int m_s = lane & 31;        // this lane's pass row of the scale load
+
+    // issue pointer: item ii, stage ikc; the item's sources at stage 0 as
+    // uniform bases plus this lane's 32-bit byte offsets.  Weight instruction
+    // t of this wave covers granules p = 64 (wave + 8 t) + lane: matrix
+    // p / (128 * 9) (uniform per instruction), row (p % 1152) / 9, granule p % 9.
+    int ii = 0, ikc = 0, ip = 0, irb = 0, inkc = 0;
+    bool iok = item(0, ip, irb, inkc);
+    // Sources are bounds-checked buffer resources (a read past the
+    // resource's size returns zeros instead of touching memory).
+    const __amdgpu_buffer_rsrc_t rA0 = gm_rsrc(a.a_hi, a.a_bytes), rA1 = gm_rsrc(a.a_lo, a.a_bytes);
+    const __amdgpu_buffer_rsrc_t rS = gm_rsrc(a.a_sc, a.sc_bytes);
+    __amdgpu_buffer_rsrc_t rW0 = rA0, rW1 = rA0;
+    uint32_t iwo[G::NWT], iao[G::NAT];
+    uint32_t iso = 0;
+    auto setup_issue = [&]() {
+        const int32_t* rec = desc + (ii % GM_DESC) * GM_REC;
+        const int ge = __builtin_amdgcn_readfirstlane(rec[0]);
+        const bool shared = ip >= n_rp;
+        const int mb = shared ? a.mb_s : a.mb_r;
+        rW0 = gm_rsrc(shared ? a.s0 : a.w0 + (int64_t)ge * a.st0, mb);
+        rW1 = NMAT == 2 ? gm_rsrc(shared ? a.s1 : a.w1 + (int64_t)ge * a.st1, mb) : rW0;
+        const uint32_t rowb = (uint32_t)(shared ? a.rb_s : a.rb_r);
+#pragma unroll
+        for (int t = 0; t < G::NWT; t++) {
+            const int p = 64 * (wave + GM_CW * t) + lane, rem = p % (GM_ROWS * 9), r = rem / 9;
+            iwo[t] = (uint32_t)(irb * GM_ROWS + r) * rowb + 16u * (uint32_t)(rem - 9 * r);
+        }
+        // activation instruction u = wave + 8 t: array u / 9, LDS granules
+        // 64 (u % 9) + lane = 17 m + jj of the array (jj = 16: pad; m >= 32:
+        // slack), loaded from granule min(jj, 15) of pass row min(m, 31)
+#pragma unroll
+        for (int t = 0; t < G::NAT; t++) {
+            const int p = 64 * ((wave + GM_CW * t) % 9) + lane, m = min(p / 17, GM_M - 1), jj = min(p % 17, 15);
+            const int pa = rec[4 + m], ra = a.by_token ? pair_token(pa, a.T, a.K) : pa;
+            iao[t] = (uint32_t)ra * (uint32_t)a.a_ld * 2u + 16u * (uint32_t)jj;
+        }
+        if constexpr (SCALED) iso = ((uint32_t)rec[4 + m_s] * (uint32_t)a.sc_ld) * 4u;
+    };
+    int issued = 0;
+    // Loads of stage (ii, ikc) into ring slot issued % S; at an item's first
+    // stage wave 6 also fetches the record of the item two ahead (after the
+    // stage's loads, so "stage landed" implies "record landed").
+    auto issue_next = [&](auto sw_tag) {
+        constexpr bool SW = decltype(sw_tag)::value;
+        if constexpr (!SW) {
+            lds8_t* dst = (lds8_t*)(gsm + (issued % S) * G::SLOT);
+            const uint32_t choff = ((uint32_t)ikc * 136u) & ~15u;
+#pragma unroll
+            for (int t = 0; t < G::NWT; t++) {
+                const int q = wave + GM_CW * t;
+                if (q < G::NW)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(q < GM_ROWS * 9 / 64 ? rW0 : rW1, (lds_void*)(dst + 1024 * q),
+                                                             16, iwo[t], choff, 0, 0);
             }
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int i = tid + 256 * q, m = i >> 4, j = i & 15;
-                rx[q] = (u32x4){0u, 0u, 0u, 0u};
-                if (m < mn) {
-                    const int tok = pair_token(a.sorted[p0 + mp + m], a.T, a.K);
-                    rx[q] = *(const u32x4*)(a.x + (int64_t)tok * H + (int64_t)kc * 128 + 8 * j);
+            for (int t = 0; t < G::NAT; t++) {
+                const int u = wave + GM_CW * t;
+                if (u < G::NA)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(u >= 9 ? rA1 : rA0,
+                                                             (lds_void*)(dst + G::W_BYTES + GM_APART * (u / 9) + 1024 * (u % 9)),
+                                                             16, iao[t], 256u * (uint32_t)ikc, 0, 0);
+            }
+            if (SCALED && wave == GM_CW - 1)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rS, (lds_void*)(dst + G::W_BYTES + G::A_BYTES), 4, iso,
+                                                         4u * (uint32_t)ikc, 0, 0);
+            if (ikc == 0 && wave == 6) {
+                int p2, r2, n2;
+                if (item(ii + 2, p2, r2, n2)) desc_dma(ii + 2, p2);
+            }
+        }
+        ++issued;
+        if (++ikc == inkc) {
+            ikc = 0;
+            ++ii;
+            iok = item(ii, ip, irb, inkc);
+            if constexpr (!SW)
+                if (iok) setup_issue();
+        }
+    };
+
+    f32x4 acc[NMAT][2];
+    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int mat = 0; mat < NMAT; mat++) acc[mat][0] = acc[mat][1] = zero;
+
+    // Stage kc of the current item from ring slot `slot`.
+    auto compute = [&](int slot, int kc, bool two) {
+        const uint8_t* sb = gsm + slot * G::SLOT;
+        const int sh8 = (kc & 1) * 8;
+        // SCALED: the stage's sums go through t and get the stage's scales
+        f32x4 t[NMAT][2];
+#pragma unroll
+        for (int mat = 0; mat < NMAT; mat++) t[mat][0] = t[mat][1] = zero;
+        f32x4(&dst)[NMAT][2] = SCALED ? t : acc;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            f16x8 A[AHL][2];
+#pragma unroll
+            for (int h = 0; h < AHL; h++)
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++)
+                    A[h][mt] = *(const f16x8*)(sb + G::W_BYTES + GM_APART * h + (16 * mt + c) * GM_ALD + 16 * (4 * b + g));
+#pragma unroll
+            for (int mat = 0; mat < NMAT; mat++) {
+                const uint8_t* rowp = sb + (mat * GM_ROWS + 16 * wave + c) * GM_RSLOT + sh8;
+                const float d = (float)*(const _Float16*)(rowp + 34 * b);
+                f16x8 B;
+                if (b == 0) B = q8_f16x8<0>(rowp, g);
+                else if (b == 1) B = q8_f16x8<1>(rowp, g);
+                else if (b == 2) B = q8_f16x8<2>(rowp, g);
+                else B = q8_f16x8<3>(rowp, g);
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++) {
+                    if (mt == 1 && !two) continue;
+                    f32x4 P = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0][mt], B, zero, 0, 0, 0);
+                    if constexpr (AHL == 2) P = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[AHL - 1][mt], B, P, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) dst[mat][mt][i] = fmaf(d, P[i], dst[mat][mt][i]);
                 }
             }
-        };
-        auto store = [&]() {
+            // one block at a time: bounds the registers of operands in flight
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (SCALED) {
+            const f32x4* scp = (const f32x4*)(sb + G::W_BYTES + G::A_BYTES);
 #pragma unroll
-            for (int q = 0; q < 5; q++) {
-                const int i = tid + 256 * q;
-                if (i < 2 * PG_N * 10) *(u32x4*)(wl + 16 * i) = rw[q];
+            for (int mt = 0; mt < 2; mt++) {
+                const f32x4 sc = scp[4 * mt + g];      // scales of pass rows 16 mt + 4 g + i
+#pragma unroll
+                for (int mat = 0; mat < NMAT; mat++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[mat][mt][i] = fmaf(sc[i], t[mat][mt][i], acc[mat][mt][i]);
             }
+        }
+    };
+
+    // Down: one half (16 pairs) of item i's outputs, staged, to registers
+    // and from registers to HBM (wave 8).
+    auto load_half = [&](u32x4(&v)[8]) {
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int i = tid + 256 * q, m = i >> 4, j = i & 15;
-                *(u32x4*)(xl + m * PG_XLD + 8 * j) = rx[q];
+        for (int it = 0; it < 8; it++) v[it] = *(const u32x4*)(gsm + G::STG + (2 * it + (lane >> 5)) * 512 + 16 * (lane & 31));
+    };
+    auto store_half = [&](int i, int rb, int half, const u32x4(&v)[8]) {
+        const int32_t* rec = desc + (i % GM_DESC) * GM_REC;
+        const int mn = rec[1];
+#pragma unroll
+        for (int it = 0; it < 8; it++) {
+            const int m = 16 * half + 2 * it + (lane >> 5);
+            if (m < mn)
+                *(u32x4*)((uint8_t*)(a.y + (int64_t)rec[4 + m] * a.y_ld + rb * GM_ROWS) + 16 * (lane & 31)) = v[it];
+        }
+    };
+    // Results of item i (row block rb) from the staging area to HBM (wave 8;
+    // down: the second half).
+    auto store = [&](int i, int rb) {
+        const int32_t* rec = desc + (i % GM_DESC) * GM_REC;
+        const int mn = rec[1];
+        if constexpr (NMAT == 2) {
+            const uint8_t* sh = gsm + G::STG;
+            const uint8_t* sl = sh + GM_M * GM_ROWS * 2;
+            const float* ss = (const float*)(sl + GM_M * GM_ROWS * 2);
+#pragma unroll
+            for (int it = 0; it < GM_M / 4; it++) {
+                const int m = 4 * it + (lane >> 4), seg = lane & 15;
+                if (m < mn) {
+                    const int64_t o = (int64_t)rec[4 + m] * a.o_ld + rb * GM_ROWS;
+                    *(u32x4*)((uint8_t*)(a.o_hi + o) + 16 * seg) = *(const u32x4*)(sh + m * 256 + 16 * seg);
+                    *(u32x4*)((uint8_t*)(a.o_lo + o) + 16 * seg) = *(const u32x4*)(sl + m * 256 + 16 * seg);
+                }
             }
-        };
-        load(0);
-        store();
-        __syncthreads();
-        for (int kc = 0; kc < nkc; kc++) {
-            if (kc + 1 < nkc) load(kc + 1);
+            if (lane < mn) a.o_sc[(int64_t)rec[4 + lane] * a.osc_ld + rb] = ss[lane];
+        } else {
+            u32x4 v[8];
+            load_half(v);
+            store_half(i, rb, 1, v);
+        }
+    };
+
+    // The compute waves and the store wave run the same schedule (item and
+    // stage pointers, barriers) in two separately compiled copies, so that
+    // neither holds the other's registers.
+    auto run = [&](auto sw_tag) {
+        constexpr bool SW = decltype(sw_tag)::value;
+        // prologue: records of the first two items, then S - 1 stages
+        if constexpr (!SW) {
+            int p1, r1, n1;
+            if (wave == 6) {
+                desc_dma(0, ip);
+                if (item(1, p1, r1, n1)) desc_dma(1, p1);
+            }
+            WM_WAIT_VMCNT(0);
+        }
+        gm_bar();
+        if constexpr (!SW) setup_issue();
+        for (int s = 0; s < S - 1 && iok; s++) issue_next(sw_tag);
+
+        int ci = 0, ckc = 0, cp = 0, crb = 0, cnkc = 0;
+        item(0, cp, crb, cnkc);
+        bool two = false, pend = false;
+        int pi = 0, prb = 0;
+        for (int sigma = 0;; sigma++) {
+            if constexpr (!SW) gm_wait_vm(min(issued - 1 - sigma, S - 2) * n_w);
+            gm_bar();
+            if constexpr (SW) {
+                if (pend) {
+                    store(pi, prb);
+                    pend = false;
+                }
+            }
+            if (iok) issue_next(sw_tag);
+            if constexpr (!SW) {
+                if (ckc == 0) two = __builtin_amdgcn_readfirstlane(desc[(ci % GM_DESC) * GM_REC + 1]) > 16;
+                compute(sigma % S, ckc, two);
+            }
+            if (ckc < cnkc - 1) {
+                ++ckc;
+                continue;
+            }
+            // item done: epilogue into the staging area
+            if constexpr (NMAT == 2) {
+                float av[2][4];
+                float* red = (float*)(gsm + G::RED);
+                if constexpr (!SW) {
 #pragma unroll
-            for (int mat = 0; mat < 2; mat++) {
-                const uint32_t shift = n0 + rl < rows ? chunk_shift(mat ? Wu : Wg, row_bytes, n0 + rl, kc) : 0u;
-                const uint8_t* slot = wl + (mat * PG_N + rl) * PG_SLOT;
+                    for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    const uint32_t off = shift + 34 * b;
-                    const float d = h2f(*(const uint16_t*)(slot + off));
-                    uint32_t qlo, qhi;
-                    lds_u64u(slot, off + 2 + 8 * g, qlo, qhi);
-                    const bf16x8 B = q8_bf16x8(qlo, qhi);
-#pragma unroll
-                    for (int mt = 0; mt < 4; mt++) {
-                        if (16 * mt < mn) {
-                            const bf16x8 A = *(const bf16x8*)(xl + (16 * mt + c) * PG_XLD + 32 * b + 8 * g);
-                            const f32x4 P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B, zero, 0, 0, 0);
-#pragma unroll
-                            for (int i = 0; i < 4; i++) acc[mt][mat][i] = fmaf(d, P[i], acc[mt][mat][i]);
+                        for (int i = 0; i < 4; i++) {
+                            const int m = 16 * mt + 4 * g + i;
+                            const int xe = (int)(int8_t)(desc[(ci % GM_DESC) * GM_REC + 4 + GM_M + m / 4] >> (8 * (m & 3)));
+                            const float xs = ldexpf(1.0f, xe);
+                            const float v = silu_mul(acc[0][mt][i] * xs, acc[1][mt][i] * xs);
+                            av[mt][i] = v;
+                            float mx = fabsf(v);
+                            mx = fmaxf(mx, dpp_f32<DPP_ROR8>(mx));
+                            mx = fmaxf(mx, dpp_f32<DPP_ROR4>(mx));
+                            mx = fmaxf(mx, dpp_f32<DPP_ROR2>(mx));
+                            mx = fmaxf(mx, dpp_f32<DPP_ROR1>(mx));
+                            if (c == 0) red[m * GM_CW + wave] = mx;
                         }
-                    }
+                }
+                gm_bar();
+                if constexpr (!SW) {
+                    uint16_t* sh = (uint16_t*)(gsm + G::STG);
+                    uint16_t* sl = sh + GM_M * GM_ROWS;
+                    float* ss = (float*)(sl + GM_M * GM_ROWS);
+#pragma unroll
+                    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const int m = 16 * mt + 4 * g + i;
+                            const f32x4 r0 = *(const f32x4*)(red + m * GM_CW), r1 = *(const f32x4*)(red + m * GM_CW + 4);
+                            const float M = fmaxf(fmaxf(fmaxf(r0[0], r0[1]), fmaxf(r0[2], r0[3])),
+                                                  fmaxf(fmaxf(r1[0], r1[1]), fmaxf(r1[2], r1[3])));
+                            const int e = pf_exp(M);
+                            const float v = av[mt][i] * ldexpf(1.0f, -e);
+                            const _Float16 hv = (_Float16)v;
+                            const _Float16 lv = (_Float16)(v - (float)hv);
+                            sh[m * GM_ROWS + 16 * wave + c] = __builtin_bit_cast(uint16_t, hv);
+                            sl[m * GM_ROWS + 16 * wave + c] = __builtin_bit_cast(uint16_t, lv);
+                            if (wave == 0 && c == 0) ss[m] = ldexpf(1.0f, e);
+                        }
+                }
+            } else {
+                // pairs 0-15 through the staging area into wave 8's
+                // registers, then pairs 16-31 into the staging area
+                float* sy = (float*)(gsm + G::STG);
+                if constexpr (!SW) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) sy[(4 * g + i) * GM_ROWS + 16 * wave + c] = acc[0][0][i];
+                }
+                gm_bar();
+                u32x4 v[8];
+                if constexpr (SW) load_half(v);
+                gm_bar();
+                if constexpr (!SW) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) sy[(4 * g + i) * GM_ROWS + 16 * wave + c] = acc[0][1][i];
+                } else {
+                    store_half(ci, crb, 0, v);
                 }
             }
-            __syncthreads();
-            if (kc + 1 < nkc) {
-                store();
-                __syncthreads();
+            if constexpr (!SW) {
+#pragma unroll
+                for (int mat = 0; mat < NMAT; mat++) acc[mat][0] = acc[mat][1] = zero;
             }
+            pend = true;
+            pi = ci;
+            prb = crb;
+            ckc = 0;
+            ++ci;
+            if (!item(ci, cp, crb, cnkc)) break;
         }
-        // lane holds C[4g + i][c] of each row tile: pair 16mt + 4g + i, row n0 + rl
-        const int row = n0 + rl;
-#pragma unroll
-        for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int m = 16 * mt + 4 * g + i;
-                if (m < mn && row < rows) {
-                    const int pair = a.sorted[p0 + mp + m];
-                    a.act[(int64_t)pair * a.act_stride + row] = silu_mul(acc[mt][0][i], acc[mt][1][i]);
-                }
-            }
-        __syncthreads();
-    }
+        gm_bar();
+        if constexpr (SW)
+            if (pend) store(pi, prb);
+    };
+    if (cw) run(std::false_type{});
+    else run(std::true_type{});
+#endif
 }
 
-// Down projection of one expert for output rows [n0, n0 + 64) and all of its
-// pairs: y[pair][row] = W_down[row] . act[pair], the activation as bf16 hi + lo.
-__global__ __launch_bounds__(256) void k_pf_down(PrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t wl[PG_N * PG_SLOT];
-    __shared__ __attribute__((aligned(16))) uint16_t ahl[PG_M * PG_XLD];
-    __shared__ __attribute__((aligned(16))) uint16_t all_[PG_M * PG_XLD];
-    const int eg = blockIdx.y;
-    const bool shared = eg == a.E;
-    const int Ie = shared ? a.Is : a.I;
-    const int rows = a.H;
-    const int n0 = blockIdx.x * PG_N;
-    const int p0 = a.offsets[eg], np = a.offsets[eg + 1] - p0;
-    if (n0 >= rows || np <= 0) return;
-    const uint8_t* W = shared ? a.sh_down : a.down + (int64_t)eg * a.dstride;
-    const int64_t row_bytes = (int64_t)(Ie / 32) * 34;
-    const int nkc = Ie / 128;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c = lane & 15;
-    const int rl = 16 * wave + c;
-    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-
-    for (int mp = 0; mp < np; mp += PG_M) {
-        const int mn = min(PG_M, np - mp);
-        f32x4 acc[4];
-#pragma unroll
-        for (int mt = 0; mt < 4; mt++) acc[mt] = zero;
-        u32x4 rw[3];
-        f32x4 ra[8];
-        auto load = [&](int kc) {
-#pragma unroll
-            for (int q = 0; q < 3; q++) {
-                const int i = tid + 256 * q, r = i / 10, j = i % 10;
-                rw[q] = (u32x4){0u, 0u, 0u, 0u};
-                if (i < PG_N * 10 && n0 + r < rows) rw[q] = *chunk_granule(W, row_bytes, n0 + r, kc, j);
-            }
-#pragma unroll
-            for (int q = 0; q < 8; q++) {
-                const int i = tid + 256 * q, m = i >> 5, j = i & 31;     // 32 float4 per pair row chunk
-                ra[q] = zero;
-                if (m < mn) {
-                    const int pair = a.sorted[p0 + mp + m];
-                    ra[q] = *(const f32x4*)(a.act + (int64_t)pair * a.act_stride + (int64_t)kc * 128 + 4 * j);
-                }
-            }
-        };
-        auto store = [&]() {
-#pragma unroll
-            for (int q = 0; q < 3; q++) {
-                const int i = tid + 256 * q;
-                if (i < PG_N * 10) *(u32x4*)(wl + 16 * i) = rw[q];
-            }
-#pragma unroll
-            for (int q = 0; q < 8; q++) {
-                const int i = tid + 256 * q, m = i >> 5, j = i & 31;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const __bf16 h = (__bf16)ra[q][e];
-                    const __bf16 lo = (__bf16)(ra[q][e] - (float)h);
-                    ahl[m * PG_XLD + 4 * j + e] = __builtin_bit_cast(uint16_t, h);
-                    all_[m * PG_XLD + 4 * j + e] = __builtin_bit_cast(uint16_t, lo);
-                }
-            }
-        };
-        load(0);
-        store();
-        __syncthreads();
-        for (int kc = 0; kc < nkc; kc++) {
-            if (kc + 1 < nkc) load(kc + 1);
-            const uint32_t shift = n0 + rl < rows ? chunk_shift(W, row_bytes, n0 + rl, kc) : 0u;
-            const uint8_t* slot = wl + rl * PG_SLOT;
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                const uint32_t off = shift + 34 * b;
-                const float d = h2f(*(const uint16_t*)(slot + off));
-                uint32_t qlo, qhi;
-                lds_u64u(slot, off + 2 + 8 * g, qlo, qhi);
-                const bf16x8 B = q8_bf16x8(qlo, qhi);
-#pragma unroll
-                for (int mt = 0; mt < 4; mt++) {
-                    if (16 * mt < mn) {
-                        const bf16x8 Ah = *(const bf16x8*)(ahl + (16 * mt + c) * PG_XLD + 32 * b + 8 * g);
-                        const bf16x8 Al = *(const bf16x8*)(all_ + (16 * mt + c) * PG_XLD + 32 * b + 8 * g);
-                        f32x4 P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah, B, zero, 0, 0, 0);
-                        P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al, B, P, 0, 0, 0);
-#pragma unroll
-                        for (int i = 0; i < 4; i++) acc[mt][i] = fmaf(d, P[i], acc[mt][i]);
-                    }
-                }
-            }
-            __syncthreads();
-            if (kc + 1 < nkc) {
-                store();
-                __syncthreads();
-            }
-        }
-        const int row = n0 + rl;
-#pragma unroll
-        for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int m = 16 * mt + 4 * g + i;
-                if (m < mn && row < rows) {
-                    const int pair = a.sorted[p0 + mp + m];
-                    a.y[(int64_t)pair * rows + row] = acc[mt][i];
-                }
-            }
-        __syncthreads();
-    }
-}
+template __global__ void k_pf_gemm<2, 1>(PfGemm);
+template __global__ void k_pf_gemm<1, 2>(PfGemm);
 
 // out[t][h] = sum_k w[t][k] y[t*K + k][h] (k order, invalid ids skipped) + gate(t) * y_shared[t][h].
 __global__ __launch_bounds__(256) void k_pf_combine(PrefillArgs a) {
@@ -471,23 +808,55 @@ int launch_prefill_route(const PrefillArgs& a, const int32_t* forced_ids, const 
         hipLaunchKernelGGL(k_pf_topk, dim3((a.T + WAVES - 1) / WAVES), dim3(256), 0, s, a.logits, a.T, a.E, a.K, a.ids,
                            a.w, a.hits, a.status);
     }
-    hipLaunchKernelGGL(k_pf_group, dim3(1), dim3(1024), 0, s, a.ids, a.T, a.K, a.E, a.has_shared, a.offsets, a.sorted);
+    hipLaunchKernelGGL(k_pf_xpack, dim3(a.T), dim3(256), 0, s, a.x, a.H, a.x16, a.xexp);
+    hipLaunchKernelGGL(k_pf_group, dim3(1), dim3(1024), 0, s, a.ids, a.T, a.K, a.E, a.has_shared, a.offsets, a.sorted,
+                       a.passes, a.pass_count, a.xexp);
     if (a.has_shared && a.sh_gate_inp)
         hipLaunchKernelGGL(k_pf_shgate, dim3(a.T), dim3(256), 0, s, a.x, a.sh_gate_inp, a.H, a.sg);
     return (int)hipGetLastError();
 }
 
-int launch_prefill_gateup(const PrefillArgs& a, hipStream_t s) {
-    const int ng = a.E + (a.has_shared ? 1 : 0);
-    const int Imax = a.has_shared && a.Is > a.I ? a.Is : a.I;
-    hipLaunchKernelGGL(k_pf_gateup, dim3((Imax + PG_N - 1) / PG_N, ng), dim3(256), 0, s, a);
+template <int NMAT, int AHL> static int launch_gemm(const PfGemm& g, int n_wg, hipStream_t s) {
+    typedef GmGeo<NMAT, AHL> G;
+    hipError_t e = hipFuncSetAttribute((const void*)k_pf_gemm<NMAT, AHL>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       G::LDS);
+    if (e != hipSuccess) return (int)e;
+    hipLaunchKernelGGL((k_pf_gemm<NMAT, AHL>), dim3(n_wg), dim3(GM_THREADS), G::LDS, s, g);
     return (int)hipGetLastError();
 }
 
+int launch_prefill_gateup(const PrefillArgs& a, hipStream_t s) {
+    PfGemm g = {};
+    g.w0 = a.gate; g.w1 = a.up; g.st0 = a.gstride; g.st1 = a.ustride;
+    g.s0 = a.sh_gate; g.s1 = a.sh_up;
+    g.rb_r = g.rb_s = (int64_t)(a.H / 32) * 34;
+    g.mb_r = (int32_t)(g.rb_r * a.I);
+    g.mb_s = a.has_shared ? (int32_t)(g.rb_s * a.Is) : g.mb_r;
+    g.a_hi = a.x16; g.a_lo = a.x16; g.a_ld = a.H; g.a_sc = nullptr; g.sc_ld = 0;
+    g.a_bytes = (int32_t)((int64_t)a.T * a.H * 2); g.sc_bytes = 0;
+    g.T = a.T; g.K = a.K; g.E = a.E; g.by_token = 1;
+    g.nrb_r = a.I / GM_ROWS; g.nrb_s = a.has_shared ? a.Is / GM_ROWS : 1;
+    g.nkc_r = g.nkc_s = a.H / 128;
+    g.recs = a.passes; g.npass = a.pass_count;
+    g.o_hi = a.act_hi; g.o_lo = a.act_lo; g.o_sc = a.act_sc; g.o_ld = a.act_stride; g.osc_ld = a.act_stride / 128;
+    return launch_gemm<2, 1>(g, a.n_wg, s);
+}
+
 int launch_prefill_down(const PrefillArgs& a, hipStream_t s) {
-    const int ng = a.E + (a.has_shared ? 1 : 0);
-    hipLaunchKernelGGL(k_pf_down, dim3((a.H + PG_N - 1) / PG_N, ng), dim3(256), 0, s, a);
-    return (int)hipGetLastError();
+    PfGemm g = {};
+    g.w0 = a.down; g.w1 = a.down; g.st0 = g.st1 = a.dstride;
+    g.s0 = g.s1 = a.sh_down;
+    g.rb_r = (int64_t)(a.I / 32) * 34; g.rb_s = a.has_shared ? (int64_t)(a.Is / 32) * 34 : g.rb_r;
+    g.mb_r = (int32_t)(g.rb_r * a.H); g.mb_s = (int32_t)(g.rb_s * a.H);
+    g.a_hi = a.act_hi; g.a_lo = a.act_lo; g.a_ld = a.act_stride; g.a_sc = a.act_sc; g.sc_ld = a.act_stride / 128;
+    const int64_t pairs = (int64_t)a.T * a.K + (a.has_shared ? a.T : 0);
+    g.a_bytes = (int32_t)(pairs * a.act_stride * 2); g.sc_bytes = (int32_t)(pairs * (a.act_stride / 128) * 4);
+    g.T = a.T; g.K = a.K; g.E = a.E; g.by_token = 0;
+    g.nrb_r = g.nrb_s = a.H / GM_ROWS;
+    g.nkc_r = a.I / 128; g.nkc_s = a.has_shared ? a.Is / 128 : g.nkc_r;
+    g.recs = a.passes; g.npass = a.pass_count;
+    g.y = a.y; g.y_ld = a.H;
+    return launch_gemm<1, 2>(g, a.n_wg, s);
 }
 
 int launch_prefill_combine(const PrefillArgs& a, hipStream_t s) {
