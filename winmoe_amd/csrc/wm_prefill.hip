@@ -323,6 +323,7 @@ constexpr int GM_THREADS = 64 * (GM_CW + 1);
 constexpr int GM_DESC = 8;            // pass records held in LDS
 constexpr int GM_ALD = 272;           // LDS bytes per activation row of a stage (256 + one pad granule)
 constexpr int GM_APART = 9 * 1024;    // one activation array of a stage: 32 rows x 272 B in 9 DMA units
+constexpr int GM_A16 = 5;             // DMA units holding rows 0-15 (16 x 272 B)
 
 template <int NMAT, int AHL> struct GmGeo {
     static constexpr int S = NMAT == 2 ? 3 : 4;                        // ring stages
@@ -440,7 +441,7 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
     const int n_r = n_rp * a.nrb_r, n_items = n_r + n_sp * a.nrb_s;
     if ((int)blockIdx.x >= n_items) return;
 
-    auto item = [&](int i, int& pass, int& rb, int& nkc) -> bool {
+    auto item = [&](int i, int& pass, int& rb, int& nkc) __attribute__((always_inline)) -> bool {
         const int j = (int)blockIdx.x + i * (int)gridDim.x;
         if (j >= n_items) return false;
         if (j < n_r) {
@@ -456,7 +457,7 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
         return true;
     };
     const int32_t* desc = (const int32_t*)(gsm + G::DESC);
-    auto desc_dma = [&](int i, int pass) {
+    auto desc_dma = [&](int i, int pass) __attribute__((always_inline)) {
         __builtin_amdgcn_global_load_lds((const void*)(a.recs + (int64_t)pass * GM_REC + lane),
                                          (lds_void*)(gsm + G::DESC + (i % GM_DESC) * GM_REC * 4), 4, 0, 0);
     };
@@ -464,14 +465,20 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
     // Down (NMAT = 1) activations carry a scale per (row, stage); gate/up
     // activations (x) one per token, applied in the epilogue.
     constexpr bool SCALED = NMAT == 1;
-    // DMA instructions per stage of this wave: weights, activations, scales
-    int n_w = AHL + (SCALED && wave == GM_CW - 1 ? 1 : 0);
+    // DMA instructions per stage of this wave: weights, activations, scales.
+    // A pass of at most 16 pairs loads only the first 5 units of each
+    // activation array (rows 0-15): n_w16 instructions.
+    int n_w = SCALED && wave == GM_CW - 1 ? 1 : 0;
 #pragma unroll
     for (int t = 0; t < G::NWT; t++)
         if (wave + GM_CW * t < G::NW) n_w++;
+    int n_w16 = n_w;
 #pragma unroll
-    for (int t = 0; t < G::NAT; t++)
-        if (wave + GM_CW * t < G::NA) n_w++;
+    for (int t = 0; t < G::NAT; t++) {
+        const int u = wave + GM_CW * t;
+        if (u < G::NA) n_w++;
+        if (u < G::NA && u % 9 < GM_A16) n_w16++;
+    }
     const int m_s = lane & 31;        // this lane's pass row of the scale load
 
     // issue pointer: item ii, stage ikc; the item's sources at stage 0 as
@@ -487,8 +494,10 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
     __amdgpu_buffer_rsrc_t rW0 = rA0, rW1 = rA0;
     uint32_t iwo[G::NWT], iao[G::NAT];
     uint32_t iso = 0;
-    auto setup_issue = [&]() {
+    bool itwo = true;                 // the issue item's pass uses rows 16-31
+    auto setup_issue = [&]() __attribute__((always_inline)) {
         const int32_t* rec = desc + (ii % GM_DESC) * GM_REC;
+        itwo = __builtin_amdgcn_readfirstlane(rec[1]) > 16;
         const int ge = __builtin_amdgcn_readfirstlane(rec[0]);
         const bool shared = ip >= n_rp;
         const int mb = shared ? a.mb_s : a.mb_r;
@@ -512,12 +521,21 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
         if constexpr (SCALED) iso = ((uint32_t)rec[4 + m_s] * (uint32_t)a.sc_ld) * 4u;
     };
     int issued = 0;
+    // Per-wave DMA instruction counts of the issued stages not yet consumed,
+    // 4 bits each, oldest in the low bits (at most S of them), and their sum:
+    // "stage landed" is vmcnt(sum minus the oldest count).
+    uint32_t qpack = 0;
+    int qn = 0, qsum = 0;
     // Loads of stage (ii, ikc) into ring slot issued % S; at an item's first
     // stage wave 6 also fetches the record of the item two ahead (after the
     // stage's loads, so "stage landed" implies "record landed").
-    auto issue_next = [&](auto sw_tag) {
+    auto issue_next = [&](auto sw_tag) __attribute__((always_inline)) {
         constexpr bool SW = decltype(sw_tag)::value;
         if constexpr (!SW) {
+            const int n = itwo ? n_w : n_w16;
+            qpack |= (uint32_t)n << (4 * qn);
+            ++qn;
+            qsum += n;
             lds8_t* dst = (lds8_t*)(gsm + (issued % S) * G::SLOT);
             const uint32_t choff = ((uint32_t)ikc * 136u) & ~15u;
 #pragma unroll
@@ -530,7 +548,7 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
 #pragma unroll
             for (int t = 0; t < G::NAT; t++) {
                 const int u = wave + GM_CW * t;
-                if (u < G::NA)
+                if (u < G::NA && (itwo || u % 9 < GM_A16))
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(u >= 9 ? rA1 : rA0,
                                                              (lds_void*)(dst + G::W_BYTES + GM_APART * (u / 9) + 1024 * (u % 9)),
                                                              16, iao[t], 256u * (uint32_t)ikc, 0, 0);
@@ -558,15 +576,16 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
 #pragma unroll
     for (int mat = 0; mat < NMAT; mat++) acc[mat][0] = acc[mat][1] = zero;
 
-    // Stage kc of the current item from ring slot `slot`.
-    auto compute = [&](int slot, int kc, bool two) {
+    // Stage kc of the current item from ring slot `slot`; TWO: pass rows
+    // 16-31 are in use (one straight-line body per case, for the scheduler).
+    auto compute = [&](int slot, int kc, auto two_tag) __attribute__((always_inline)) {
+        constexpr bool TWO = decltype(two_tag)::value;
         const uint8_t* sb = gsm + slot * G::SLOT;
         const int sh8 = (kc & 1) * 8;
-        // SCALED: the stage's sums go through t and get the stage's scales
+        // the stage's sums; SCALED: times the stage's activation scales
         f32x4 t[NMAT][2];
 #pragma unroll
         for (int mat = 0; mat < NMAT; mat++) t[mat][0] = t[mat][1] = zero;
-        f32x4(&dst)[NMAT][2] = SCALED ? t : acc;
 #pragma unroll
         for (int b = 0; b < 4; b++) {
             f16x8 A[AHL][2];
@@ -586,15 +605,13 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                 else B = q8_f16x8<3>(rowp, g);
 #pragma unroll
                 for (int mt = 0; mt < 2; mt++) {
-                    if (mt == 1 && !two) continue;
+                    if (mt == 1 && !TWO) continue;
                     f32x4 P = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0][mt], B, zero, 0, 0, 0);
                     if constexpr (AHL == 2) P = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[AHL - 1][mt], B, P, 0, 0, 0);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) dst[mat][mt][i] = fmaf(d, P[i], dst[mat][mt][i]);
+                    for (int i = 0; i < 4; i++) t[mat][mt][i] = fmaf(d, P[i], t[mat][mt][i]);
                 }
             }
-            // one block at a time: bounds the registers of operands in flight
-            __builtin_amdgcn_sched_barrier(0);
         }
         if constexpr (SCALED) {
             const f32x4* scp = (const f32x4*)(sb + G::W_BYTES + G::A_BYTES);
@@ -605,6 +622,12 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                 for (int mat = 0; mat < NMAT; mat++)
 #pragma unroll
                     for (int i = 0; i < 4; i++) acc[mat][mt][i] = fmaf(sc[i], t[mat][mt][i], acc[mat][mt][i]);
+            }
+        } else {
+#pragma unroll
+            for (int mat = 0; mat < NMAT; mat++) {
+                acc[mat][0] += t[mat][0];
+                if constexpr (TWO) acc[mat][1] += t[mat][1];
             }
         }
     };
@@ -627,7 +650,7 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
     };
     // Results of item i (row block rb) from the staging area to HBM (wave 8;
     // down: the second half).
-    auto store = [&](int i, int rb) {
+    auto store = [&](int i, int rb) __attribute__((always_inline)) {
         const int32_t* rec = desc + (i % GM_DESC) * GM_REC;
         const int mn = rec[1];
         if constexpr (NMAT == 2) {
@@ -654,7 +677,7 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
     // The compute waves and the store wave run the same schedule (item and
     // stage pointers, barriers) in two separately compiled copies, so that
     // neither holds the other's registers.
-    auto run = [&](auto sw_tag) {
+    auto run = [&](auto sw_tag) __attribute__((always_inline)) {
         constexpr bool SW = decltype(sw_tag)::value;
         // prologue: records of the first two items, then S - 1 stages
         if constexpr (!SW) {
@@ -674,7 +697,13 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
         bool two = false, pend = false;
         int pi = 0, prb = 0;
         for (int sigma = 0;; sigma++) {
-            if constexpr (!SW) gm_wait_vm(min(issued - 1 - sigma, S - 2) * n_w);
+            if constexpr (!SW) {
+                const int oldest = (int)(qpack & 15u);
+                gm_wait_vm(qsum - oldest);
+                qsum -= oldest;
+                qpack >>= 4;
+                --qn;
+            }
             gm_bar();
             if constexpr (SW) {
                 if (pend) {
@@ -685,7 +714,8 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
             if (iok) issue_next(sw_tag);
             if constexpr (!SW) {
                 if (ckc == 0) two = __builtin_amdgcn_readfirstlane(desc[(ci % GM_DESC) * GM_REC + 1]) > 16;
-                compute(sigma % S, ckc, two);
+                if (two) compute(sigma % S, ckc, std::true_type{});
+                else compute(sigma % S, ckc, std::false_type{});
             }
             if (ckc < cnkc - 1) {
                 ++ckc;
@@ -695,13 +725,17 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
             if constexpr (NMAT == 2) {
                 float av[2][4];
                 float* red = (float*)(gsm + G::RED);
+                // this lane's pass rows are 16 mt + 4 g + i: one base per
+                // array plus constant offsets
                 if constexpr (!SW) {
+                    const uint32_t xw = (uint32_t)desc[(ci % GM_DESC) * GM_REC + 4 + GM_M + g];   // rows 4g..4g+3
+                    const uint32_t xw1 = (uint32_t)desc[(ci % GM_DESC) * GM_REC + 4 + GM_M + 4 + g];
+                    float* redp = red + 4 * g * GM_CW + wave;
 #pragma unroll
                     for (int mt = 0; mt < 2; mt++)
 #pragma unroll
                         for (int i = 0; i < 4; i++) {
-                            const int m = 16 * mt + 4 * g + i;
-                            const int xe = (int)(int8_t)(desc[(ci % GM_DESC) * GM_REC + 4 + GM_M + m / 4] >> (8 * (m & 3)));
+                            const int xe = (int)(int8_t)((mt ? xw1 : xw) >> (8 * i));
                             const float xs = ldexpf(1.0f, xe);
                             const float v = silu_mul(acc[0][mt][i] * xs, acc[1][mt][i] * xs);
                             av[mt][i] = v;
@@ -710,38 +744,39 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                             mx = fmaxf(mx, dpp_f32<DPP_ROR4>(mx));
                             mx = fmaxf(mx, dpp_f32<DPP_ROR2>(mx));
                             mx = fmaxf(mx, dpp_f32<DPP_ROR1>(mx));
-                            if (c == 0) red[m * GM_CW + wave] = mx;
+                            if (c == 0) redp[(16 * mt + i) * GM_CW] = mx;
                         }
                 }
                 gm_bar();
                 if constexpr (!SW) {
-                    uint16_t* sh = (uint16_t*)(gsm + G::STG);
-                    uint16_t* sl = sh + GM_M * GM_ROWS;
-                    float* ss = (float*)(sl + GM_M * GM_ROWS);
+                    uint16_t* shp = (uint16_t*)(gsm + G::STG) + 4 * g * GM_ROWS + 16 * wave + c;
+                    uint16_t* slp = shp + GM_M * GM_ROWS;
+                    float* ss = (float*)(gsm + G::STG + GM_M * GM_ROWS * 4);
+                    const float* redr = red + 4 * g * GM_CW;
 #pragma unroll
                     for (int mt = 0; mt < 2; mt++)
 #pragma unroll
                         for (int i = 0; i < 4; i++) {
-                            const int m = 16 * mt + 4 * g + i;
-                            const f32x4 r0 = *(const f32x4*)(red + m * GM_CW), r1 = *(const f32x4*)(red + m * GM_CW + 4);
+                            const int o = 16 * mt + i;
+                            const f32x4 r0 = *(const f32x4*)(redr + o * GM_CW), r1 = *(const f32x4*)(redr + o * GM_CW + 4);
                             const float M = fmaxf(fmaxf(fmaxf(r0[0], r0[1]), fmaxf(r0[2], r0[3])),
                                                   fmaxf(fmaxf(r1[0], r1[1]), fmaxf(r1[2], r1[3])));
                             const int e = pf_exp(M);
                             const float v = av[mt][i] * ldexpf(1.0f, -e);
                             const _Float16 hv = (_Float16)v;
                             const _Float16 lv = (_Float16)(v - (float)hv);
-                            sh[m * GM_ROWS + 16 * wave + c] = __builtin_bit_cast(uint16_t, hv);
-                            sl[m * GM_ROWS + 16 * wave + c] = __builtin_bit_cast(uint16_t, lv);
-                            if (wave == 0 && c == 0) ss[m] = ldexpf(1.0f, e);
+                            shp[o * GM_ROWS] = __builtin_bit_cast(uint16_t, hv);
+                            slp[o * GM_ROWS] = __builtin_bit_cast(uint16_t, lv);
+                            if (wave == 0 && c == 0) ss[4 * g + o] = ldexpf(1.0f, e);
                         }
                 }
             } else {
                 // pairs 0-15 through the staging area into wave 8's
                 // registers, then pairs 16-31 into the staging area
-                float* sy = (float*)(gsm + G::STG);
+                float* sy = (float*)(gsm + G::STG) + 4 * g * GM_ROWS + 16 * wave + c;
                 if constexpr (!SW) {
 #pragma unroll
-                    for (int i = 0; i < 4; i++) sy[(4 * g + i) * GM_ROWS + 16 * wave + c] = acc[0][0][i];
+                    for (int i = 0; i < 4; i++) sy[i * GM_ROWS] = acc[0][0][i];
                 }
                 gm_bar();
                 u32x4 v[8];
@@ -749,7 +784,7 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                 gm_bar();
                 if constexpr (!SW) {
 #pragma unroll
-                    for (int i = 0; i < 4; i++) sy[(4 * g + i) * GM_ROWS + 16 * wave + c] = acc[0][1][i];
+                    for (int i = 0; i < 4; i++) sy[i * GM_ROWS] = acc[0][1][i];
                 } else {
                     store_half(ci, crb, 0, v);
                 }
