@@ -663,7 +663,7 @@ extern "C" int wm_prefill_workspace_routing(const wm_layer_desc* d, int max_toke
 static int run_prefill(const wm_layer_desc* d, const uint16_t* x, int T, const int32_t* fids, const float* fw,
                        float* out, void* ws, int64_t ws_bytes, int max_tokens, void* stream) {
     if (int rc = validate_desc(d, fids == nullptr)) return rc;
-    WM_CHECK_ARG(x && out && ws && al(ws, 256) && al(x, 16) && T > 0 && T <= max_tokens);
+    WM_CHECK_ARG(x && out && ws && al(ws, 256) && al(x, 16) && al(out, 16) && T > 0 && T <= max_tokens);
     PfLayout L = pf_layout(d, max_tokens);
     WM_CHECK_ARG(ws_bytes >= L.total);
     const bool sh = has_shared(d);

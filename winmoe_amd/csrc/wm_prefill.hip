@@ -144,6 +144,39 @@ __global__ __launch_bounds__(256) void k_pf_forced(const int32_t* __restrict__ f
     else atomicOr(status, WM_STATUS_BAD_EXPERT_ID);
 }
 
+// Exclusive prefix sums of (a, b) over the 1024 threads of a workgroup; the
+// totals go to *tot.  wsum: 16 x 2 ints of LDS.
+WM_DEV int2 block_excl_scan2(int2 v, int* wsum, int2* tot) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int2 inc = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int ux = __shfl_up(inc.x, d), uy = __shfl_up(inc.y, d);
+        if (lane >= d) {
+            inc.x += ux;
+            inc.y += uy;
+        }
+    }
+    if (lane == 63) {
+        wsum[2 * wave] = inc.x;
+        wsum[2 * wave + 1] = inc.y;
+    }
+    __syncthreads();
+    int2 before = make_int2(0, 0), all = make_int2(0, 0);
+    for (int w = 0; w < 16; w++) {
+        const int2 ws = make_int2(wsum[2 * w], wsum[2 * w + 1]);
+        if (w < wave) {
+            before.x += ws.x;
+            before.y += ws.y;
+        }
+        all.x += ws.x;
+        all.y += ws.y;
+    }
+    __syncthreads();
+    *tot = all;
+    return make_int2(before.x + inc.x - v.x, before.y + inc.y - v.y);
+}
+
 // One workgroup: pairs grouped by expert (order inside an expert is free:
 // every pair's output row is computed independently of the others), then
 // cut into pass records: routed passes first, in expert order, then the
@@ -153,65 +186,80 @@ __global__ __launch_bounds__(1024) void k_pf_group(const int32_t* __restrict__ i
                                                    int32_t* __restrict__ offsets, int32_t* __restrict__ sorted,
                                                    int32_t* __restrict__ passes, int32_t* __restrict__ pass_count,
                                                    const int32_t* __restrict__ xexp) {
-    __shared__ int cnt[1024];
+    __shared__ int cnt[1025];
     __shared__ int off[1026];
     __shared__ int pbase[1026];
-    __shared__ int s_total;
-    const int tid = threadIdx.x, P = T * K;
+    __shared__ int wsum[32];
+    const int tid = threadIdx.x, P = T * K, G = E + 1;      // group E: the shared expert (empty without one)
     for (int e = tid; e < E; e += 1024) cnt[e] = 0;
+    if (tid == 0) cnt[E] = has_shared ? T : 0;
     __syncthreads();
     for (int p = tid; p < P; p += 1024) {
         const int e = ids[p];
         if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
+    // pair offsets and pass bases of the groups, 1024 groups per round
+    int2 carry = make_int2(0, 0);
+    for (int base = 0; base < G; base += 1024) {
+        const int e = base + tid;
+        const int n = e < G ? cnt[e] : 0;
+        int2 tot;
+        const int2 ex = block_excl_scan2(make_int2(n, (n + GM_M - 1) / GM_M), wsum, &tot);
+        if (e < G) {
+            off[e] = carry.x + ex.x;
+            pbase[e] = carry.y + ex.y;
+            cnt[e] = carry.x + ex.x;          // scatter cursor
+        }
+        carry.x += tot.x;
+        carry.y += tot.y;
+    }
     if (tid == 0) {
-        int run = 0;
-        for (int e = 0; e < E; e++) {
-            const int c = cnt[e];
-            cnt[e] = run;
-            off[e] = run;
-            offsets[e] = run;
-            run += c;
-        }
-        off[E] = offsets[E] = run;
-        off[E + 1] = offsets[E + 1] = run + (has_shared ? T : 0);
-        s_total = run;
-        int np = 0;
-        for (int e = 0; e <= E; e++) {
-            pbase[e] = np;
-            np += (off[e + 1] - off[e] + GM_M - 1) / GM_M;
-        }
-        pass_count[0] = pbase[E];
-        pass_count[1] = np - pbase[E];
+        off[G] = carry.x;
+        pbase[G] = carry.y;
     }
     __syncthreads();
+    for (int e = tid; e <= G; e += 1024) offsets[e] = off[e];
+    if (tid == 0) {
+        pass_count[0] = pbase[E];
+        pass_count[1] = pbase[G] - pbase[E];
+    }
     for (int p = tid; p < P; p += 1024) {
         const int e = ids[p];
         if (e >= 0 && e < E) sorted[atomicAdd(&cnt[e], 1)] = p;
     }
     if (has_shared)
-        for (int t = tid; t < T; t += 1024) sorted[s_total + t] = P + t;
+        for (int t = tid; t < T; t += 1024) sorted[off[E] + t] = P + t;
     __syncthreads();
-    for (int e = tid; e <= E; e += 1024) {
-        const int o = off[e], n = off[e + 1] - o;
-        for (int q = 0; q * GM_M < n; q++) {
-            int32_t* rec = passes + (int64_t)(pbase[e] + q) * GM_REC;
-            const int mn = min(GM_M, n - q * GM_M);
-            rec[0] = e;
-            rec[1] = mn;
-            rec[2] = 0;
-            rec[3] = 0;
+    // one thread per pass: its group by binary search over the pass bases
+    const int npass = pbase[G];
+    for (int q = tid; q < npass; q += 1024) {
+        int lo = 0, hi = G - 1;                  // largest e with pbase[e] <= q
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (pbase[mid] <= q) lo = mid;
+            else hi = mid - 1;
+        }
+        const int e = lo, first = off[e] + (q - pbase[e]) * GM_M;
+        const int mn = min(GM_M, off[e + 1] - first);
+        int32_t* rec = passes + (int64_t)q * GM_REC;
+        rec[0] = e;
+        rec[1] = mn;
+        rec[2] = 0;
+        rec[3] = 0;
+        int prs[GM_M];
+#pragma unroll
+        for (int m = 0; m < GM_M; m++) prs[m] = sorted[first + min(m, mn - 1)];
+#pragma unroll
+        for (int m4 = 0; m4 < GM_M / 4; m4++) {
             uint32_t ex = 0;
-            for (int m = 0; m < GM_M; m++) {
-                const int pr = sorted[o + q * GM_M + min(m, mn - 1)];
-                rec[4 + m] = pr;
-                ex |= (uint32_t)(xexp[pair_token(pr, T, K)] & 0xFF) << (8 * (m & 3));
-                if ((m & 3) == 3) {
-                    rec[4 + GM_M + m / 4] = (int32_t)ex;
-                    ex = 0;
-                }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int pr = prs[4 * m4 + j];
+                rec[4 + 4 * m4 + j] = pr;
+                ex |= (uint32_t)(xexp[pair_token(pr, T, K)] & 0xFF) << (8 * j);
             }
+            rec[4 + GM_M + m4] = (int32_t)ex;
         }
     }
 }
@@ -812,22 +860,33 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
 template __global__ void k_pf_gemm<2, 1>(PfGemm);
 template __global__ void k_pf_gemm<1, 2>(PfGemm);
 
-// out[t][h] = sum_k w[t][k] y[t*K + k][h] (k order, invalid ids skipped) + gate(t) * y_shared[t][h].
+// out[t][h] = sum_k w[t][k] y[t*K + k][h] (k order, invalid ids skipped) + gate(t) * y_shared[t][h];
+// 4 consecutive h per thread.
 __global__ __launch_bounds__(256) void k_pf_combine(PrefillArgs a) {
-    const int t = blockIdx.y, h = blockIdx.x * 256 + threadIdx.x;
-    if (h >= a.H) return;
-    float acc = 0.0f;
+    const int t = blockIdx.y, h4 = blockIdx.x * 256 + threadIdx.x;
+    if (4 * h4 >= a.H) return;
+    const int H4 = a.H / 4;
+    const f32x4* y4 = (const f32x4*)a.y;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int k = 0; k < a.K; k++) {
         const int e = a.ids[(int64_t)t * a.K + k];
         if (e < 0 || e >= a.E) continue;
-        acc = fmaf(a.w[(int64_t)t * a.K + k], a.y[((int64_t)t * a.K + k) * a.H + h], acc);
+        const float wk = a.w[(int64_t)t * a.K + k];
+        const f32x4 v = y4[((int64_t)t * a.K + k) * H4 + h4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] = fmaf(wk, v[i], acc[i]);
     }
     if (a.has_shared) {
-        float ys = a.y[((int64_t)a.T * a.K + t) * a.H + h];
-        if (a.sh_gate_inp) ys *= a.sg[t];
-        acc = acc + ys;
+        f32x4 ys = y4[((int64_t)a.T * a.K + t) * H4 + h4];
+        if (a.sh_gate_inp) {
+            const float gt = a.sg[t];
+#pragma unroll
+            for (int i = 0; i < 4; i++) ys[i] *= gt;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] = acc[i] + ys[i];
     }
-    a.out[(int64_t)t * a.H + h] = acc;
+    ((f32x4*)a.out)[(int64_t)t * H4 + h4] = acc;
 }
 
 // ------------------------------------------------------------------ launcher
@@ -895,7 +954,7 @@ int launch_prefill_down(const PrefillArgs& a, hipStream_t s) {
 }
 
 int launch_prefill_combine(const PrefillArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(k_pf_combine, dim3((a.H + 255) / 256, a.T), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(k_pf_combine, dim3((a.H / 4 + 255) / 256, a.T), dim3(256), 0, s, a);
     return (int)hipGetLastError();
 }
 
