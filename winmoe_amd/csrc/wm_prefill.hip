@@ -373,23 +373,28 @@ constexpr int GM_ALD = 272;           // LDS bytes per activation row of a stage
 constexpr int GM_APART = 9 * 1024;    // one activation array of a stage: 32 rows x 272 B in 9 DMA units
 constexpr int GM_A16 = 5;             // DMA units holding rows 0-15 (16 x 272 B)
 
-template <int NMAT, int AHL> struct GmGeo {
-    static constexpr int S = NMAT == 2 ? 3 : 4;                        // ring stages
+template <int NMAT, int AHL, int NSUB> struct GmGeo {
+    static constexpr int S = NMAT == 2 ? 3 : 5;                        // weight ring stages
     static constexpr int W_BYTES = NMAT * GM_ROWS * GM_RSLOT;
     static constexpr int A_BYTES = AHL * GM_APART;
-    static constexpr int SLOT = W_BYTES + A_BYTES + 256;                // + 64 scale dwords
-    static constexpr int DESC = S * SLOT;
+    static constexpr int A_SLOT = A_BYTES + 256;                        // + 64 scale dwords
+    // activation slots: a slot is refilled S - 1 stages after its last use
+    static constexpr int NAS = (S - 1 + NSUB - 1) / NSUB + 1;
+    static constexpr int ABASE = S * W_BYTES;
+    static constexpr int DESC = ABASE + NAS * A_SLOT;
     static constexpr int RED = DESC + GM_DESC * GM_REC * 4;             // [32 pairs][8 waves] maxima
     static constexpr int STG = RED + (NMAT == 2 ? GM_M * GM_CW * 4 : 0);
     // staging: gate/up 32 pairs x 128 rows of fp16 hi and lo + 32 scales;
-    // down 16 pairs x 128 rows of fp32 (the two halves pass through in turn)
+    // down 16 pairs x 128 rows of fp32 (the halves of a pass pass through in turn)
     static constexpr int LDS = STG + (NMAT == 2 ? GM_M * GM_ROWS * 4 + GM_M * 4 : 16 * GM_ROWS * 4);
     static constexpr int NW = NMAT * GM_ROWS * 9 / 64;                // weight DMA instructions per stage
     static constexpr int NWT = (NW + GM_CW - 1) / GM_CW;
-    static constexpr int NA = AHL * 9;                                // activation DMA instructions per stage
+    static constexpr int NA = AHL * 9;                                // activation DMA instructions per column step
     static constexpr int NAT = (NA + GM_CW - 1) / GM_CW;
+    static_assert(NAS * NSUB >= NSUB + S - 1, "activation slot reuse");
 };
-static_assert(GmGeo<2, 1>::LDS <= 163840 && GmGeo<1, 2>::LDS <= 163840, "LDS per workgroup");
+static_assert(GmGeo<2, 1, 1>::LDS <= 163840 && GmGeo<1, 2, 4>::LDS <= 163840 && GmGeo<1, 2, 2>::LDS <= 163840,
+              "LDS per workgroup");
 static_assert(4 + GM_M + GM_M / 4 <= GM_REC, "pass record");
 
 struct PfGemm {
@@ -407,7 +412,7 @@ struct PfGemm {
     int64_t sc_ld;
     int32_t a_bytes, sc_bytes;         // sizes of the activation and scale arrays
     int32_t T, K, E, by_token;         // activation row: token of the pair (1) or the pair (0)
-    int32_t nrb_r, nrb_s, nkc_r, nkc_s;    // row blocks per pass and stages per item: routed, shared
+    int32_t nrb_r, nrb_s, nkc_r, nkc_s;    // row groups per pass and column steps per item: routed, shared
     const int32_t* recs;
     const int32_t* npass;              // {routed passes, shared passes}
     uint16_t* o_hi;                    // gate/up: SwiGLU output hi / lo [pair][o_ld], scales [pair][osc_ld]
@@ -475,11 +480,13 @@ template <int B> WM_DEV f16x8 q8_f16x8(const uint8_t* rowp, int g) {
 
 // NMAT = 2: gate and up of a pass (activations: the tokens' x, AHL = 1),
 // SwiGLU epilogue.  NMAT = 1: down (activations: the pairs' SwiGLU outputs as
-// hi + lo, AHL = 2), fp32 epilogue.
-template <int NMAT, int AHL>
+// hi + lo, AHL = 2), fp32 epilogue.  An item covers NSUB blocks of 128 rows:
+// each column step loads the activations once and the NSUB weight blocks in
+// turn (one ring stage each).
+template <int NMAT, int AHL, int NSUB>
 __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
 #if defined(__HIP_DEVICE_COMPILE__)      // the host pass only needs the launch stub (buffer resources are device types)
-    typedef GmGeo<NMAT, AHL> G;
+    typedef GmGeo<NMAT, AHL, NSUB> G;
     constexpr int S = G::S;
     extern __shared__ __attribute__((aligned(16))) uint8_t gsm[];
     // the wave index is uniform: readfirstlane lets the compiler keep what depends on it in SGPRs
@@ -489,16 +496,17 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
     const int n_r = n_rp * a.nrb_r, n_items = n_r + n_sp * a.nrb_s;
     if ((int)blockIdx.x >= n_items) return;
 
-    auto item = [&](int i, int& pass, int& rb, int& nkc) __attribute__((always_inline)) -> bool {
+    // item i of this workgroup: pass, row group, column steps
+    auto item = [&](int i, int& pass, int& rg, int& nkc) __attribute__((always_inline)) -> bool {
         const int j = (int)blockIdx.x + i * (int)gridDim.x;
         if (j >= n_items) return false;
         if (j < n_r) {
             pass = j / a.nrb_r;
-            rb = j - pass * a.nrb_r;
+            rg = j - pass * a.nrb_r;
             nkc = a.nkc_r;
         } else {
             const int q = (j - n_r) / a.nrb_s;
-            rb = (j - n_r) - q * a.nrb_s;
+            rg = (j - n_r) - q * a.nrb_s;
             pass = n_rp + q;
             nkc = a.nkc_s;
         }
@@ -510,38 +518,39 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                                          (lds_void*)(gsm + G::DESC + (i % GM_DESC) * GM_REC * 4), 4, 0, 0);
     };
 
-    // Down (NMAT = 1) activations carry a scale per (row, stage); gate/up
-    // activations (x) one per token, applied in the epilogue.
+    // Down (NMAT = 1) activations carry a scale per (row, column step);
+    // gate/up activations (x) one per token, applied in the epilogue.
     constexpr bool SCALED = NMAT == 1;
-    // DMA instructions per stage of this wave: weights, activations, scales.
-    // A pass of at most 16 pairs loads only the first 5 units of each
-    // activation array (rows 0-15): n_w16 instructions.
-    int n_w = SCALED && wave == GM_CW - 1 ? 1 : 0;
+    // DMA instructions of this wave per weight stage, and per activation
+    // column step (activations + scales; a pass of at most 16 pairs loads only
+    // the first 5 units of each activation array: rows 0-15)
+    int n_wt = 0, n_a = SCALED && wave == GM_CW - 1 ? 1 : 0;
 #pragma unroll
     for (int t = 0; t < G::NWT; t++)
-        if (wave + GM_CW * t < G::NW) n_w++;
-    int n_w16 = n_w;
+        if (wave + GM_CW * t < G::NW) n_wt++;
+    int n_a16 = n_a;
 #pragma unroll
     for (int t = 0; t < G::NAT; t++) {
         const int u = wave + GM_CW * t;
-        if (u < G::NA) n_w++;
-        if (u < G::NA && u % 9 < GM_A16) n_w16++;
+        if (u < G::NA) n_a++;
+        if (u < G::NA && u % 9 < GM_A16) n_a16++;
     }
     const int m_s = lane & 31;        // this lane's pass row of the scale load
 
-    // issue pointer: item ii, stage ikc; the item's sources at stage 0 as
-    // uniform bases plus this lane's 32-bit byte offsets.  Weight instruction
-    // t of this wave covers granules p = 64 (wave + 8 t) + lane: matrix
-    // p / (128 * 9) (uniform per instruction), row (p % 1152) / 9, granule p % 9.
-    int ii = 0, ikc = 0, ip = 0, irb = 0, inkc = 0;
-    bool iok = item(0, ip, irb, inkc);
+    // issue pointer: item ii, stage ist = NSUB * column step + row block; the
+    // item's sources as uniform bases plus this lane's 32-bit byte offsets.
+    // Weight instruction t of this wave covers granules p = 64 (wave + 8 t) +
+    // lane of a stage: matrix p / (128 * 9) (uniform per instruction), row
+    // (p % 1152) / 9, granule p % 9.
+    int ii = 0, ist = 0, ip = 0, irg = 0, inkc = 0;
+    bool iok = item(0, ip, irg, inkc);
     // Sources are bounds-checked buffer resources (a read past the
     // resource's size returns zeros instead of touching memory).
     const __amdgpu_buffer_rsrc_t rA0 = gm_rsrc(a.a_hi, a.a_bytes), rA1 = gm_rsrc(a.a_lo, a.a_bytes);
     const __amdgpu_buffer_rsrc_t rS = gm_rsrc(a.a_sc, a.sc_bytes);
     __amdgpu_buffer_rsrc_t rW0 = rA0, rW1 = rA0;
     uint32_t iwo[G::NWT], iao[G::NAT];
-    uint32_t iso = 0;
+    uint32_t iso = 0, irowb = 0;
     bool itwo = true;                 // the issue item's pass uses rows 16-31
     auto setup_issue = [&]() __attribute__((always_inline)) {
         const int32_t* rec = desc + (ii % GM_DESC) * GM_REC;
@@ -551,11 +560,11 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
         const int mb = shared ? a.mb_s : a.mb_r;
         rW0 = gm_rsrc(shared ? a.s0 : a.w0 + (int64_t)ge * a.st0, mb);
         rW1 = NMAT == 2 ? gm_rsrc(shared ? a.s1 : a.w1 + (int64_t)ge * a.st1, mb) : rW0;
-        const uint32_t rowb = (uint32_t)(shared ? a.rb_s : a.rb_r);
+        irowb = (uint32_t)(shared ? a.rb_s : a.rb_r);
 #pragma unroll
         for (int t = 0; t < G::NWT; t++) {
             const int p = 64 * (wave + GM_CW * t) + lane, rem = p % (GM_ROWS * 9), r = rem / 9;
-            iwo[t] = (uint32_t)(irb * GM_ROWS + r) * rowb + 16u * (uint32_t)(rem - 9 * r);
+            iwo[t] = (uint32_t)(irg * NSUB * GM_ROWS + r) * irowb + 16u * (uint32_t)(rem - 9 * r);
         }
         // activation instruction u = wave + 8 t: array u / 9, LDS granules
         // 64 (u % 9) + lane = 17 m + jj of the array (jj = 16: pad; m >= 32:
@@ -568,72 +577,86 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
         }
         if constexpr (SCALED) iso = ((uint32_t)rec[4 + m_s] * (uint32_t)a.sc_ld) * 4u;
     };
-    int issued = 0;
+    int issued = 0, a_issued = 0;
     // Per-wave DMA instruction counts of the issued stages not yet consumed,
     // 4 bits each, oldest in the low bits (at most S of them), and their sum:
     // "stage landed" is vmcnt(sum minus the oldest count).
     uint32_t qpack = 0;
     int qn = 0, qsum = 0;
-    // Loads of stage (ii, ikc) into ring slot issued % S; at an item's first
-    // stage wave 6 also fetches the record of the item two ahead (after the
-    // stage's loads, so "stage landed" implies "record landed").
+    // Loads of stage (ii, ist): the weight block into ring slot issued % S;
+    // at a column step's first block also the activations and scales into
+    // activation slot a_issued % NAS; at an item's first stage wave 6 also
+    // fetches the record of the item two ahead (after the stage's loads, so
+    // "stage landed" implies "record landed").
     auto issue_next = [&](auto sw_tag) __attribute__((always_inline)) {
         constexpr bool SW = decltype(sw_tag)::value;
+        const int kc = ist / NSUB, sub = ist - kc * NSUB;
         if constexpr (!SW) {
-            const int n = itwo ? n_w : n_w16;
+            const int n = n_wt + (sub == 0 ? (itwo ? n_a : n_a16) : 0);
             qpack |= (uint32_t)n << (4 * qn);
             ++qn;
             qsum += n;
-            lds8_t* dst = (lds8_t*)(gsm + (issued % S) * G::SLOT);
-            const uint32_t choff = ((uint32_t)ikc * 136u) & ~15u;
+            lds8_t* dst = (lds8_t*)(gsm + (issued % S) * G::W_BYTES);
+            const uint32_t soff = (((uint32_t)kc * 136u) & ~15u) + (uint32_t)(sub * GM_ROWS) * irowb;
 #pragma unroll
             for (int t = 0; t < G::NWT; t++) {
                 const int q = wave + GM_CW * t;
                 if (q < G::NW)
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(q < GM_ROWS * 9 / 64 ? rW0 : rW1, (lds_void*)(dst + 1024 * q),
-                                                             16, iwo[t], choff, 0, 0);
+                                                             16, iwo[t], soff, 0, 0);
             }
+            if (sub == 0) {
+                lds8_t* adst = (lds8_t*)(gsm + G::ABASE + (a_issued % G::NAS) * G::A_SLOT);
 #pragma unroll
-            for (int t = 0; t < G::NAT; t++) {
-                const int u = wave + GM_CW * t;
-                if (u < G::NA && (itwo || u % 9 < GM_A16))
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(u >= 9 ? rA1 : rA0,
-                                                             (lds_void*)(dst + G::W_BYTES + GM_APART * (u / 9) + 1024 * (u % 9)),
-                                                             16, iao[t], 256u * (uint32_t)ikc, 0, 0);
+                for (int t = 0; t < G::NAT; t++) {
+                    const int u = wave + GM_CW * t;
+                    if (u < G::NA && (itwo || u % 9 < GM_A16))
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(u >= 9 ? rA1 : rA0,
+                                                                 (lds_void*)(adst + GM_APART * (u / 9) + 1024 * (u % 9)),
+                                                                 16, iao[t], 256u * (uint32_t)kc, 0, 0);
+                }
+                if (SCALED && wave == GM_CW - 1)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rS, (lds_void*)(adst + G::A_BYTES), 4, iso,
+                                                             4u * (uint32_t)kc, 0, 0);
             }
-            if (SCALED && wave == GM_CW - 1)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rS, (lds_void*)(dst + G::W_BYTES + G::A_BYTES), 4, iso,
-                                                         4u * (uint32_t)ikc, 0, 0);
-            if (ikc == 0 && wave == 6) {
+            if (ist == 0 && wave == 6) {
                 int p2, r2, n2;
                 if (item(ii + 2, p2, r2, n2)) desc_dma(ii + 2, p2);
             }
         }
         ++issued;
-        if (++ikc == inkc) {
-            ikc = 0;
+        if (sub == 0) ++a_issued;
+        if (++ist == inkc * NSUB) {
+            ist = 0;
             ++ii;
-            iok = item(ii, ip, irb, inkc);
+            iok = item(ii, ip, irg, inkc);
             if constexpr (!SW)
                 if (iok) setup_issue();
         }
     };
 
-    f32x4 acc[NMAT][2];
+    f32x4 acc[NSUB][NMAT][2];
     const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int mat = 0; mat < NMAT; mat++) acc[mat][0] = acc[mat][1] = zero;
-
-    // Stage kc of the current item from ring slot `slot`; TWO: pass rows
-    // 16-31 are in use (one straight-line body per case, for the scheduler).
-    auto compute = [&](int slot, int kc, auto two_tag) __attribute__((always_inline)) {
-        constexpr bool TWO = decltype(two_tag)::value;
-        const uint8_t* sb = gsm + slot * G::SLOT;
-        const int sh8 = (kc & 1) * 8;
-        // the stage's sums; SCALED: times the stage's activation scales
-        f32x4 t[NMAT][2];
+    for (int u = 0; u < NSUB; u++)
 #pragma unroll
-        for (int mat = 0; mat < NMAT; mat++) t[mat][0] = t[mat][1] = zero;
+        for (int mat = 0; mat < NMAT; mat++) acc[u][mat][0] = acc[u][mat][1] = zero;
+
+    // The sums of one stage (column step kc of a weight block) from weight
+    // slot ws and activation slot as, not yet scaled; TWO: pass rows 16-31
+    // are in use (one straight-line body per case, for the scheduler; the
+    // row tile 16-31 sums stay zero otherwise).
+    struct Sums {
+        f32x4 v[NMAT][2];
+    };
+    auto compute = [&](int ws, int as, int kc, auto two_tag) __attribute__((always_inline)) -> Sums {
+        constexpr bool TWO = decltype(two_tag)::value;
+        const uint8_t* wb = gsm + ws * G::W_BYTES;
+        const uint8_t* ab = gsm + G::ABASE + as * G::A_SLOT;
+        const int sh8 = (kc & 1) * 8;
+        Sums t;
+#pragma unroll
+        for (int mat = 0; mat < NMAT; mat++) t.v[mat][0] = t.v[mat][1] = zero;
 #pragma unroll
         for (int b = 0; b < 4; b++) {
             f16x8 A[AHL][2];
@@ -641,10 +664,10 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
             for (int h = 0; h < AHL; h++)
 #pragma unroll
                 for (int mt = 0; mt < 2; mt++)
-                    A[h][mt] = *(const f16x8*)(sb + G::W_BYTES + GM_APART * h + (16 * mt + c) * GM_ALD + 16 * (4 * b + g));
+                    A[h][mt] = *(const f16x8*)(ab + GM_APART * h + (16 * mt + c) * GM_ALD + 16 * (4 * b + g));
 #pragma unroll
             for (int mat = 0; mat < NMAT; mat++) {
-                const uint8_t* rowp = sb + (mat * GM_ROWS + 16 * wave + c) * GM_RSLOT + sh8;
+                const uint8_t* rowp = wb + (mat * GM_ROWS + 16 * wave + c) * GM_RSLOT + sh8;
                 const float d = (float)*(const _Float16*)(rowp + 34 * b);
                 f16x8 B;
                 if (b == 0) B = q8_f16x8<0>(rowp, g);
@@ -657,36 +680,37 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                     f32x4 P = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0][mt], B, zero, 0, 0, 0);
                     if constexpr (AHL == 2) P = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[AHL - 1][mt], B, P, 0, 0, 0);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) t[mat][mt][i] = fmaf(d, P[i], t[mat][mt][i]);
+                    for (int i = 0; i < 4; i++) t.v[mat][mt][i] = fmaf(d, P[i], t.v[mat][mt][i]);
                 }
             }
         }
-        if constexpr (SCALED) {
-            const f32x4* scp = (const f32x4*)(sb + G::W_BYTES + G::A_BYTES);
+        return t;
+    };
+    // acc[SUB] += the stage's sums (SCALED: times the column step's
+    // activation scales of the pass rows 16 mt + 4 g + i)
+    auto accumulate = [&](int as, const Sums& t, auto sub_tag) __attribute__((always_inline)) {
+        constexpr int SUB = decltype(sub_tag)::value;
+        const f32x4* scp = (const f32x4*)(gsm + G::ABASE + as * G::A_SLOT + G::A_BYTES);
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++) {
-                const f32x4 sc = scp[4 * mt + g];      // scales of pass rows 16 mt + 4 g + i
-#pragma unroll
-                for (int mat = 0; mat < NMAT; mat++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) acc[mat][mt][i] = fmaf(sc[i], t[mat][mt][i], acc[mat][mt][i]);
-            }
-        } else {
+        for (int mt = 0; mt < 2; mt++) {
+            const f32x4 sc = SCALED ? scp[4 * mt + g] : (f32x4){1.0f, 1.0f, 1.0f, 1.0f};
 #pragma unroll
             for (int mat = 0; mat < NMAT; mat++) {
-                acc[mat][0] += t[mat][0];
-                if constexpr (TWO) acc[mat][1] += t[mat][1];
+                f32x4 r = acc[SUB][mat][mt];
+#pragma unroll
+                for (int i = 0; i < 4; i++) r[i] = SCALED ? fmaf(sc[i], t.v[mat][mt][i], r[i]) : r[i] + t.v[mat][mt][i];
+                acc[SUB][mat][mt] = r;
             }
         }
     };
 
-    // Down: one half (16 pairs) of item i's outputs, staged, to registers
-    // and from registers to HBM (wave 8).
-    auto load_half = [&](u32x4(&v)[8]) {
+    // Down: 16 pairs (one row tile) of row block rb of item i, staged, to
+    // registers and from registers to HBM (wave 8).
+    auto load_half = [&](u32x4(&v)[8]) __attribute__((always_inline)) {
 #pragma unroll
         for (int it = 0; it < 8; it++) v[it] = *(const u32x4*)(gsm + G::STG + (2 * it + (lane >> 5)) * 512 + 16 * (lane & 31));
     };
-    auto store_half = [&](int i, int rb, int half, const u32x4(&v)[8]) {
+    auto store_half = [&](int i, int rb, int half, const u32x4(&v)[8]) __attribute__((always_inline)) {
         const int32_t* rec = desc + (i % GM_DESC) * GM_REC;
         const int mn = rec[1];
 #pragma unroll
@@ -696,30 +720,23 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                 *(u32x4*)((uint8_t*)(a.y + (int64_t)rec[4 + m] * a.y_ld + rb * GM_ROWS) + 16 * (lane & 31)) = v[it];
         }
     };
-    // Results of item i (row block rb) from the staging area to HBM (wave 8;
-    // down: the second half).
-    auto store = [&](int i, int rb) __attribute__((always_inline)) {
+    // Gate/up: results of item i (row block rb) from the staging area to HBM (wave 8).
+    auto store_gu = [&](int i, int rb) __attribute__((always_inline)) {
         const int32_t* rec = desc + (i % GM_DESC) * GM_REC;
         const int mn = rec[1];
-        if constexpr (NMAT == 2) {
-            const uint8_t* sh = gsm + G::STG;
-            const uint8_t* sl = sh + GM_M * GM_ROWS * 2;
-            const float* ss = (const float*)(sl + GM_M * GM_ROWS * 2);
+        const uint8_t* sh = gsm + G::STG;
+        const uint8_t* sl = sh + GM_M * GM_ROWS * 2;
+        const float* ss = (const float*)(sl + GM_M * GM_ROWS * 2);
 #pragma unroll
-            for (int it = 0; it < GM_M / 4; it++) {
-                const int m = 4 * it + (lane >> 4), seg = lane & 15;
-                if (m < mn) {
-                    const int64_t o = (int64_t)rec[4 + m] * a.o_ld + rb * GM_ROWS;
-                    *(u32x4*)((uint8_t*)(a.o_hi + o) + 16 * seg) = *(const u32x4*)(sh + m * 256 + 16 * seg);
-                    *(u32x4*)((uint8_t*)(a.o_lo + o) + 16 * seg) = *(const u32x4*)(sl + m * 256 + 16 * seg);
-                }
+        for (int it = 0; it < GM_M / 4; it++) {
+            const int m = 4 * it + (lane >> 4), seg = lane & 15;
+            if (m < mn) {
+                const int64_t o = (int64_t)rec[4 + m] * a.o_ld + rb * GM_ROWS;
+                *(u32x4*)((uint8_t*)(a.o_hi + o) + 16 * seg) = *(const u32x4*)(sh + m * 256 + 16 * seg);
+                *(u32x4*)((uint8_t*)(a.o_lo + o) + 16 * seg) = *(const u32x4*)(sl + m * 256 + 16 * seg);
             }
-            if (lane < mn) a.o_sc[(int64_t)rec[4 + lane] * a.osc_ld + rb] = ss[lane];
-        } else {
-            u32x4 v[8];
-            load_half(v);
-            store_half(i, rb, 1, v);
         }
+        if (lane < mn) a.o_sc[(int64_t)rec[4 + lane] * a.osc_ld + rb] = ss[lane];
     };
 
     // The compute waves and the store wave run the same schedule (item and
@@ -740,11 +757,12 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
         if constexpr (!SW) setup_issue();
         for (int s = 0; s < S - 1 && iok; s++) issue_next(sw_tag);
 
-        int ci = 0, ckc = 0, cp = 0, crb = 0, cnkc = 0;
-        item(0, cp, crb, cnkc);
+        int ci = 0, ckc = 0, cp = 0, crg = 0, cnkc = 0, sigma = 0, a_cons = 0;
+        item(0, cp, crg, cnkc);
         bool two = false, pend = false;
         int pi = 0, prb = 0;
-        for (int sigma = 0;; sigma++) {
+        // one stage: wait for it, meet, refill the ring, compute
+        auto stage = [&](auto sub_tag) __attribute__((always_inline)) {
             if constexpr (!SW) {
                 const int oldest = (int)(qpack & 15u);
                 gm_wait_vm(qsum - oldest);
@@ -755,26 +773,36 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
             gm_bar();
             if constexpr (SW) {
                 if (pend) {
-                    store(pi, prb);
+                    store_gu(pi, prb);
                     pend = false;
                 }
             }
             if (iok) issue_next(sw_tag);
             if constexpr (!SW) {
-                if (ckc == 0) two = __builtin_amdgcn_readfirstlane(desc[(ci % GM_DESC) * GM_REC + 1]) > 16;
-                if (two) compute(sigma % S, ckc, std::true_type{});
-                else compute(sigma % S, ckc, std::false_type{});
+                const int as = a_cons % G::NAS;
+                const Sums t = two ? compute(sigma % S, as, ckc, std::true_type{})
+                                   : compute(sigma % S, as, ckc, std::false_type{});
+                accumulate(as, t, sub_tag);
             }
+            ++sigma;
+        };
+        for (;;) {
+            if (ckc == 0) two = __builtin_amdgcn_readfirstlane(desc[(ci % GM_DESC) * GM_REC + 1]) > 16;
+            stage(std::integral_constant<int, 0>{});
+            if constexpr (NSUB > 1) stage(std::integral_constant<int, 1>{});
+            if constexpr (NSUB > 2) stage(std::integral_constant<int, 2>{});
+            if constexpr (NSUB > 3) stage(std::integral_constant<int, 3>{});
+            ++a_cons;
             if (ckc < cnkc - 1) {
                 ++ckc;
                 continue;
             }
             // item done: epilogue into the staging area
             if constexpr (NMAT == 2) {
-                float av[2][4];
-                float* red = (float*)(gsm + G::RED);
                 // this lane's pass rows are 16 mt + 4 g + i: one base per
                 // array plus constant offsets
+                float av[2][4];
+                float* red = (float*)(gsm + G::RED);
                 if constexpr (!SW) {
                     const uint32_t xw = (uint32_t)desc[(ci % GM_DESC) * GM_REC + 4 + GM_M + g];   // rows 4g..4g+3
                     const uint32_t xw1 = (uint32_t)desc[(ci % GM_DESC) * GM_REC + 4 + GM_M + 4 + g];
@@ -785,7 +813,7 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                         for (int i = 0; i < 4; i++) {
                             const int xe = (int)(int8_t)((mt ? xw1 : xw) >> (8 * i));
                             const float xs = ldexpf(1.0f, xe);
-                            const float v = silu_mul(acc[0][mt][i] * xs, acc[1][mt][i] * xs);
+                            const float v = silu_mul(acc[0][0][mt][i] * xs, acc[0][1][mt][i] * xs);
                             av[mt][i] = v;
                             float mx = fabsf(v);
                             mx = fmaxf(mx, dpp_f32<DPP_ROR8>(mx));
@@ -818,47 +846,58 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                             if (wave == 0 && c == 0) ss[4 * g + o] = ldexpf(1.0f, e);
                         }
                 }
+                pend = true;
+                pi = ci;
+                prb = crg;
             } else {
-                // pairs 0-15 through the staging area into wave 8's
-                // registers, then pairs 16-31 into the staging area
+                // each row block's two row tiles pass through the staging
+                // area into wave 8's registers, which it then stores
                 float* sy = (float*)(gsm + G::STG) + 4 * g * GM_ROWS + 16 * wave + c;
-                if constexpr (!SW) {
+                auto half = [&](auto u_tag, auto mt_tag) __attribute__((always_inline)) {
+                    constexpr int U = decltype(u_tag)::value, MT = decltype(mt_tag)::value;
+                    if constexpr (!SW) {
+                        const f32x4 r = acc[U][0][MT];
 #pragma unroll
-                    for (int i = 0; i < 4; i++) sy[i * GM_ROWS] = acc[0][0][i];
-                }
-                gm_bar();
-                u32x4 v[8];
-                if constexpr (SW) load_half(v);
-                gm_bar();
-                if constexpr (!SW) {
-#pragma unroll
-                    for (int i = 0; i < 4; i++) sy[i * GM_ROWS] = acc[0][1][i];
-                } else {
-                    store_half(ci, crb, 0, v);
-                }
+                        for (int i = 0; i < 4; i++) sy[i * GM_ROWS] = r[i];
+                    }
+                    gm_bar();
+                    u32x4 v[8];
+                    if constexpr (SW) load_half(v);
+                    gm_bar();
+                    if constexpr (SW) store_half(ci, crg * NSUB + U, MT, v);
+                };
+                auto block = [&](auto u_tag) __attribute__((always_inline)) {
+                    half(u_tag, std::integral_constant<int, 0>{});
+                    if (two) half(u_tag, std::integral_constant<int, 1>{});
+                };
+                block(std::integral_constant<int, 0>{});
+                if constexpr (NSUB > 1) block(std::integral_constant<int, 1>{});
+                if constexpr (NSUB > 2) block(std::integral_constant<int, 2>{});
+                if constexpr (NSUB > 3) block(std::integral_constant<int, 3>{});
             }
             if constexpr (!SW) {
 #pragma unroll
-                for (int mat = 0; mat < NMAT; mat++) acc[mat][0] = acc[mat][1] = zero;
+                for (int u = 0; u < NSUB; u++)
+#pragma unroll
+                    for (int mat = 0; mat < NMAT; mat++) acc[u][mat][0] = acc[u][mat][1] = zero;
             }
-            pend = true;
-            pi = ci;
-            prb = crb;
             ckc = 0;
             ++ci;
-            if (!item(ci, cp, crb, cnkc)) break;
+            if (!item(ci, cp, crg, cnkc)) break;
         }
         gm_bar();
         if constexpr (SW)
-            if (pend) store(pi, prb);
+            if (pend) store_gu(pi, prb);
     };
     if (cw) run(std::false_type{});
     else run(std::true_type{});
 #endif
 }
 
-template __global__ void k_pf_gemm<2, 1>(PfGemm);
-template __global__ void k_pf_gemm<1, 2>(PfGemm);
+template __global__ void k_pf_gemm<2, 1, 1>(PfGemm);
+template __global__ void k_pf_gemm<1, 2, 4>(PfGemm);
+template __global__ void k_pf_gemm<1, 2, 2>(PfGemm);
+
 
 // out[t][h] = sum_k w[t][k] y[t*K + k][h] (k order, invalid ids skipped) + gate(t) * y_shared[t][h];
 // 4 consecutive h per thread.
@@ -910,12 +949,12 @@ int launch_prefill_route(const PrefillArgs& a, const int32_t* forced_ids, const 
     return (int)hipGetLastError();
 }
 
-template <int NMAT, int AHL> static int launch_gemm(const PfGemm& g, int n_wg, hipStream_t s) {
-    typedef GmGeo<NMAT, AHL> G;
-    hipError_t e = hipFuncSetAttribute((const void*)k_pf_gemm<NMAT, AHL>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       G::LDS);
+template <int NMAT, int AHL, int NSUB> static int launch_gemm(const PfGemm& g, int n_wg, hipStream_t s) {
+    typedef GmGeo<NMAT, AHL, NSUB> G;
+    hipError_t e = hipFuncSetAttribute((const void*)k_pf_gemm<NMAT, AHL, NSUB>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS);
     if (e != hipSuccess) return (int)e;
-    hipLaunchKernelGGL((k_pf_gemm<NMAT, AHL>), dim3(n_wg), dim3(GM_THREADS), G::LDS, s, g);
+    hipLaunchKernelGGL((k_pf_gemm<NMAT, AHL, NSUB>), dim3(n_wg), dim3(GM_THREADS), G::LDS, s, g);
     return (int)hipGetLastError();
 }
 
@@ -933,7 +972,7 @@ int launch_prefill_gateup(const PrefillArgs& a, hipStream_t s) {
     g.nkc_r = g.nkc_s = a.H / 128;
     g.recs = a.passes; g.npass = a.pass_count;
     g.o_hi = a.act_hi; g.o_lo = a.act_lo; g.o_sc = a.act_sc; g.o_ld = a.act_stride; g.osc_ld = a.act_stride / 128;
-    return launch_gemm<2, 1>(g, a.n_wg, s);
+    return launch_gemm<2, 1, 1>(g, a.n_wg, s);
 }
 
 int launch_prefill_down(const PrefillArgs& a, hipStream_t s) {
@@ -946,11 +985,16 @@ int launch_prefill_down(const PrefillArgs& a, hipStream_t s) {
     const int64_t pairs = (int64_t)a.T * a.K + (a.has_shared ? a.T : 0);
     g.a_bytes = (int32_t)(pairs * a.act_stride * 2); g.sc_bytes = (int32_t)(pairs * (a.act_stride / 128) * 4);
     g.T = a.T; g.K = a.K; g.E = a.E; g.by_token = 0;
-    g.nrb_r = g.nrb_s = a.H / GM_ROWS;
     g.nkc_r = a.I / 128; g.nkc_s = a.has_shared ? a.Is / 128 : g.nkc_r;
     g.recs = a.passes; g.npass = a.pass_count;
     g.y = a.y; g.y_ld = a.H;
-    return launch_gemm<1, 2>(g, a.n_wg, s);
+    // row groups of 4 blocks of 128 rows when H allows, else of 2 (H % 256 == 0)
+    if (a.H % (4 * GM_ROWS) == 0) {
+        g.nrb_r = g.nrb_s = a.H / (4 * GM_ROWS);
+        return launch_gemm<1, 2, 4>(g, a.n_wg, s);
+    }
+    g.nrb_r = g.nrb_s = a.H / (2 * GM_ROWS);
+    return launch_gemm<1, 2, 2>(g, a.n_wg, s);
 }
 
 int launch_prefill_combine(const PrefillArgs& a, hipStream_t s) {
