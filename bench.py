@@ -264,7 +264,7 @@ def main():
         ach = per_launch / (gu["avg_us"] * 1e-6) / 1e9
         roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                     "frac": round(ach / PEAK_HBM_GBPS, 4), "traffic": None,
-                    "kernel": "k_pf_gateup (prefill gate+up+SwiGLU, bf16 MFMA over Q8_0 blocks)",
+                    "kernel": "k_pf_gemm<2,1,1> (prefill gate+up+SwiGLU: fp16 MFMA over Q8_0 blocks, LDS-DMA ring)",
                     "bytes_per_launch": per_launch, "avg_launch_us": round(gu["avg_us"], 2)}
     elif prefill:
         pass
@@ -291,7 +291,8 @@ def main():
         "metric": METRIC, "value": round(tokens_per_s, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int8 dot (quantised weights x int8 activation digits) -> int32, fp32 scales/accumulation",
+        "dtype": ("fp16 MFMA (int8 weights exact in fp16, x fp16 per-token scaled, SwiGLU output fp16 hi+lo) -> fp32"
+                  if prefill else "int8 dot (quantised weights x int8 activation digits) -> int32, fp32 scales/accumulation"),
         "data": "synthetic (seeded N(0,0.02) weights quantised on device, N(0,1) hidden states)",
         "config": {"workload": cfg.name, "experts": cfg.E, "top_k": cfg.K, "hidden": cfg.H, "inter": cfg.I,
                    "types": [wm.TYPE_NAMES[t] for t in cfg.types],
