@@ -499,10 +499,15 @@ static int run_fused(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, con
     a.it_router = 1;
     a.n_rgroups = (a.n_router + RGROUP - 1) / RGROUP;
     if (a.n_rgroups > C_MAX_RGROUPS) return 1;
-    a.it_sgu = a.it_router + a.n_router;
+    // Item order: routers, routed gate/up, shared gate/up, shared down, routed
+    // down.  The routed gate/up items that get a workgroup slot at launch only
+    // wait for the routing, so the router's rows have the memory system to
+    // themselves; the shared expert's items take the slots the routers free
+    // and stream while the routing completes.
+    a.it_gu = a.it_router + a.n_router;
+    a.it_sgu = a.it_gu + K * a.n_gu_slot;
     a.it_sdn = a.it_sgu + a.n_sgu;
-    a.it_gu = a.it_sdn + (sh ? a.n_dn_slot : 0);
-    a.it_dn = a.it_gu + K * a.n_gu_slot;
+    a.it_dn = a.it_sdn + (sh ? a.n_dn_slot : 0);
     a.n_items = a.it_dn + K * a.n_dn_slot;
     if (d->flags & WM_FLAG_TIMELINE) {
         a.timeline = (uint64_t*)(ws + L.timeline);

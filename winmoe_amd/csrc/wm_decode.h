@@ -24,7 +24,9 @@ enum : int {
     C_MAX_RGROUPS = 64,
     C_RANGE = C_RGROUP + C_MAX_RGROUPS,   // + range: down items finished for the row range
     C_MAX_RANGES = 256,
-    C_TOTAL = C_RANGE + C_MAX_RANGES,     // counters (lines)
+    C_GO = C_RANGE + C_MAX_RANGES,        // + i: every logit is written (C_RTOP fanned out to C_NGO lines)
+    C_NGO = 32,
+    C_TOTAL = C_GO + C_NGO,               // counters (lines)
 };
 
 struct DecodeArgs {

@@ -46,6 +46,12 @@ WM_DEV void st_relaxed(uint32_t* p, uint32_t v) { __hip_atomic_store(p, v, __ATO
 WM_DEV uint32_t add_relaxed(uint32_t* p, uint32_t v) {
     return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+WM_DEV uint64_t ld_relaxed64(const uint64_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+WM_DEV void st_relaxed64(uint64_t* p, uint64_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+// Dwords 2-3 of a slot's gate/up counter line: (expert id << 32) | 1 once the
+// slot's first gate/up item knows the expert, 0 before.
+WM_DEV uint64_t* slot_expert(uint32_t* gu_line) { return (uint64_t*)(gu_line + 2); }
 
 // All of this workgroup's stores complete, then one thread bumps *ctr.
 // Returns the counter value before the increment (to all threads).
@@ -86,6 +92,27 @@ WM_DEV void wg_wait(const uint32_t* ctr, uint32_t target, int32_t* status) {
 }
 
 // All of this workgroup's stores complete, then one thread sets *ctr = 1.
+// The whole workgroup waits until *p != 0 (bounded) and gets the value.
+WM_DEV uint64_t wg_wait_set64(const uint64_t* p, int32_t* status) {
+    __shared__ uint64_t s_v;
+    if (threadIdx.x == 0) {
+        uint32_t it = 0;
+        int nap = 1;
+        uint64_t v;
+        while ((v = ld_relaxed64(p)) == 0ull) {
+            if (++it > SPIN_LIMIT) {
+                atomicOr(status, WM_STATUS_SPIN_TIMEOUT);
+                break;
+            }
+            for (int i = 0; i < nap; i++) __builtin_amdgcn_s_sleep(4);
+            nap = nap < 4 ? 2 * nap : 4;
+        }
+        s_v = v;
+    }
+    __syncthreads();
+    return s_v;
+}
+
 WM_DEV void wg_flag(uint32_t* ctr) {
     WM_WAIT_VMCNT(0);
     __syncthreads();
@@ -106,6 +133,16 @@ WM_DEV void item_down(const DecodeArgs& a, const uint8_t* W, int in, int range, 
     const Geo g = geometry(T, in);
     const int tpw = a.rows_dn_item / (WAVES * g.rpt);
     wg_gemv_item<T, true>(W, a.H, in, range * WAVES * tpw, tpw, act, y, smem, scale);
+}
+
+// item_down with the weights' first tiles issued before `wait` (the input is
+// not ready yet).
+template <int T, typename F>
+WM_DEV void item_down_prefetch(const DecodeArgs& a, const uint8_t* W, int in, int range, const float* act, float* y,
+                               uint8_t* smem, const float* scale, F&& wait) {
+    const Geo g = geometry(T, in);
+    const int tpw = a.rows_dn_item / (WAVES * g.rpt);
+    wg_gemv_item_prefetch<T, true>(W, a.H, in, range * WAVES * tpw, tpw, act, y, smem, scale, wait);
 }
 
 WM_DEV uint32_t* ctr(const DecodeArgs& a, int i) { return a.ctr + (int64_t)i * CTR_STRIDE; }
@@ -140,7 +177,7 @@ __global__ __launch_bounds__(256) void k_decode_step(DecodeArgs a) {
         t_work = __builtin_amdgcn_s_memrealtime();
         wg_flag(ctr(a, C_AUX));
         if (a.forced && threadIdx.x == 0) st_relaxed(ctr(a, C_TOPK), 1u);
-    } else if (item < a.it_sgu) {
+    } else if (item < a.it_gu) {
         // ---- router rows.  The last item of each group of RGROUP bumps the
         // top counter (all logits are in once it reaches n_rgroups); the last
         // of those writes the trace: top-K, softmax weights, hit counts.
@@ -154,19 +191,22 @@ __global__ __launch_bounds__(256) void k_decode_step(DecodeArgs a) {
         if (wg_signal(ctr(a, C_RGROUP + g)) == gsize - 1) {
             t_x1 = __builtin_amdgcn_s_memrealtime();
             if (wg_signal(ctr(a, C_RTOP)) == (uint32_t)(a.n_rgroups - 1)) {
+                // every logit is in: one flag line per group of routed items,
+                // so that their polls spread over C_NGO lines
+                if (threadIdx.x < C_NGO) st_relaxed(ctr(a, C_GO + threadIdx.x), 1u);
                 if (threadIdx.x < 64) wave_topk<true>(a.logits, a.E, K, a.ids, a.w, a.hits, a.status, threadIdx.x);
                 t_x2 = __builtin_amdgcn_s_memrealtime();
                 wg_flag(ctr(a, C_TOPK));
             }
         }
-    } else if (item < a.it_sdn) {
+    } else if (item >= a.it_sgu && item < a.it_sdn) {
         // ---- shared expert gate/up + SwiGLU (needs no routing)
         kind = 2;
         item_gateup<SGUT>(a, a.sh_gate, a.sh_up, a.Is, item - a.it_sgu, a.tpw_sgu, a.act + (int64_t)K * a.act_stride,
                           smem);
         t_work = __builtin_amdgcn_s_memrealtime();
         wg_post(ctr(a, C_GU + K));
-    } else if (item >= a.it_gu && item < a.it_dn) {
+    } else if (item < a.it_sgu) {
         // ---- routed gate/up + SwiGLU.  The item finds its slot's expert
         // itself (slot + 1 picks over the logits), so it does not wait for the
         // whole top-K; the slot's first item publishes the id for the down items.
@@ -179,7 +219,8 @@ __global__ __launch_bounds__(256) void k_decode_step(DecodeArgs a) {
             wg_wait(ctr(a, C_TOPK), 1u, a.status);
             e = gld<true>(a.ids + slot);
         } else {
-            wg_wait(ctr(a, C_RTOP), (uint32_t)a.n_rgroups, a.status);
+            wg_wait(ctr(a, C_GO + item % C_NGO), 1u, a.status);
+            t_x1 = __builtin_amdgcn_s_memrealtime();
             e = wave_pick(a.logits, a.E, slot, threadIdx.x & 63, v);
         }
         t_ready = __builtin_amdgcn_s_memrealtime();
@@ -187,6 +228,8 @@ __global__ __launch_bounds__(256) void k_decode_step(DecodeArgs a) {
         if (jj == 0 && threadIdx.x == 0) {
             gst<true>((int32_t*)ctr(a, C_SLOTEID) + slot, (int32_t)e);
             gst<true>((float*)ctr(a, C_SLOTEID) + MAX_TOPK + slot, v);
+            // the down items of the slot start loading its weights on this
+            st_relaxed64(slot_expert(ctr(a, C_GU + slot)), ((uint64_t)(uint32_t)e << 32) | 1ull);
         }
         item_gateup<GUT>(a, routed(a.gate, a.gstride, e, a.E), routed(a.up, a.ustride, e, a.E), a.I, jj, a.tpw_gu,
                          a.act + (int64_t)slot * a.act_stride, smem);
@@ -195,27 +238,36 @@ __global__ __launch_bounds__(256) void k_decode_step(DecodeArgs a) {
     } else {
         // ---- down projection of one (slot, row range); the last slot of a range combines it
         int slot, range;
-        if (item < a.it_gu) { slot = K; range = item - a.it_sdn; }
+        if (item < a.it_dn) { slot = K; range = item - a.it_sdn; }
         else { slot = (item - a.it_dn) / a.n_dn_slot; range = (item - a.it_dn) % a.n_dn_slot; }
-        wg_wait(ctr(a, C_GU + slot), (uint32_t)(slot == K ? a.n_sgu : a.n_gu_slot), a.status);
-        t_ready = __builtin_amdgcn_s_memrealtime();
         kind = 4;
         const float* act = a.act + (int64_t)slot * a.act_stride;
         float* y = a.ypart + (int64_t)slot * a.H;
+        const uint32_t n_need = (uint32_t)(slot == K ? a.n_sgu : a.n_gu_slot);
+        // The weights' first tiles are loaded while the slot's gate/up items
+        // finish (the expert is known before its SwiGLU output is).
         if (slot == K) {
             // the shared-expert gate multiplies the shared rows here (the
             // same product the combine would form)
             __shared__ float s_gate;
             const bool gated = a.sh_gate_inp != nullptr;
-            if (gated) {
-                wg_wait(ctr(a, C_AUX), 1u, a.status);
-                if (threadIdx.x == 0) s_gate = gld<true>(a.shgate);
-                __syncthreads();
-            }
-            item_down<SDT>(a, a.sh_down, a.Is, range, act, y, smem, gated ? &s_gate : nullptr);
+            item_down_prefetch<SDT>(a, a.sh_down, a.Is, range, act, y, smem, gated ? &s_gate : nullptr, [&]() {
+                wg_wait(ctr(a, C_GU + K), n_need, a.status);
+                if (gated) {
+                    wg_wait(ctr(a, C_AUX), 1u, a.status);
+                    if (threadIdx.x == 0) s_gate = gld<true>(a.shgate);
+                    __syncthreads();
+                }
+                t_ready = __builtin_amdgcn_s_memrealtime();
+            });
+        } else {
+            const uint64_t se = wg_wait_set64(slot_expert(ctr(a, C_GU + slot)), a.status);
+            item_down_prefetch<DT>(a, routed(a.down, a.dstride, (int32_t)(se >> 32), a.E), a.I, range, act, y, smem,
+                                   nullptr, [&]() {
+                                       wg_wait(ctr(a, C_GU + slot), n_need, a.status);
+                                       t_ready = __builtin_amdgcn_s_memrealtime();
+                                   });
         }
-        else item_down<DT>(a, routed(a.down, a.dstride, gld<true>((const int32_t*)ctr(a, C_SLOTEID) + slot), a.E),
-                           a.I, range, act, y, smem);
         t_work = __builtin_amdgcn_s_memrealtime();
         uint32_t old = wg_signal(ctr(a, C_RANGE + range));
         if (old == (uint32_t)(K1 - 1)) {
@@ -245,7 +297,7 @@ __global__ __launch_bounds__(256) void k_decode_step(DecodeArgs a) {
                 float yv[MAX_TOPK + 1];
 #pragma unroll
                 for (int k = 0; k <= MAX_TOPK; k++)          // clamped, unconditional: loads in flight together
-                    yv[k] = gld<true>(a.ypart + (int64_t)min(k, K1 - 1) * a.H + h);
+                    yv[k] = a.ypart[(int64_t)min(k, K1 - 1) * a.H + h];   // ordinary loads, as for the vectors
                 float acc = 0.0f;
 #pragma unroll
                 for (int k = 0; k < MAX_TOPK; k++)
@@ -262,6 +314,7 @@ __global__ __launch_bounds__(256) void k_decode_step(DecodeArgs a) {
                 wg_wait(ctr(a, C_TOPK), 1u, a.status);
                 wg_wait(ctr(a, C_AUX), 1u, a.status);
                 for (int i = threadIdx.x; i < C_TOTAL; i += 256) st_relaxed(a.ctr + (int64_t)i * CTR_STRIDE, 0u);
+                if ((int)threadIdx.x < K) st_relaxed64(slot_expert(ctr(a, C_GU + threadIdx.x)), 0ull);
             }
         }
     }

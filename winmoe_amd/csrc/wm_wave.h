@@ -123,7 +123,21 @@ template <int NI, int S> WM_DEV void wait_tiles(int ahead) {
 // first S tiles are in flight.  Row results go to gout[row] (global,
 // device-coherent when COH) and/or lout[row - lrow0] (LDS).  ring holds
 // S * tile_buf<T>() bytes.
-template <int T, int S, bool COH>
+// The first S tiles of wave_stream's range (repeating the last one when the
+// wave has fewer), issued ahead of the stream (PRE = true below).
+template <int T, int S>
+WM_DEV void wave_stream_prologue(const uint8_t* W, int rows, const Geo& g, int t0, int t1, lds8_t* ring, int lane) {
+    constexpr int NI = tile_ni<T>(), BUF = tile_buf<T>();
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        const int t = min(t0 + s, t1 - 1);
+        tile_dma<NI>(W, (int64_t)t * g.tile_bytes, tile_nbytes(g, rows, t), lane, ring + s * BUF);
+    }
+}
+
+// PRE: the prologue was issued earlier (wave_stream_prologue), before the
+// input vector was ready; the operand fetch then waits for it as well.
+template <int T, int S, bool COH, bool PRE = false>
 WM_DEV void wave_stream(const uint8_t* W, int rows, const Geo& g, int t0, int t1, const float* xsrc, lds8_t* ring,
                         float* gout, __attribute__((address_space(3))) float* lout, int lrow0, int lane,
                         float gscale = 1.0f, bool scaled = false) {
@@ -133,11 +147,7 @@ WM_DEV void wave_stream(const uint8_t* W, int rows, const Geo& g, int t0, int t1
     xop_fetch<T>(xsrc, sub, xr);
     // The prologue always issues S tiles (repeating the last one when the
     // wave has fewer), so exactly S * NI loads follow the operand fetch.
-#pragma unroll
-    for (int s = 0; s < S; s++) {
-        const int t = min(t0 + s, t1 - 1);
-        tile_dma<NI>(W, (int64_t)t * g.tile_bytes, tile_nbytes(g, rows, t), lane, ring + s * BUF);
-    }
+    if constexpr (!PRE) wave_stream_prologue<T, S>(W, rows, g, t0, t1, ring, lane);
     // keep the operand arithmetic (which waits for the operand loads) after
     // the tile loads have been issued
     __builtin_amdgcn_sched_barrier(0);
@@ -222,6 +232,34 @@ WM_DEV void wg_gemv_item(const uint8_t* W, int rows, int in, int tb, int tpw, co
     }
     wave_stream<T, RING_S, COH>(W, rows, g, t0, t1, x, (lds8_t*)(lds + wave * RING_S * BUF), y, nullptr, 0, lane,
                                 scale ? *scale : 1.0f, scale != nullptr);
+}
+
+// wg_gemv_item for an input vector that is not ready yet: every wave issues
+// its first RING_S weight tiles, then `wait()` (called by all threads of the
+// workgroup) returns once x (and *scale) may be read, and the stream goes on
+// with those tiles already on their way.
+template <int T, bool COH, typename F>
+WM_DEV void wg_gemv_item_prefetch(const uint8_t* W, int rows, int in, int tb, int tpw, const float* x, float* y,
+                                  uint8_t* lds, const float* scale, F&& wait) {
+    constexpr int BUF = tile_buf<T>();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const Geo g = geometry(T, in);
+    const int ntiles = (rows + g.rpt - 1) / g.rpt;
+    const int t0 = tb + wave * tpw, t1 = min(t0 + tpw, ntiles);
+    lds8_t* ring = (lds8_t*)(lds + wave * RING_S * BUF);
+    if (W && t0 < t1) wave_stream_prologue<T, RING_S>(W, rows, g, t0, t1, ring, lane);
+    wait();
+    if (t0 >= t1) return;
+    if (!W) {
+        const int rig = lane / g.lpr, sub = lane % g.lpr;
+        for (int t = t0; t < t1; t++) {
+            int row = t * g.rpt + rig;
+            if (sub == 0 && rig < g.rpt && row < rows) gst<COH>(y + row, 0.0f);
+        }
+        return;
+    }
+    wave_stream<T, RING_S, COH, true>(W, rows, g, t0, t1, x, ring, y, nullptr, 0, lane, scale ? *scale : 1.0f,
+                                      scale != nullptr);
 }
 
 // ---------------------------------------------------------------- router
@@ -370,8 +408,11 @@ template <int MAXV> struct Picker {
 template <int MAXV, bool COH>
 WM_DEV void wave_topk_n(const float* logits, int E, int K, int32_t* ids, float* w, uint32_t* hits, int32_t* status,
                         int lane) {
+    // the logits are read with ordinary loads also inside one launch: their
+    // writers finish (device-coherent stores) before the flag that lets this
+    // wave read them, and no cache holds an older copy (see wg_wait's users)
     Picker<MAXV> pk;
-    pk.template init<COH>(logits, E, lane);
+    pk.template init<false>(logits, E, lane);
     int my_e = 0;
     float my_v = 0.0f;
     bool degenerate = false;
