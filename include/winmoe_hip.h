@@ -57,6 +57,18 @@ enum {
  * dependency-satisfied and end times (device constant-rate clock) and its kind
  * into the workspace (diagnostics; see wm_workspace_timeline). */
 #define WM_FLAG_TIMELINE 2
+/* wm_layer_desc.flags: the fused decode step has two kernels with the same
+ * results, bit for bit: the persistent kernel (one workgroup per CU; needs
+ * every workgroup resident at once, every supported type pair, inter ==
+ * inter_shared and the LDS budget of one workgroup per CU) and the
+ * work-item-list kernel (one workgroup per work item, items wait only for
+ * smaller ids).  By default the persistent kernel runs layers with top_k <= 4
+ * that fit it (it is the faster one there; at top-10 the item-list kernel is)
+ * and the item-list kernel everything else.  WM_FLAG_ITEM_KERNEL always picks
+ * the item-list kernel; WM_FLAG_PERSIST_KERNEL picks the persistent kernel
+ * whenever the layer fits it. */
+#define WM_FLAG_ITEM_KERNEL 4
+#define WM_FLAG_PERSIST_KERNEL 8
 
 /* One MoE layer.  Expert tensors are the raw GGUF blocks, stacked by expert:
  * gate/up expert e = [inter rows][hidden/QK blocks] at gate_exps + e*gate_stride,

@@ -310,32 +310,40 @@ def test_legacy_expert_cache_and_ffn(wm, orc):
 
 # ------------------------------------------------------------------ fused step vs per-phase launches
 
-@pytest.mark.parametrize("name,E,tokens", [("c1", 64, 4), ("c2", 40, 6), ("c3", 24, 4), ("c4", 24, 4)])
-def test_fused_step_matches_multi_kernel(wm, name, E, tokens):
-    """One fused launch per token == the per-phase kernel sequence, bit for bit,
-    over several consecutive tokens (the counters reset between launches)."""
+_KERNEL_FLAGS = {"persist": 8, "item": 4}
+
+
+@pytest.mark.parametrize("kernel", ["persist", "item"])
+@pytest.mark.parametrize("name,E,tokens", [("c1", 64, 4), ("c2", 40, 6), ("c2", 512, 3), ("c3", 24, 4),
+                                           ("c4", 24, 4)])
+def test_fused_step_matches_multi_kernel(wm, name, E, tokens, kernel):
+    """One fused launch per token (persistent or work-item-list kernel) == the
+    per-phase kernel sequence, bit for bit, over several consecutive tokens
+    (the counters and hand-off tags carry over between launches).  E=512 puts
+    two router rows on each workgroup of the persistent kernel."""
     from winmoe_amd import synth
     cfg = synth.CONFIGS[name]
     sl = synth.build_layer(cfg, E=E, max_tokens=8)
+    fused = synth.twin_layer(sl, multi_kernel=False, flags=_KERNEL_FLAGS[kernel])
     multi = synth.twin_layer(sl, multi_kernel=True)
     X = synth.make_hidden(cfg, tokens=tokens)
     routes = synth.forced_routes(cfg, E=E, tokens=tokens) if cfg.routing != "router" else None
     for t in range(tokens):
-        case(f"fused vs multi {name} E={E} token={t}")
+        case(f"{kernel} vs multi {name} E={E} token={t}")
         if routes is None:
-            a = host(sl.layer.decode(X[t]))
+            a = host(fused.decode(X[t]))
             b = host(multi.decode(X[t]))
         else:
             ids, w = dev(routes[0][t]), dev(routes[1][t])
-            a = host(sl.layer.decode_forced(X[t], ids, w))
+            a = host(fused.decode_forced(X[t], ids, w))
             b = host(multi.decode_forced(X[t], ids, w))
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), t
-    ta, wa = sl.layer.trace()
+    ta, wa = fused.trace()
     tb, wb = multi.trace()
     assert np.array_equal(host(ta[:tokens]), host(tb[:tokens]))
     assert np.array_equal(host(wa[:tokens]).view(np.uint32), host(wb[:tokens]).view(np.uint32))
-    assert np.array_equal(host(sl.layer.hits()), host(multi.hits()))
-    assert sl.layer.status() == 0 and multi.status() == 0
+    assert np.array_equal(host(fused.hits()), host(multi.hits()))
+    assert fused.status() == 0 and multi.status() == 0
 
 
 # ------------------------------------------------------------------ prefill

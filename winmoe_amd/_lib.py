@@ -26,6 +26,8 @@ STATUS_NONFINITE_WEIGHT = 4
 STATUS_SPIN_TIMEOUT = 8
 FLAG_MULTI_KERNEL = 1
 FLAG_TIMELINE = 2
+FLAG_ITEM_KERNEL = 4
+FLAG_PERSIST_KERNEL = 8
 
 _vp, _i64 = C.c_void_p, C.c_int64
 

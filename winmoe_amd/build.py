@@ -15,11 +15,16 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libwinmoe_hip.so")
 OBJ_DIR = os.path.join(PKG, "_build")
-SOURCES = ["wm_kernels.hip", "wm_decode.hip", "wm_capi.hip", "wm_prefill.hip"]
+SOURCES = ["wm_kernels.hip", "wm_decode.hip", "wm_persist.hip", "wm_capi.hip", "wm_prefill.hip"]
 ARCH = os.environ.get("WINMOE_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    # no implicit FMA contraction: the fused step, the per-phase kernels and
+    # the standalone entry points share device functions and must agree bit
+    # for bit whatever each call site's inlining leads the compiler to fuse;
+    # the fused multiply-adds the kernels want are written as fmaf
+    "-ffp-contract=off",
     # packed fp32 ops stay off in every kernel (hipcc's host pass warns that it
     # does not know the feature; the device pass applies it)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

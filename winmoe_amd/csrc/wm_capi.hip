@@ -235,7 +235,8 @@ extern "C" int wm_router_topk(const float* x, const float* W, int H, int E, int 
 // ------------------------------------------------------------------ layer descriptor + workspace
 
 struct WsLayout {
-    int64_t status, ctr, logits, tr_ids, tr_w, hits, shgate, xin, gbuf, ubuf, act, ypart, timeline, total;
+    int64_t status, ctr, logits, tr_ids, tr_w, hits, shgate, xin, gbuf, ubuf, act, ypart, tlog, hello, pctr, tact,
+        timeline, total;
     int K1, Imax, Is;
 };
 
@@ -286,6 +287,12 @@ static WsLayout layout(const wm_layer_desc* d, int max_tokens) {
     L.ubuf = o; o += up256((int64_t)L.K1 * L.Imax * 4);
     L.act = o; o += up256((int64_t)L.K1 * L.Imax * 4);
     L.ypart = o; o += up256((int64_t)L.K1 * H * 4);
+    // persistent step: tagged logits, per-workgroup start tags, epoch line,
+    // tagged SwiGLU outputs
+    L.tlog = o; o += up256((int64_t)P_REP * E * 8);
+    L.hello = o; o += up256((int64_t)P_MAX_WG * 4);
+    L.pctr = o; o += (int64_t)CTR_STRIDE * 4;
+    L.tact = o; o += up256((int64_t)L.K1 * P_AREP * L.Imax * 8);
     L.timeline = o;
     if (d->flags & WM_FLAG_TIMELINE) o += up256((int64_t)TIMELINE_CAP * 8 * 8);
     L.total = o;
@@ -436,10 +443,99 @@ static int cu_count() {
 // per CU (each holds a 64 KB LDS ring set).
 static int resident_slots() { return 2 * cu_count(); }
 
+// Dynamic LDS one workgroup may use on the current device (cached per device).
+static int max_lds_per_wg() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 65536;
+    if (!cached[dev]) {
+        // the opt-in limit (what hipFuncAttributeMaxDynamicSharedMemorySize may
+        // raise a kernel to: 160 KB on gfx950), else the default per-block limit
+        int v = 0, opt = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0) v = 65536;
+        if (hipDeviceGetAttribute(&opt, hipDeviceAttributeSharedMemPerBlockOptin, dev) == hipSuccess && opt > v) v = opt;
+        cached[dev] = v;
+    }
+    return cached[dev];
+}
+
+// One launch of the persistent step kernel (wm_persist.hip); returns 1 when
+// the layer does not fit it (the caller then uses the work-item-list kernel).
+static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, const float* x, float* out,
+                       const int32_t* forced_ids, const float* forced_w, int32_t* ids, float* w, hipStream_t s) {
+    const bool sh = has_shared(d);
+    if (d->gate_type != d->up_type || (sh && d->sh_gate_type != d->sh_up_type)) return 1;
+    const int gut = d->gate_type, dt = d->down_type;
+    const int sgut = sh ? d->sh_gate_type : gut, sdt = sh ? d->sh_down_type : dt;
+    if (!persist_supported(gut, dt, sgut, sdt)) return 1;
+    const int H = d->hidden, I = d->inter, K = d->top_k, E = d->n_experts;
+    const bool forced = forced_ids != nullptr;
+    if (sh && L.Is != I) return 1;
+    if (!gemv_shape_ok(gut, H) || !gemv_shape_ok(sgut, H) || !gemv_shape_ok(dt, I) || !gemv_shape_ok(sdt, I)) return 1;
+    if (!forced && !al(d->router, 16)) return 1;
+    const int nwg = cu_count();
+    if (nwg > P_MAX_WG) return 1;
+    const int rr = forced ? 0 : (E + nwg - 1) / nwg;
+    if (rr > 4) return 1;
+    PersistArgs a = {};
+    a.H = H; a.I = I; a.E = E; a.K = K; a.has_shared = sh ? 1 : 0; a.forced = forced ? 1 : 0;
+    a.nwg = nwg; a.rr = rr;
+    const int rpt_gu = rpt_of(gut, H), rpt_dn = rpt_of(dt, I);
+    a.gu_tiles = (I + rpt_gu - 1) / rpt_gu;
+    a.dn_tiles = (H + rpt_dn - 1) / rpt_dn;
+    a.gu_cap = (a.gu_tiles + nwg - 1) / nwg * rpt_gu;
+    a.y_cap = (a.dn_tiles + nwg - 1) / nwg * rpt_dn;
+    a.ring_buf = std::max(std::max(ring_tile_bytes_rt(gut), ring_tile_bytes_rt(dt)),
+                          std::max(ring_tile_bytes_rt(sgut), ring_tile_bytes_rt(sdt)));
+    // LDS: control block | rings (x and the router rows at the start) |
+    // SwiGLU operand records | x operand records | gate/up row sums | down row sums
+    int o = (int)((sizeof(PersistCtl) + 255) / 256 * 256);
+    a.o_ring = o; o += PW * PRING * a.ring_buf;
+    a.x_region = (H * 4 + 1023) / 1024 * 1024;
+    const int router_bytes = forced ? 0 : (1 + rr) * a.x_region;
+    a.n_rwaves = (router_bytes + PRING * a.ring_buf - 1) / (PRING * a.ring_buf);
+    if (a.n_rwaves > PW - 1) return 1;
+    const int rec = XOP_DW * 4;
+    a.o_reg = o; o += (K + 1) * (I / SEG) * rec;
+    a.o_xop = o; o += (H / SEG) * rec;
+    a.o_xop2 = a.o_xop;
+    if (sh && sgut != gut) { a.o_xop2 = o; o += (H / SEG) * rec; }
+    a.o_gu = o; o += 2 * (K + 1) * a.gu_cap * 4;
+    a.o_y = o; o += (K + 1) * a.y_cap * 4;
+    const int lds = (o + 255) / 256 * 256;
+    if (lds > max_lds_per_wg()) return 1;
+    if (int rc = aligned_input(x, H, (float*)(ws + L.xin), s)) return rc;
+    a.x = x; a.out = out; a.router = d->router;
+    a.gate = (const uint8_t*)d->gate_exps; a.up = (const uint8_t*)d->up_exps; a.down = (const uint8_t*)d->down_exps;
+    a.gstride = d->gate_stride ? d->gate_stride : matrix_bytes(gut, I, H);
+    a.ustride = d->up_stride ? d->up_stride : matrix_bytes(gut, I, H);
+    a.dstride = d->down_stride ? d->down_stride : matrix_bytes(dt, H, I);
+    a.sh_gate = (const uint8_t*)d->sh_gate; a.sh_up = (const uint8_t*)d->sh_up; a.sh_down = (const uint8_t*)d->sh_down;
+    a.sh_gate_inp = sh ? d->sh_gate_inp : nullptr;
+    a.forced_ids = forced_ids; a.forced_w = forced_w;
+    a.ids = ids; a.w = w;
+    a.hits = (uint32_t*)(ws + L.hits); a.status = (int32_t*)(ws + L.status);
+    a.tlogits = (uint64_t*)(ws + L.tlog);
+    a.hello = (uint32_t*)(ws + L.hello);
+    a.epoch = (uint32_t*)(ws + L.pctr);
+    a.tact = (uint64_t*)(ws + L.tact);
+    if (d->flags & WM_FLAG_TIMELINE) a.timeline = (uint64_t*)(ws + L.timeline);
+    PhaseTimer pt(PH_STEP, s);
+    WM_FAIL_HIP(launch_persist(a, (size_t)lds, gut, dt, sgut, sdt, s));
+    return WM_OK;
+}
+
 // One launch of the fused step kernel; returns 1 when the type combination has
 // no fused instantiation (the caller then runs the per-phase kernels).
 static int run_fused(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, const float* x, float* out,
                      const int32_t* forced_ids, const float* forced_w, int32_t* ids, float* w, hipStream_t s) {
+    // the persistent kernel wins at top-K <= 4 (measured: 1 token of 64
+    // experts top-4, 512 experts top-3), the item-list kernel at top-10
+    const bool persist = !(d->flags & WM_FLAG_ITEM_KERNEL) && ((d->flags & WM_FLAG_PERSIST_KERNEL) || d->top_k <= 4);
+    if (persist) {
+        const int rc = run_persist(d, L, ws, x, out, forced_ids, forced_w, ids, w, s);
+        if (rc <= 0) return rc;
+    }
     const bool sh = has_shared(d);
     if (d->gate_type != d->up_type || (sh && d->sh_gate_type != d->sh_up_type)) return 1;
     const int gut = d->gate_type, dt = d->down_type;

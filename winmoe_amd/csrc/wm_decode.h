@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "wm_format.h"
+
 namespace wm {
 
 // Counters (uint32) inside the workspace, each alone in its own 256-byte line:
@@ -65,5 +67,88 @@ constexpr int DECODE_LDS = 65536;   // dynamic LDS of a decode-step workgroup (2
 
 bool decode_step_supported(int gut, int dt, int sgut, int sdt);
 int launch_decode_step(const DecodeArgs& a, int gut, int dt, int sgut, int sdt, hipStream_t s);
+
+}  // namespace wm
+
+// ------------------------------------------------------------------ persistent step
+// One workgroup per CU: PW streaming waves + 2 helper waves (router rows,
+// routing, operand staging, SwiGLU publishing, combine).  Internal.
+namespace wm {
+
+constexpr int PW = 8;                    // streaming waves per workgroup
+constexpr int PTHREADS = 64 * (PW + 2);  // + 2 helper waves
+constexpr int PRING = 3;                 // tiles in flight per streaming wave
+constexpr int PMAXK = 16;
+constexpr int P_TL = 32;                 // timeline words per workgroup
+constexpr int P_MAX_WG = 1024;           // workgroups (CUs) the workspace has start-tag words for
+constexpr int P_REP = 8;                 // replicas of the tagged logits (each read by 1/8 of the workgroups)
+constexpr int P_AREP = 4;                // replicas of the tagged SwiGLU outputs
+
+// Ring buffer bytes of one tile of type T: NI DMA units of 1 KB, except Q8_0
+// whose 5th unit is cut to the 4352-byte tile + 16 B of alignment shift (the
+// lanes beyond it issue no load) + over-read pad.
+template <int T> WM_HD constexpr int ring_tile_bytes() { return T == Q8_0 ? 4416 : (T == Q6_K ? 4096 : ((T == Q4_K || T == Q5_K) ? 3072 : 2048)); }
+WM_HD int ring_tile_bytes_rt(int t) { return t == Q8_0 ? 4416 : (t == Q6_K ? 4096 : ((t == Q4_K || t == Q5_K) ? 3072 : 2048)); }
+
+// LDS control block of one workgroup.  The streaming waves never use LDS
+// atomics (the compiler makes every LDS atomic wait for all of the wave's
+// LDS-DMA loads, which would drain its weight stream): each writes its own
+// words, and readers combine them.
+struct PersistCtl {
+    uint32_t progress[PW];         // streaming wave w: next tile-list entry it will process (all of its
+                                   // entries below are done); a large value when its list is done
+    uint32_t xop_built[PW];        // streaming wave w wrote its part of the x operand records
+    uint32_t routed;               // routing of this step is in ids / w / valid
+    uint32_t sgate_ready;          // sgate holds the shared-expert gate
+    uint32_t tag;                  // this launch's tag (epoch + 1)
+    uint32_t abort;                // a wait of this workgroup gave up: every later wait ends at once
+    uint32_t rows_in;              // x and the router rows are in LDS
+    uint32_t router_done[2];       // helper h is done with the router rows (their ring space is free)
+    uint32_t pad;
+    uint32_t act_ready[PMAXK + 1]; // the slot's SwiGLU operand records are in LDS
+    int32_t ids[PMAXK];
+    float w[PMAXK];
+    int32_t valid[PMAXK];
+    float sgate;
+    uint32_t pad2[2];
+    uint64_t t[P_TL];              // timeline (device clock)
+};
+
+struct PersistArgs {
+    int32_t H, I, E, K, has_shared, forced, nwg, rr;
+    int32_t gu_tiles, dn_tiles;        // tiles of one gate/up matrix (I rows) and of one down matrix (H rows)
+    int32_t n_rwaves;                  // streaming waves whose rings hold x and the router rows at the start
+    int32_t o_ring, ring_buf;          // LDS: streaming rings (PW x PRING buffers of ring_buf bytes)
+    int32_t x_region;                  // bytes of x / of one router row in the ring space
+    int32_t o_reg;                     // LDS: SwiGLU operand records [K+1][I/64]
+    int32_t o_xop, o_xop2;             // LDS: x operand records of the routed / shared gate-up types
+    int32_t o_gu, gu_cap;              // LDS: gate and up row sums [K+1][gu_cap] each
+    int32_t o_y, y_cap;                // LDS: down row sums [K+1][y_cap]
+    const float* x;
+    float* out;
+    const float* router;
+    const uint8_t* gate;
+    const uint8_t* up;
+    const uint8_t* down;
+    int64_t gstride, ustride, dstride;
+    const uint8_t* sh_gate;
+    const uint8_t* sh_up;
+    const uint8_t* sh_down;
+    const float* sh_gate_inp;
+    const int32_t* forced_ids;
+    const float* forced_w;
+    int32_t* ids;                      // trace slot of this step
+    float* w;
+    uint32_t* hits;
+    int32_t* status;
+    uint64_t* tlogits;                 // [P_REP][E] (tag << 32) | logit bits
+    uint32_t* hello;                   // [nwg] tag of the launch each workgroup started in
+    uint32_t* epoch;                   // launches completed since the workspace was reset
+    uint64_t* tact;                    // [K+1][P_AREP][I] (tag << 32) | SwiGLU output bits
+    uint64_t* timeline;                // NULL or [nwg][P_TL]
+};
+
+bool persist_supported(int gut, int dt, int sgut, int sdt);
+int launch_persist(const PersistArgs& a, size_t lds, int gut, int dt, int sgut, int sdt, hipStream_t s);
 
 }  // namespace wm

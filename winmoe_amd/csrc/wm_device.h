@@ -344,7 +344,9 @@ template <int T> WM_DEV float seg_dot(const Seg<T>& s, const XOp& x) {
         for (int i = 0; i < 9; i++) { h0 = dot4(s.q[i], x.hi[i], h0); l0 = dot4(s.q[i], x.lo[i], l0); }
 #pragma unroll
         for (int i = 9; i < 17; i++) { h1 = dot4(s.q[i], x.hi[i], h1); l1 = dot4(s.q[i], x.lo[i], l1); }
-        float r = s.a[0] * (float)(h0 * 256 + l0) + s.a[1] * (float)(h1 * 256 + l1);
+        // explicit fused multiply-adds: every kernel computes the same value
+        // whatever the compiler would otherwise contract (contraction is off)
+        const float r = fmaf(s.a[0], (float)(h0 * 256 + l0), s.a[1] * (float)(h1 * 256 + l1));
         return r * x.s;
     } else {
         constexpr int NR = Seg<T>::NRUN, DPR = 16 / NR;
@@ -355,7 +357,7 @@ template <int T> WM_DEV float seg_dot(const Seg<T>& s, const XOp& x) {
 #pragma unroll
             for (int i = run * DPR; i < (run + 1) * DPR; i++) { hs = dot4(s.q[i], x.hi[i], hs); ls = dot4(s.q[i], x.lo[i], ls); }
             int S = hs * 256 + ls - Seg<T>::BIAS * x.sum[run];
-            r += s.a[run] * (float)S - s.b[run] * (float)x.sum[run];
+            r += fmaf(s.a[run], (float)S, -(s.b[run] * (float)x.sum[run]));
         }
         return r * x.s;
     }
@@ -406,6 +408,18 @@ WM_DEV uint64_t swap_max_u64_halves(uint64_t v) {
     const auto h = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
     const auto l = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
     return max_u64(((uint64_t)h[0] << 32) | l[0], ((uint64_t)h[1] << 32) | l[1]);
+}
+
+// Maximum of a 32-bit value over the wave (all 64 lanes active), in every lane.
+WM_DEV uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_u32<DPP_XOR1>(v));
+    v = max(v, dpp_u32<DPP_XOR2>(v));
+    v = max(v, dpp_u32<DPP_HALF_MIRROR>(v));
+    v = max(v, dpp_u32<DPP_MIRROR>(v));
+    const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = max((uint32_t)a[0], (uint32_t)a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return max((uint32_t)b[0], (uint32_t)b[1]);
 }
 
 // Maximum of a 64-bit key over the wave (all 64 lanes active), in every lane:

@@ -1,0 +1,856 @@
+// wm_persist.hip -- one decode token through the MoE block in one launch of a
+// persistent kernel: one workgroup per CU, and every workgroup takes an equal
+// share of every phase of the step.
+//
+// Workgroup w of nwg (PW streaming waves + 2 helper waves):
+//   * router rows [w*rr, (w+1)*rr): reference-order fp32 logits, stored with
+//     this launch's tag in the upper 32 bits, in P_REP replicas;
+//   * gate/up tiles [tw0, tw1) of the shared expert and of every routed slot
+//     (the same row range in every slot);
+//   * down rows of its own output range [d0, d1) for every slot, which it
+//     then combines itself: out[h] = sum_k w_k y_k[h] + shared, in k order.
+// The streaming waves walk one tile list: shared gate/up, routed gate/up slot
+// 0 .. K-1, shared down, routed down slot 0 .. K-1, each wave taking the next
+// entry from an LDS counter and keeping PRING tiles in flight (LDS-DMA ring).
+// Row sums go to LDS.
+//
+// Hand-offs between workgroups carry the launch tag in every 64-bit word
+// (tag << 32 | value), so a reader needs one read of the data itself and no
+// counter: the routing (every workgroup reads one replica of the tagged
+// logits and runs the K-pass arg-max itself) and the SwiGLU outputs of each
+// slot (every workgroup writes its rows into P_AREP replicas; every workgroup
+// reads one replica back and builds the integer-dot operand records in LDS).
+// A stale word carries an older tag, so a reader never takes it.  The tag is
+// epoch + 1; workgroup 0 stores the new epoch at its end, after it has seen
+// every workgroup's start tag (so no workgroup can still read the old one).
+// Nothing is reset between launches; wm_workspace_reset zeroes the words.
+//
+// Helper 0: router DMA and rows 0/2, routing, operand records.  Helper 1:
+// rows 1/3, shared-expert gate, SwiGLU publishing, combine.
+//
+// Progress: every workgroup must be resident at once (the routing needs every
+// workgroup's router rows).  The host launches one workgroup per CU with more
+// than half the CU's LDS, so each CU holds exactly one; a workgroup delayed by
+// other work on the device only delays the step.  Every wait is bounded and
+// reports WM_STATUS_SPIN_TIMEOUT when it gives up.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "../../include/winmoe_hip.h"
+#include "wm_decode.h"
+#include "wm_device.h"
+#include "wm_launch.h"
+#include "wm_wave.h"
+
+namespace wm {
+
+static_assert(PRING == 3, "the streaming FIFO below holds three tiles");
+
+typedef __attribute__((address_space(3))) PersistCtl lctl_t;
+typedef __attribute__((address_space(3))) float lf32_t;
+
+constexpr uint32_t PSPIN = 1u << 20;    // LDS polls (~0.2 us each after the first few) before a wait gives up
+constexpr uint32_t PSPIN_G = 1u << 17;  // device-memory polls (~1 us each) before a wait gives up
+
+#define WM_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xC07F)
+
+WM_DEV uint32_t gld_agent(const uint32_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+WM_DEV uint64_t gld_agent64(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+WM_DEV void gst_agent(uint32_t* p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+WM_DEV void gst_agent64(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+WM_DEV uint64_t tagged(uint32_t tag, float v) { return ((uint64_t)tag << 32) | (uint64_t)__builtin_bit_cast(uint32_t, v); }
+
+// LDS flag / counter read.  A volatile load, not an atomic one: the compiler
+// treats an atomic LDS load as possibly depending on the wave's LDS-DMA tile
+// loads and waits for all of them first (vmcnt(0)), which would drain the
+// weight stream at every flag check.
+WM_DEV uint32_t lds_ld(const lds32_t* p) { return *(const volatile lds32_t*)p; }
+
+// Every LDS write of this wave is complete, then lane 0 stores v to *p (a
+// word with one writer; volatile, not atomic, for the reason above).
+WM_DEV void lds_set(lds32_t* p, uint32_t v, int lane) {
+    WM_WAIT_LGKM0();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (lane == 0) *(volatile lds32_t*)p = v;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// A wait gave up: report it and make every later wait of the workgroup end
+// at once (the step's results are invalid; the launch still finishes).
+WM_DEV void give_up(lctl_t* ctl, int32_t* status, int lane) {
+    if (lane == 0) {
+        atomicOr(status, WM_STATUS_SPIN_TIMEOUT);
+        *(volatile lds32_t*)&ctl->abort = 1u;
+    }
+}
+WM_DEV bool aborted(lctl_t* ctl) { return lds_ld(&ctl->abort) != 0u; }
+
+// Pause between polls: 64 clocks at first, doubling to 512.  Polling waves
+// share their SIMD with the streaming waves; every poll costs issue slots.
+WM_DEV void backoff(uint32_t it) {
+    if (it < 2) __builtin_amdgcn_s_sleep(1);
+    else if (it < 4) __builtin_amdgcn_s_sleep(2);
+    else if (it < 8) __builtin_amdgcn_s_sleep(4);
+    else __builtin_amdgcn_s_sleep(8);
+}
+
+// The wave waits until *p >= target (bounded).
+WM_DEV void lds_wait(lctl_t* ctl, const lds32_t* p, uint32_t target, int32_t* status, int lane) {
+    uint32_t it = 0;
+    while (lds_ld(p) < target) {
+        if (++it > PSPIN || aborted(ctl)) {
+            give_up(ctl, status, lane);
+            break;
+        }
+        backoff(it);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Smallest progress word of the streaming waves: every tile-list entry below
+// it has been processed.
+WM_DEV uint32_t min_progress(lctl_t* ctl) {
+    uint32_t m = lds_ld(&ctl->progress[0]);
+#pragma unroll
+    for (int w = 1; w < PW; w++) m = min(m, lds_ld(&ctl->progress[w]));
+    return m;
+}
+// The wave waits until every entry below `target` has been processed (bounded).
+WM_DEV void wait_progress(lctl_t* ctl, uint32_t target, int32_t* status, int lane) {
+    uint32_t it = 0;
+    while (min_progress(ctl) < target) {
+        if (++it > PSPIN || aborted(ctl)) {
+            give_up(ctl, status, lane);
+            break;
+        }
+        backoff(it);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// The wave waits until all n words at p are nonzero (bounded).
+WM_DEV void wait_all(lctl_t* ctl, const lds32_t* p, int n, int32_t* status, int lane) {
+    for (int i = 0; i < n; i++) lds_wait(ctl, p + i, 1u, status, lane);
+}
+
+WM_DEV uint64_t now() { return __builtin_amdgcn_s_memrealtime(); }
+
+// s_waitcnt vmcnt(n), n in [0, 10] (instructions of at most two later tiles).
+WM_DEV void wait_vm(int n) {
+    switch (n) {
+    case 0: WM_WAIT_VMCNT(0); break;
+    case 1: WM_WAIT_VMCNT(1); break;
+    case 2: WM_WAIT_VMCNT(2); break;
+    case 3: WM_WAIT_VMCNT(3); break;
+    case 4: WM_WAIT_VMCNT(4); break;
+    case 5: WM_WAIT_VMCNT(5); break;
+    case 6: WM_WAIT_VMCNT(6); break;
+    case 7: WM_WAIT_VMCNT(7); break;
+    case 8: WM_WAIT_VMCNT(8); break;
+    case 9: WM_WAIT_VMCNT(9); break;
+    default: WM_WAIT_VMCNT(10); break;
+    }
+}
+
+// The DMA loads of one tile of type T into a ring buffer (as tile_dma; for
+// Q8_0 the lanes whose 16 bytes would fall past the buffer issue nothing, so
+// a buffer holds 4416 bytes instead of 5 KB).  Returns the instruction count.
+template <int T> WM_DEV int ring_dma(const uint8_t* W, int64_t off, int64_t nbytes, int lane, lds8_t* dst) {
+    constexpr int NI = tile_ni<T>(), CAP = ring_tile_bytes<T>() / 16;
+    const uintptr_t G = (uintptr_t)(W + off);
+    const uintptr_t A = G & ~(uintptr_t)15;
+    const int nch = (int)(((G - A) + (uintptr_t)nbytes + 15) >> 4);
+#pragma unroll
+    for (int k = 0; k < NI; k++) {
+        int i = lane + 64 * k;
+        if (64 * k + 63 < CAP || i < CAP) {     // lane 0 always issues: every instruction counts
+            i = i < nch ? i : nch - 1;
+            __builtin_amdgcn_global_load_lds((const void*)(A + 16 * (uintptr_t)i),
+                                             (__attribute__((address_space(3))) void*)(dst + 1024 * k), 16, 0, CPOL_NT);
+        }
+    }
+    return NI;
+}
+
+// ------------------------------------------------------------------ tile list
+enum : int { K_SG = 0, K_SU = 1, K_RG = 2, K_RU = 3, K_SD = 4, K_RD = 5 };
+struct TRef {
+    int kind, slot, t;    // t: tile within the workgroup's range
+};
+
+// floor(j / d) for 0 <= j, d < 2^16 with m = floor((2^32 - 1) / d) + 1
+// (exact in that range; d == 1 is passed through).
+WM_DEV int fdiv(int j, int d, uint32_t m) { return d == 1 ? j : (int)__umulhi((uint32_t)j, m); }
+WM_HD uint32_t fdiv_magic(int d) { return d > 1 ? 0xFFFFFFFFu / (uint32_t)d + 1u : 0u; }
+
+struct Part {
+    int w, tw0, ngu, d0, ndn;
+};
+WM_DEV Part partition(const PersistArgs& a) {
+    Part p;
+    p.w = (int)blockIdx.x;
+    p.tw0 = (int)((int64_t)p.w * a.gu_tiles / a.nwg);
+    p.ngu = (int)((int64_t)(p.w + 1) * a.gu_tiles / a.nwg) - p.tw0;
+    p.d0 = (int)((int64_t)p.w * a.dn_tiles / a.nwg);
+    p.ndn = (int)((int64_t)(p.w + 1) * a.dn_tiles / a.nwg) - p.d0;
+    return p;
+}
+
+// The workgroup's tile list [shared gate/up] [routed gate/up, slot 0..K-1]
+// [shared down] [routed down, slot 0..K-1]; gate and up of a tile adjacent.
+struct TileList {
+    int K, sh, ngu, ndn, na, nb, nc, n;
+    uint32_t m2gu, mdn;
+    WM_DEV void init(int K_, int sh_, int ngu_, int ndn_) {
+        K = K_; sh = sh_; ngu = ngu_; ndn = ndn_;
+        na = sh ? 2 * ngu : 0;
+        nb = K * 2 * ngu;
+        nc = sh ? ndn : 0;
+        n = na + nb + nc + K * ndn;
+        m2gu = fdiv_magic(2 * ngu);
+        mdn = fdiv_magic(ndn);
+    }
+    // list position after the gate/up tiles of `slot` (slot K: shared)
+    WM_DEV int gu_end(int slot) const { return slot == K ? na : na + (slot + 1) * 2 * ngu; }
+    WM_DEV TRef at(int j) const {
+        TRef r;
+        if (j < na) {
+            r.kind = (j & 1) ? K_SU : K_SG; r.slot = K; r.t = j >> 1;
+            return r;
+        }
+        j -= na;
+        if (j < nb) {
+            const int q = fdiv(j, 2 * ngu, m2gu), rr = j - q * 2 * ngu;
+            r.kind = (rr & 1) ? K_RU : K_RG; r.slot = q; r.t = rr >> 1;
+            return r;
+        }
+        j -= nb;
+        if (j < nc) {
+            r.kind = K_SD; r.slot = K; r.t = j;
+            return r;
+        }
+        j -= nc;
+        const int q = fdiv(j, ndn, mdn);
+        r.kind = K_RD; r.slot = q; r.t = j - q * ndn;
+        return r;
+    }
+};
+
+// Slot at position q of the order shared, 0 .. K-1 (shared first when present).
+WM_DEV int slot_at(int q, int K, int sh) { return sh ? (q == 0 ? K : q - 1) : q; }
+
+// ------------------------------------------------------------------ streaming waves
+template <int GUT, int DT, int SGUT, int SDT>
+WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lane) {
+    lctl_t* ctl = (lctl_t*)smem;
+    lds8_t* lds = (lds8_t*)smem;
+    // the wave index is uniform: keep it (and every address derived from it,
+    // such as the LDS-DMA destinations that go to M0) in scalar registers
+    const int wave = __builtin_amdgcn_readfirstlane(wave_v);
+    const Part P = partition(a);
+    const int K = a.K, sh = a.has_shared, H = a.H, I = a.I, E = a.E;
+    TileList L;
+    L.init(K, sh, P.ngu, P.ndn);
+    lds8_t* ring = lds + a.o_ring + wave * PRING * a.ring_buf;
+    lf32_t* garr = (lf32_t*)(lds + a.o_gu);
+    lf32_t* uarr = garr + (K + 1) * a.gu_cap;
+    lf32_t* yarr = (lf32_t*)(lds + a.o_y);
+    const int nseg_dn = I / SEG;
+    // geometry (rows per tile, lanes per row: powers of two; a tile is 64
+    // segments, so every lane holds one)
+    const int lg_gu = 31 - __builtin_clz((unsigned)(H / SEG)), lg_dn = 31 - __builtin_clz((unsigned)(I / SEG));
+    const int rpt_gu = SEG >> lg_gu, rpt_dn = SEG >> lg_dn;
+    const int sub_gu = lane & ((1 << lg_gu) - 1), rig_gu = lane >> lg_gu;
+    const int sub_dn = lane & ((1 << lg_dn) - 1), rig_dn = lane >> lg_dn;
+    const int64_t rb_sg = matrix_bytes(SGUT, 1, H), rb_g = matrix_bytes(GUT, 1, H);
+    const int64_t rb_sd = matrix_bytes(SDT, 1, I), rb_d = matrix_bytes(DT, 1, I);
+
+    // routing in a register: lane k holds the expert id of slot k (-1 when
+    // invalid); read once, when the first routed tile comes up
+    int my_e = -1;
+    bool routed = false;
+
+    // Weights of a tile: matrix base (null for an invalid routed id), its
+    // rows, the tile index in the matrix, row bytes.
+    auto weights_of = [&](const TRef& r, int& rows, int& abs_t, int64_t& rb) -> const uint8_t* {
+        int e = 0;
+        if (r.kind == K_RG || r.kind == K_RU || r.kind == K_RD) {
+            e = __builtin_amdgcn_readlane(my_e, r.slot);
+            if (e < 0) return nullptr;
+        }
+        if (r.kind <= K_RU) {
+            rows = I; abs_t = P.tw0 + r.t;
+            switch (r.kind) {
+            case K_SG: rb = rb_sg; return a.sh_gate;
+            case K_SU: rb = rb_sg; return a.sh_up;
+            case K_RG: rb = rb_g; return a.gate + (int64_t)e * a.gstride;
+            default: rb = rb_g; return a.up + (int64_t)e * a.ustride;
+            }
+        }
+        rows = H; abs_t = P.d0 + r.t;
+        if (r.kind == K_SD) { rb = rb_sd; return a.sh_down; }
+        rb = rb_d;
+        return a.down + (int64_t)e * a.dstride;
+    };
+
+    // ---- FIFO of issued tiles: entry 0 is the oldest; an entry keeps the
+    // list index, instruction count, ring buffer and the tile's first byte
+    // (null: no weights).  Wave w takes the entries w, w + PW, ... of the list.
+    int j0 = 0, j1 = 0, j2 = 0, ni0 = 0, ni1 = 0, ni2 = 0, b0 = 0, b1 = 0, b2 = 0, cnt = 0, seq = 0;
+    const uint8_t *t0p = nullptr, *t1p = nullptr, *t2p = nullptr;
+    int pend = wave;
+
+    // Issue the next tile of the list; false when the list is done, or (when
+    // !block) when the next tile needs the routing and it is not known yet.
+    auto try_issue = [&](bool block) -> bool {
+        if (pend >= L.n) return false;
+        const TRef r = L.at(pend);
+        if (!routed && (r.kind == K_RG || r.kind == K_RU || r.kind == K_RD)) {
+            if (lds_ld(&ctl->routed) == 0u) {
+                if (!block) return false;
+                lds_wait(ctl, &ctl->routed, 1u, a.status, lane);
+            }
+            routed = true;
+            my_e = lane < K ? (ctl->valid[lane] ? ctl->ids[lane] : -1) : -1;
+            (void)E;
+        }
+        const int b = seq % PRING;
+        lds8_t* buf = ring + b * a.ring_buf;
+        int rows = 0, abs_t = 0;
+        int64_t rb = 0;
+        const uint8_t* W = weights_of(r, rows, abs_t, rb);
+        int ni = 0;
+        const uint8_t* tp = nullptr;
+        if (W) {
+            const int rpt = r.kind <= K_RU ? rpt_gu : rpt_dn;
+            const int64_t off = (int64_t)abs_t * rpt * rb, nbytes = (int64_t)min(rpt, rows - abs_t * rpt) * rb;
+            tp = W + off;
+            switch (r.kind) {
+            case K_SG: case K_SU: ni = ring_dma<SGUT>(W, off, nbytes, lane, buf); break;
+            case K_RG: case K_RU: ni = ring_dma<GUT>(W, off, nbytes, lane, buf); break;
+            case K_SD: ni = ring_dma<SDT>(W, off, nbytes, lane, buf); break;
+            default: ni = ring_dma<DT>(W, off, nbytes, lane, buf); break;
+            }
+        }
+        // (selects, not a branch per entry: the entries stay in registers)
+        j0 = cnt == 0 ? pend : j0; ni0 = cnt == 0 ? ni : ni0; b0 = cnt == 0 ? b : b0; t0p = cnt == 0 ? tp : t0p;
+        j1 = cnt == 1 ? pend : j1; ni1 = cnt == 1 ? ni : ni1; b1 = cnt == 1 ? b : b1; t1p = cnt == 1 ? tp : t1p;
+        j2 = cnt == 2 ? pend : j2; ni2 = cnt == 2 ? ni : ni2; b2 = cnt == 2 ? b : b2; t2p = cnt == 2 ? tp : t2p;
+        cnt++;
+        seq++;
+        pend += PW;
+        return true;
+    };
+
+    // operand in registers and what it is: 1000 + type (x) or the slot (act)
+    XOp xo;
+    int xkey = -1;
+    float sgate = 1.0f;
+    bool have_sgate = false;
+
+    // Row sums of the tile at the head of the FIFO (tp: its first byte in
+    // memory, null when it has no weights).
+    auto process = [&](int j, int b, const uint8_t* tp) {
+        const TRef r = L.at(j);
+        const lds8_t* buf = ring + b * a.ring_buf + (((uintptr_t)tp) & 15u);
+        auto rowsum = [&](auto tag_t, int lpr) -> float {
+            constexpr int T = decltype(tag_t)::value;
+            if (!tp) return 0.0f;
+            Seg<T> sg;
+            sg.load(buf, lane);
+            return row_reduce(seg_dot<T>(sg, xo), lpr);
+        };
+        if (r.kind <= K_RU) {
+            const bool shared = r.kind <= K_SU;
+            const int key = 1000 + (shared ? SGUT : GUT);
+            if (xkey != key) {
+                const int o = (shared && SGUT != GUT) ? a.o_xop2 : a.o_xop;
+                xop_read((const lds32_t*)(lds + o) + sub_gu * XOP_DW, xo);
+                xkey = key;
+            }
+            float p;
+            if (SGUT == GUT || !shared) p = rowsum(std::integral_constant<int, GUT>(), 1 << lg_gu);
+            else p = rowsum(std::integral_constant<int, SGUT>(), 1 << lg_gu);
+            const int local = r.t * rpt_gu + rig_gu, row = (P.tw0 + r.t) * rpt_gu + rig_gu;
+            if (sub_gu == (1 << lg_gu) - 1 && row < I) {
+                lf32_t* dst = (r.kind == K_SG || r.kind == K_RG) ? garr : uarr;
+                dst[r.slot * a.gu_cap + local] = p;
+            }
+        } else {
+            const bool shared = r.kind == K_SD;
+            if (xkey != r.slot) {
+                lds_wait(ctl, &ctl->act_ready[r.slot], 1u, a.status, lane);
+                xop_read((const lds32_t*)(lds + a.o_reg) + ((int64_t)r.slot * nseg_dn + sub_dn) * XOP_DW, xo);
+                xkey = r.slot;
+            }
+            float p;
+            if (SDT == DT || !shared) p = rowsum(std::integral_constant<int, DT>(), 1 << lg_dn);
+            else p = rowsum(std::integral_constant<int, SDT>(), 1 << lg_dn);
+            if (shared && a.sh_gate_inp) {
+                if (!have_sgate) {
+                    lds_wait(ctl, &ctl->sgate_ready, 1u, a.status, lane);
+                    sgate = ctl->sgate;
+                    have_sgate = true;
+                }
+                p = p * sgate;
+            }
+            const int local = r.t * rpt_dn + rig_dn, row = (P.d0 + r.t) * rpt_dn + rig_dn;
+            if (sub_dn == (1 << lg_dn) - 1 && row < H) yarr[r.slot * a.y_cap + local] = p;
+        }
+    };
+
+    // ---- x operand records (8 lanes per segment, 8 segments per wave) and
+    // the first tiles.  Waves whose rings hold the router rows build first and
+    // then wait for the helpers to finish with the rows; the others send
+    // their first tiles at once and build while those are in flight.
+    {
+        const int nseg = H / SEG, seg = wave * 8 + (lane >> 3), part = lane & 7;
+        const bool two = sh && SGUT != GUT;
+        const bool rwave = wave < a.n_rwaves;
+        float v[8], v2[8];
+        if (seg < nseg) {
+            xop_part_fetch<GUT>(a.x, seg, part, v);
+            if (two) xop_part_fetch<SGUT>(a.x, seg, part, v2);
+        }
+        if (!rwave) while (cnt < PRING && try_issue(false)) {}
+        if (seg < nseg) {
+            xop_part<GUT>(v, part, (lds32_t*)(lds + a.o_xop) + seg * XOP_DW);
+            if (two) xop_part<SGUT>(v2, part, (lds32_t*)(lds + a.o_xop2) + seg * XOP_DW);
+        }
+        lds_set(&ctl->xop_built[wave], 1u, lane);
+        if (rwave) {
+            wait_all(ctl, ctl->router_done, 2, a.status, lane);
+            while (cnt < PRING && try_issue(false)) {}
+        }
+    }
+    wait_all(ctl, ctl->xop_built, PW, a.status, lane);
+    if (wave == 0 && lane == 0) ctl->t[8] = now();
+
+    uint64_t c_wait = 0, c_proc = 0, c_issue = 0, n_tiles = 0;
+    while (true) {
+        uint64_t c0 = __builtin_amdgcn_s_memtime();
+        if (cnt == 0) {
+            if (!try_issue(true)) break;
+            while (cnt < PRING && try_issue(false)) {}
+        }
+        uint64_t c1 = __builtin_amdgcn_s_memtime();
+        wait_vm(cnt == 3 ? ni1 + ni2 : (cnt == 2 ? ni1 : 0));
+        uint64_t c2 = __builtin_amdgcn_s_memtime();
+        process(j0, b0, t0p);
+        // progress after the row sums (LDS executes one wave's writes in order)
+        if (lane == 0) *(volatile lds32_t*)&ctl->progress[wave] = (uint32_t)(j0 + PW);
+        wave_lds_sync();          // every lane's reads of the buffer are done before it is refilled
+        uint64_t c3 = __builtin_amdgcn_s_memtime();
+        j0 = j1; ni0 = ni1; b0 = b1; t0p = t1p;
+        j1 = j2; ni1 = ni2; b1 = b2; t1p = t2p;
+        cnt--;
+        while (cnt < PRING && try_issue(false)) {}
+        uint64_t c4 = __builtin_amdgcn_s_memtime();
+        c_wait += c2 - c1; c_proc += c3 - c2; c_issue += (c1 - c0) + (c4 - c3); n_tiles++;
+    }
+    lds_set(&ctl->progress[wave], 0xFFFFFFFFu, lane);
+    if (wave == 0 && lane == 0) {
+        ctl->t[9] = now();
+        ctl->t[12] = c_wait; ctl->t[13] = c_proc; ctl->t[14] = c_issue; ctl->t[15] = n_tiles;
+    }
+}
+
+// ------------------------------------------------------------------ helpers: router rows
+
+// x and router rows [r0, r0 + nr) into LDS regions of `region` bytes (x
+// first, then the rows; 16-byte aligned sources; x with the default policy,
+// the rows non-temporal), all in flight together.
+WM_DEV void router_dma(const float* x, const float* W, int H, int r0, int nr, lds8_t* dst0, int region, int lane) {
+    const int64_t nbytes = (int64_t)H * 4;
+    const int units = (int)((nbytes + 1023) >> 10);
+    const int nch = (int)((nbytes + 15) >> 4);
+    for (int q = 0; q <= nr; q++) {
+        const uint8_t* src = (const uint8_t*)(q == 0 ? x : W + (int64_t)(r0 + q - 1) * H);
+        lds8_t* dst = dst0 + q * region;
+        for (int k = 0; k < units; k++) {
+            int i = lane + 64 * k;
+            i = i < nch ? i : nch - 1;
+            if (q == 0)
+                __builtin_amdgcn_global_load_lds((const void*)(src + 16 * i),
+                                                 (__attribute__((address_space(3))) void*)(dst + 1024 * k), 16, 0, 0);
+            else
+                __builtin_amdgcn_global_load_lds((const void*)(src + 16 * i),
+                                                 (__attribute__((address_space(3))) void*)(dst + 1024 * k), 16, 0,
+                                                 CPOL_NT);
+        }
+    }
+    WM_WAIT_VMCNT(0);
+}
+
+// Router logits of up to two of the rows in LDS: lanes 16i .. 16i+15 take row
+// rsel i (none when < 0), in the reference order (transformer.h:172-191; as
+// wg_router_rows): lane c of a row keeps the running fp32 FMA over columns
+// c, c+16, ...; xor tree 8, 4, 2, 1 over the 16 lanes; lane 0 of the row adds
+// the scalar tail.  The LDS reads of the next 16 steps are issued before the
+// FMAs of the current ones.  Each logit goes with the tag in its upper 32
+// bits into all P_REP replicas (lane r of the row stores replica r).
+WM_DEV void router_chains(const lds8_t* lx, int region, int H, int r0, int ra, int rb, int E, uint32_t tag,
+                          uint64_t* tlogits, int lane) {
+    const int q = lane >> 4, c = lane & 15;
+    const int row = q == 0 ? ra : (q == 1 ? rb : -1);
+    const lf32_t* xr = (const lf32_t*)lx;
+    const lf32_t* wr = (const lf32_t*)(lx + (1 + (row >= 0 ? row : 0)) * region);
+    const int H16 = H - (H & 15), nsteps = H16 / 16;
+    float acc = 0.0f;
+    int s = 0;
+    if (nsteps >= 16) {
+        float wa[16], xa[16], wb[16], xb[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) { wa[j] = wr[c + 16 * j]; xa[j] = xr[c + 16 * j]; }
+        for (; s + 32 <= nsteps; s += 32) {
+#pragma unroll
+            for (int j = 0; j < 16; j++) { wb[j] = wr[c + 16 * (s + 16 + j)]; xb[j] = xr[c + 16 * (s + 16 + j)]; }
+#pragma unroll
+            for (int j = 0; j < 16; j++) acc = fmaf(wa[j], xa[j], acc);
+            const int sn = min(s + 32, nsteps - 16);        // next block (a repeat at the end is never used)
+#pragma unroll
+            for (int j = 0; j < 16; j++) { wa[j] = wr[c + 16 * (sn + j)]; xa[j] = xr[c + 16 * (sn + j)]; }
+#pragma unroll
+            for (int j = 0; j < 16; j++) acc = fmaf(wb[j], xb[j], acc);
+        }
+        if (s + 16 <= nsteps) {
+#pragma unroll
+            for (int j = 0; j < 16; j++) acc = fmaf(wa[j], xa[j], acc);
+            s += 16;
+        }
+    }
+    for (; s < nsteps; s++) acc = fmaf(wr[c + 16 * s], xr[c + 16 * s], acc);
+    acc += dpp_f32<DPP_ROR8>(acc);
+    acc += dpp_f32<DPP_ROR4>(acc);
+    acc += dpp_f32<DPP_ROR2>(acc);
+    acc += dpp_f32<DPP_ROR1>(acc);
+    if (c == 0)
+        for (int col = H16; col < H; col++) acc = fmaf(wr[col], xr[col], acc);
+    acc = __shfl(acc, lane & ~15);                  // the row's total (lane 0 of the row) in all its lanes
+    if (row >= 0 && c < P_REP) gst_agent64(tlogits + (int64_t)c * E + r0 + row, tagged(tag, acc));
+}
+
+// Routing from replica `rep` of the tagged logits (polled, with a pause
+// between polls, until every one carries `tag`), then the K-pass arg-max and
+// softmax of wave_topk_n.  Lanes k < K return their pick (id, weight).
+template <int MAXV>
+WM_DEV void route_tagged(const PersistArgs& a, lctl_t* ctl, int rep, uint32_t tag, int lane, int& my_e, float& wk,
+                         bool& degenerate, bool& nonfinite) {
+    const int E = a.E, K = a.K;
+    const uint64_t* src = a.tlogits + (int64_t)rep * E;
+    // the first read takes every logit; later polls re-read only the words
+    // that still carry an older tag (a poll of the whole vector by every
+    // workgroup would take bandwidth from the weight streams)
+    uint64_t tv[MAXV];
+#pragma unroll
+    for (int i = 0; i < MAXV; i++) tv[i] = gld_agent64(src + min(lane + 64 * i, E - 1));
+    uint32_t it = 0;
+    while (true) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < MAXV; i++) ok = ok && (uint32_t)(tv[i] >> 32) == tag;
+        if (__builtin_amdgcn_ballot_w64(!ok) == 0ull) break;
+        if (++it > PSPIN_G || aborted(ctl)) {
+            give_up(ctl, a.status, lane);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(8);
+#pragma unroll
+        for (int i = 0; i < MAXV; i++)
+            if ((uint32_t)(tv[i] >> 32) != tag) tv[i] = gld_agent64(src + min(lane + 64 * i, E - 1));
+    }
+    if (lane == 0) ctl->t[11] = now();
+    float lv[MAXV];
+#pragma unroll
+    for (int i = 0; i < MAXV; i++) lv[i] = __builtin_bit_cast(float, (uint32_t)tv[i]);
+    Picker<MAXV> pk;
+    pk.init_vals(lv, E, lane);
+    float my_v = 0.0f;
+    my_e = 0;
+    degenerate = false;
+    for (int k = 0; k < K; k++) {
+        const uint64_t best = pk.next();
+        degenerate = degenerate || best == 0ull;
+        if (lane == k) { my_e = Picker<MAXV>::id_of(best); my_v = pk.value_of(best); }
+    }
+    const bool mine = lane < K;
+    float wmax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_v), 0));
+    for (int k = 1; k < K; k++) {
+        const float vk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_v), k));
+        if (vk > wmax) wmax = vk;
+    }
+    const float ex = mine ? expf(my_v - wmax) : 0.0f;
+    float wsum = 0.0f;
+    for (int k = 0; k < K; k++) wsum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), k));
+    wk = wsum > 0.0f ? ex / wsum : ex;
+    nonfinite = __builtin_amdgcn_ballot_w64(mine && !isfinite(wk)) != 0ull;
+}
+
+// Operand records of the slots at positions q0 .. q0+n-1 of the down order
+// (n * passes <= 4, a pass = 8 segments, 8 lanes per segment, 8 values per
+// lane): reads replica `rep` of their tagged SwiGLU outputs, all loads in
+// flight together, until every word carries `tag`, then builds the records.
+template <int DT, int SDT>
+WM_DEV void stage_batch(const PersistArgs& a, lctl_t* ctl, lds8_t* lds, int q0, int n, uint32_t tag, int rep,
+                        int lane) {
+    const int K = a.K, sh = a.has_shared, I = a.I, nseg = I / SEG, passes = (nseg + 7) / 8;
+    const int part = lane & 7;
+    uint64_t tv[4][8];
+    int slot[4], seg[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int q = q0 + i / passes;
+        slot[i] = slot_at(q, K, sh);
+        seg[i] = (i % passes) * 8 + (lane >> 3);
+    }
+    uint32_t it = 0;
+    while (true) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const bool on = i < n * passes && seg[i] < nseg;
+            const int col = on ? (slot[i] == K ? seg_col(SDT, seg[i], 8 * part) : seg_col(DT, seg[i], 8 * part)) : 0;
+            const uint64_t* src = a.tact + ((int64_t)slot[i] * P_AREP + rep) * I + col;
+#pragma unroll
+            for (int j = 0; j < 8; j++) tv[i][j] = on ? gld_agent64(src + j) : tagged(tag, 0.0f);
+        }
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) ok = ok && (uint32_t)(tv[i][j] >> 32) == tag;
+        if (__builtin_amdgcn_ballot_w64(!ok) == 0ull) break;
+        if (++it > PSPIN_G || aborted(ctl)) {
+            give_up(ctl, a.status, lane);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(8);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if (i < n * passes && seg[i] < nseg) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = __builtin_bit_cast(float, (uint32_t)tv[i][j]);
+            lds32_t* rec = (lds32_t*)(lds + a.o_reg) + ((int64_t)slot[i] * nseg + seg[i]) * XOP_DW;
+            if (slot[i] == K) xop_part<SDT>(v, part, rec);
+            else xop_part<DT>(v, part, rec);
+        }
+    }
+    for (int i = 0; i < n; i++) lds_set(&ctl->act_ready[slot_at(q0 + i, K, sh)], 1u, lane);
+}
+
+// ------------------------------------------------------------------ helper 0: router rows, routing, operand records
+
+template <int GUT, int DT, int SGUT, int SDT>
+WM_DEV void helper_router(const PersistArgs& a, uint8_t* smem, int lane) {
+    lctl_t* ctl = (lctl_t*)smem;
+    lds8_t* lds = (lds8_t*)smem;
+    const Part P = partition(a);
+    const int K = a.K, E = a.E;
+    const uint64_t t0 = now();
+    const uint32_t tag = gld_agent(a.epoch) + 1u;
+    if (lane == 0) {
+        ctl->t[0] = t0;
+        ctl->tag = tag;
+        gst_agent(a.hello + P.w, tag);
+    }
+    int my_e = 0;
+    float wk = 0.0f;
+    bool valid = false;
+    if (!a.forced) {
+        const int r0 = P.w * a.rr, nr = max(0, min(a.rr, E - r0));
+        if (nr > 0) router_dma(a.x, a.router, a.H, r0, nr, lds + a.o_ring, a.x_region, lane);
+        lds_set(&ctl->rows_in, 1u, lane);          // (also when this workgroup has no router rows)
+        if (lane == 0) ctl->t[1] = now();
+        if (nr > 0)   // rows 0 and 2 here, rows 1 and 3 on the other helper
+            router_chains(lds + a.o_ring, a.x_region, a.H, r0, 0, nr > 2 ? 2 : -1, E, tag, a.tlogits, lane);
+        lds_set(&ctl->router_done[0], 1u, lane);
+        if (lane == 0) ctl->t[2] = now();
+        bool degenerate = false, nonfinite = false;
+        if (E <= 512) route_tagged<8>(a, ctl, P.w % P_REP, tag, lane, my_e, wk, degenerate, nonfinite);
+        else route_tagged<16>(a, ctl, P.w % P_REP, tag, lane, my_e, wk, degenerate, nonfinite);
+        valid = lane < K;
+        if (P.w == 0) {
+            if (lane < K) {
+                a.ids[lane] = my_e;
+                a.w[lane] = wk;
+                if (a.hits) atomicAdd(a.hits + my_e, 1u);
+            }
+            const int st = (degenerate ? WM_STATUS_DEGENERATE_ROUTING : 0) | (nonfinite ? WM_STATUS_NONFINITE_WEIGHT : 0);
+            if (lane == 0 && st) atomicOr(a.status, st);
+        }
+    } else {
+        lds_set(&ctl->rows_in, 1u, lane);
+        lds_set(&ctl->router_done[0], 1u, lane);
+        if (lane < K) {
+            my_e = a.forced_ids[lane];
+            wk = a.forced_w[lane];
+            valid = my_e >= 0 && my_e < E;
+            if (P.w == 0) {
+                a.ids[lane] = my_e;
+                a.w[lane] = wk;
+                if (valid) { if (a.hits) atomicAdd(a.hits + my_e, 1u); }
+                else atomicOr(a.status, WM_STATUS_BAD_EXPERT_ID);
+            }
+        }
+    }
+    if (lane < K) {
+        ctl->ids[lane] = my_e;
+        ctl->w[lane] = valid ? wk : 0.0f;
+        ctl->valid[lane] = valid ? 1 : 0;
+    }
+    lds_set(&ctl->routed, 1u, lane);
+    if (lane == 0) ctl->t[3] = now();
+
+    // ---- stager: the operand records of every slot, in down order.  The
+    // next slot is read once this workgroup has finished its own gate/up
+    // tiles of it (the others finish theirs at about the same time), together
+    // with the following slots this workgroup has also finished (up to 4
+    // passes of loads in flight).
+    if (P.ndn > 0) {
+        TileList L;
+        L.init(K, a.has_shared, P.ngu, P.ndn);
+        const int nq = K + a.has_shared, passes = (a.I / SEG + 7) / 8, maxb = max(1, 4 / passes);
+        for (int q = 0; q < nq;) {
+            wait_progress(ctl, (uint32_t)L.gu_end(slot_at(q, K, a.has_shared)), a.status, lane);
+            int n = 1;
+            while (n < maxb && q + n < nq && min_progress(ctl) >= (uint32_t)L.gu_end(slot_at(q + n, K, a.has_shared)))
+                n++;
+            stage_batch<DT, SDT>(a, ctl, lds, q, n, tag, P.w % P_AREP, lane);
+            q += n;
+        }
+    }
+    if (lane == 0) ctl->t[5] = now();
+}
+
+// ------------------------------------------------------------------ helper 1: router rows, shared gate, SwiGLU publisher, combine
+
+template <int GUT, int DT, int SGUT, int SDT>
+WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
+    lctl_t* ctl = (lctl_t*)smem;
+    lds8_t* lds = (lds8_t*)smem;
+    const Part P = partition(a);
+    const int K = a.K, sh = a.has_shared, nq = K + sh;
+    lds_wait(ctl, &ctl->rows_in, 1u, a.status, lane);
+    const uint32_t tag = ctl->tag;
+    if (!a.forced) {
+        const int r0 = P.w * a.rr, nr = max(0, min(a.rr, a.E - r0));
+        if (nr > 1) router_chains(lds + a.o_ring, a.x_region, a.H, r0, 1, nr > 3 ? 3 : -1, a.E, tag, a.tlogits, lane);
+    }
+    lds_set(&ctl->router_done[1], 1u, lane);
+    if (sh && a.sh_gate_inp) {
+        const float g = wave_shgate(a.x, a.sh_gate_inp, a.H, lane);
+        if (lane == 0) ctl->sgate = g;
+    }
+    lds_set(&ctl->sgate_ready, 1u, lane);
+
+    lf32_t* garr = (lf32_t*)(lds + a.o_gu);
+    lf32_t* uarr = garr + (K + 1) * a.gu_cap;
+    lf32_t* yarr = (lf32_t*)(lds + a.o_y);
+    TileList L;
+    L.init(K, sh, P.ngu, P.ndn);
+    if (P.ngu > 0) {
+        const int rpt = geometry(GUT, a.H).rpt;
+        const int row0 = P.tw0 * rpt, nrows = min(a.I, (P.tw0 + P.ngu) * rpt) - row0;
+        for (int q = 0; q < nq; q++) {
+            const int slot = slot_at(q, K, sh);
+            wait_progress(ctl, (uint32_t)L.gu_end(slot), a.status, lane);
+            if (lane == 0 && q < 12) ctl->t[16 + q] = now();
+            const bool valid = slot == K || ctl->valid[slot] != 0;
+            uint64_t* dst = a.tact + (int64_t)slot * P_AREP * a.I + row0;
+            // rows x replicas over the lanes, one tagged word each
+            for (int i = lane; i < nrows * P_AREP; i += 64) {
+                const int r = i / P_AREP, rp = i - r * P_AREP;
+                const float v = valid ? silu_mul(garr[slot * a.gu_cap + r], uarr[slot * a.gu_cap + r]) : 0.0f;
+                gst_agent64(dst + (int64_t)rp * a.I + r, tagged(tag, v));
+            }
+        }
+    }
+    if (lane == 0) ctl->t[4] = now();
+    if (P.ndn > 0) {
+        wait_progress(ctl, (uint32_t)L.n, a.status, lane);
+        if (lane == 0) ctl->t[6] = now();
+        const int rpt = geometry(DT, a.I).rpt;
+        const int h0 = P.d0 * rpt, nrows = min(a.H, (P.d0 + P.ndn) * rpt) - h0;
+        for (int r = lane; r < nrows; r += 64) {
+            // out[h] = sum_k w_k y_k[h] (k order, invalid ids skipped) + gate * y_shared[h]
+            float acc = 0.0f;
+            for (int k = 0; k < K; k++)
+                if (ctl->valid[k]) acc = fmaf(ctl->w[k], yarr[k * a.y_cap + r], acc);
+            if (sh) acc = acc + yarr[K * a.y_cap + r];
+            a.out[h0 + r] = acc;
+        }
+    }
+
+    if (P.w == 0) {
+        // every workgroup has read the old epoch once all have posted this tag
+        for (int i = lane; i < a.nwg; i += 64) {
+            uint32_t it = 0;
+            while (gld_agent(a.hello + i) != tag) {
+                if (++it > PSPIN_G || aborted(ctl)) {
+                    atomicOr(a.status, WM_STATUS_SPIN_TIMEOUT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+        if (lane == 0) gst_agent(a.epoch, tag);
+    }
+    if (lane == 0) ctl->t[7] = now();
+    if (a.timeline && lane < P_TL) a.timeline[(int64_t)P.w * P_TL + lane] = ctl->t[lane];
+}
+
+// ------------------------------------------------------------------ kernel
+
+template <int GUT, int DT, int SGUT, int SDT>
+__global__ __launch_bounds__(PTHREADS) void k_decode_persist(PersistArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    for (int i = threadIdx.x; i < (int)(sizeof(PersistCtl) / 4); i += PTHREADS)
+        ((lds32_t*)(lds8_t*)smem)[i] = i < PW ? (uint32_t)i : 0u;     // progress[w] = w: wave w's first entry
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (wave < PW) stream_wave<GUT, DT, SGUT, SDT>(a, smem, wave, lane);
+    else if (wave == PW) helper_router<GUT, DT, SGUT, SDT>(a, smem, lane);
+    else helper_publish<GUT, DT, SGUT, SDT>(a, smem, lane);
+}
+
+template <int GUT, int DT, int SGUT, int SDT>
+static int launch_p(const PersistArgs& a, size_t lds, hipStream_t s) {
+    static size_t configured = 0;
+    if (configured < lds) {
+        hipError_t e = hipFuncSetAttribute((const void*)k_decode_persist<GUT, DT, SGUT, SDT>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return (int)e;
+        configured = lds;
+    }
+    hipLaunchKernelGGL((k_decode_persist<GUT, DT, SGUT, SDT>), dim3(a.nwg), dim3(PTHREADS), lds, s, a);
+    return (int)hipGetLastError();
+}
+
+#define WM_P_CASE(g, d, sg, sd) \
+    if (gut == g && dt == d && sgut == sg && sdt == sd) return launch_p<g, d, sg, sd>(a, lds, s);
+
+int launch_persist(const PersistArgs& a, size_t lds, int gut, int dt, int sgut, int sdt, hipStream_t s) {
+    WM_P_CASE(Q8_0, Q8_0, Q8_0, Q8_0)
+    WM_P_CASE(Q2_K, Q2_K, Q2_K, Q2_K)
+    WM_P_CASE(Q3_K, Q3_K, Q3_K, Q3_K)
+    WM_P_CASE(Q4_K, Q4_K, Q4_K, Q4_K)
+    WM_P_CASE(Q5_K, Q5_K, Q5_K, Q5_K)
+    WM_P_CASE(Q6_K, Q6_K, Q6_K, Q6_K)
+    WM_P_CASE(Q4_K, Q6_K, Q8_0, Q8_0)
+    WM_P_CASE(Q4_K, Q6_K, Q4_K, Q6_K)
+    WM_P_CASE(Q4_K, Q5_K, Q8_0, Q8_0)
+    WM_P_CASE(Q4_K, Q5_K, Q4_K, Q5_K)
+    WM_P_CASE(Q2_K, Q3_K, Q8_0, Q8_0)
+    WM_P_CASE(Q2_K, Q3_K, Q2_K, Q3_K)
+    return -1;
+}
+
+bool persist_supported(int gut, int dt, int sgut, int sdt) { return decode_step_supported(gut, dt, sgut, sdt); }
+
+}  // namespace wm

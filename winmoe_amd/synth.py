@@ -129,11 +129,14 @@ def build_layer(cfg: LayerConfig, device="cuda", layer_index: int = 0, max_token
     return SynthLayer(cfg, layer, router, gate, up, down, shared)
 
 
-def twin_layer(sl: SynthLayer, multi_kernel: bool) -> MoELayer:
-    """A second MoELayer over the same device tensors (own workspace)."""
+def twin_layer(sl: SynthLayer, multi_kernel: bool, flags: int = 0) -> MoELayer:
+    """A second MoELayer over the same device tensors (own workspace); flags
+    are extra wm_layer_desc.flags bits (the kernel choice)."""
     c = sl.cfg
-    return MoELayer(c.H, c.I, sl.layer.E, c.K, sl.router, sl.gate, sl.up, sl.down, c.types, shared=sl.shared,
-                    max_tokens=sl.layer.max_tokens, multi_kernel=multi_kernel)
+    m = MoELayer(c.H, c.I, sl.layer.E, c.K, sl.router, sl.gate, sl.up, sl.down, c.types, shared=sl.shared,
+                 max_tokens=sl.layer.max_tokens, multi_kernel=multi_kernel)
+    m.desc.flags |= flags
+    return m
 
 
 def make_hidden(cfg: LayerConfig, device="cuda", tokens: Optional[int] = None, seed_offset: int = 0) -> torch.Tensor:
