@@ -92,7 +92,7 @@ def measured_traffic(cfg):
     """HBM bytes per launch of the fused kernel from the committed rocprofv3
     PMC summary for this workload (FETCH_SIZE + WRITE_SIZE, scaled by the copy
     kernel calibration), or None when there is none."""
-    path = os.path.join(ROOT, "profiles", f"k_decode_step_{cfg.name}_traffic.json")
+    path = os.path.join(ROOT, "profiles", f"k_decode_persist_{cfg.name}_traffic.json")
     try:
         with open(path) as f:
             return json.load(f).get("traffic_bytes_per_launch")
@@ -277,7 +277,8 @@ def main():
         ach = per_launch / (launch_us * 1e-6) / 1e9
         roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                     "frac": round(ach / PEAK_HBM_GBPS, 4), "traffic": measured_traffic(cfg),
-                    "kernel": "k_decode_step (fused decode step, 1 launch per layer per token)",
+                    "kernel": "k_decode_persist (fused decode step: one persistent workgroup per CU, "
+                              "1 launch per layer per token)",
                     "bytes_per_launch": per_launch, "avg_launch_us": round(launch_us, 2)}
     elif "gate_up_swiglu" in phases:
         gu = phases["gate_up_swiglu"]

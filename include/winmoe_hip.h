@@ -62,11 +62,10 @@ enum {
  * every workgroup resident at once, every supported type pair, inter ==
  * inter_shared and the LDS budget of one workgroup per CU) and the
  * work-item-list kernel (one workgroup per work item, items wait only for
- * smaller ids).  By default the persistent kernel runs layers with top_k <= 4
- * that fit it (it is the faster one there; at top-10 the item-list kernel is)
- * and the item-list kernel everything else.  WM_FLAG_ITEM_KERNEL always picks
- * the item-list kernel; WM_FLAG_PERSIST_KERNEL picks the persistent kernel
- * whenever the layer fits it. */
+ * smaller ids).  By default the persistent kernel runs every layer that fits
+ * it and the item-list kernel everything else; WM_FLAG_ITEM_KERNEL always
+ * picks the item-list kernel.  WM_FLAG_PERSIST_KERNEL is the default choice,
+ * stated explicitly. */
 #define WM_FLAG_ITEM_KERNEL 4
 #define WM_FLAG_PERSIST_KERNEL 8
 

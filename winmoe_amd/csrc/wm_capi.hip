@@ -529,10 +529,7 @@ static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
 // no fused instantiation (the caller then runs the per-phase kernels).
 static int run_fused(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, const float* x, float* out,
                      const int32_t* forced_ids, const float* forced_w, int32_t* ids, float* w, hipStream_t s) {
-    // the persistent kernel wins at top-K <= 4 (measured: 1 token of 64
-    // experts top-4, 512 experts top-3), the item-list kernel at top-10
-    const bool persist = !(d->flags & WM_FLAG_ITEM_KERNEL) && ((d->flags & WM_FLAG_PERSIST_KERNEL) || d->top_k <= 4);
-    if (persist) {
+    if (!(d->flags & WM_FLAG_ITEM_KERNEL)) {
         const int rc = run_persist(d, L, ws, x, out, forced_ids, forced_w, ids, w, s);
         if (rc <= 0) return rc;
     }

@@ -76,8 +76,9 @@ int launch_decode_step(const DecodeArgs& a, int gut, int dt, int sgut, int sdt, 
 namespace wm {
 
 constexpr int PW = 8;                    // streaming waves per workgroup
-constexpr int PTHREADS = 64 * (PW + 2);  // + 2 helper waves
-constexpr int PRING = 3;                 // tiles in flight per streaming wave
+constexpr int PSTAGE = 2;                // operand staging waves (the first is also the router wave)
+constexpr int PTHREADS = 64 * (PW + 1 + PSTAGE);  // + publisher + stagers
+constexpr int PRING = 2;                 // ring buffers per streaming wave
 constexpr int PMAXK = 16;
 constexpr int P_TL = 32;                 // timeline words per workgroup
 constexpr int P_MAX_WG = 1024;           // workgroups (CUs) the workspace has start-tag words for

@@ -46,7 +46,7 @@
 
 namespace wm {
 
-static_assert(PRING == 3, "the streaming FIFO below holds three tiles");
+static_assert(PRING >= 1 && PRING <= 3, "the streaming FIFO below holds one to three tiles");
 
 typedef __attribute__((address_space(3))) PersistCtl lctl_t;
 typedef __attribute__((address_space(3))) float lf32_t;
@@ -304,6 +304,7 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
     int j0 = 0, j1 = 0, j2 = 0, ni0 = 0, ni1 = 0, ni2 = 0, b0 = 0, b1 = 0, b2 = 0, cnt = 0, seq = 0;
     const uint8_t *t0p = nullptr, *t1p = nullptr, *t2p = nullptr;
     int pend = wave;
+    uint64_t c_dma = 0;
 
     // Issue the next tile of the list; false when the list is done, or (when
     // !block) when the next tile needs the routing and it is not known yet.
@@ -330,12 +331,14 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
             const int rpt = r.kind <= K_RU ? rpt_gu : rpt_dn;
             const int64_t off = (int64_t)abs_t * rpt * rb, nbytes = (int64_t)min(rpt, rows - abs_t * rpt) * rb;
             tp = W + off;
+            const uint64_t d0 = __builtin_amdgcn_s_memtime();
             switch (r.kind) {
             case K_SG: case K_SU: ni = ring_dma<SGUT>(W, off, nbytes, lane, buf); break;
             case K_RG: case K_RU: ni = ring_dma<GUT>(W, off, nbytes, lane, buf); break;
             case K_SD: ni = ring_dma<SDT>(W, off, nbytes, lane, buf); break;
             default: ni = ring_dma<DT>(W, off, nbytes, lane, buf); break;
             }
+            c_dma += __builtin_amdgcn_s_memtime() - d0;
         }
         // (selects, not a branch per entry: the entries stay in registers)
         j0 = cnt == 0 ? pend : j0; ni0 = cnt == 0 ? ni : ni0; b0 = cnt == 0 ? b : b0; t0p = cnt == 0 ? tp : t0p;
@@ -422,6 +425,14 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
             xop_part<GUT>(v, part, (lds32_t*)(lds + a.o_xop) + seg * XOP_DW);
             if (two) xop_part<SGUT>(v2, part, (lds32_t*)(lds + a.o_xop2) + seg * XOP_DW);
         }
+        for (int sg = seg + PW * 8; sg < nseg; sg += PW * 8) {     // hidden sizes beyond PW * 8 segments
+            xop_part_fetch<GUT>(a.x, sg, part, v);
+            xop_part<GUT>(v, part, (lds32_t*)(lds + a.o_xop) + sg * XOP_DW);
+            if (two) {
+                xop_part_fetch<SGUT>(a.x, sg, part, v2);
+                xop_part<SGUT>(v2, part, (lds32_t*)(lds + a.o_xop2) + sg * XOP_DW);
+            }
+        }
         lds_set(&ctl->xop_built[wave], 1u, lane);
         if (rwave) {
             wait_all(ctl, ctl->router_done, 2, a.status, lane);
@@ -431,7 +442,7 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
     wait_all(ctl, ctl->xop_built, PW, a.status, lane);
     if (wave == 0 && lane == 0) ctl->t[8] = now();
 
-    uint64_t c_wait = 0, c_proc = 0, c_issue = 0, n_tiles = 0;
+    uint64_t c_wait = 0, c_proc = 0, c_issue = 0, n_tiles = 0, c_pgu = 0, n_gu = 0;
     while (true) {
         uint64_t c0 = __builtin_amdgcn_s_memtime();
         if (cnt == 0) {
@@ -441,6 +452,7 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
         uint64_t c1 = __builtin_amdgcn_s_memtime();
         wait_vm(cnt == 3 ? ni1 + ni2 : (cnt == 2 ? ni1 : 0));
         uint64_t c2 = __builtin_amdgcn_s_memtime();
+        const int jp = j0;
         process(j0, b0, t0p);
         // progress after the row sums (LDS executes one wave's writes in order)
         if (lane == 0) *(volatile lds32_t*)&ctl->progress[wave] = (uint32_t)(j0 + PW);
@@ -452,11 +464,13 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
         while (cnt < PRING && try_issue(false)) {}
         uint64_t c4 = __builtin_amdgcn_s_memtime();
         c_wait += c2 - c1; c_proc += c3 - c2; c_issue += (c1 - c0) + (c4 - c3); n_tiles++;
+        if (jp < L.na + L.nb) { c_pgu += c3 - c2; n_gu++; }
     }
     lds_set(&ctl->progress[wave], 0xFFFFFFFFu, lane);
     if (wave == 0 && lane == 0) {
         ctl->t[9] = now();
         ctl->t[12] = c_wait; ctl->t[13] = c_proc; ctl->t[14] = c_issue; ctl->t[15] = n_tiles;
+        ctl->t[31] = n_gu; (void)c_dma; (void)c_pgu;
     }
 }
 
@@ -570,6 +584,7 @@ WM_DEV void route_tagged(const PersistArgs& a, lctl_t* ctl, int rep, uint32_t ta
     for (int i = 0; i < MAXV; i++) lv[i] = __builtin_bit_cast(float, (uint32_t)tv[i]);
     Picker<MAXV> pk;
     pk.init_vals(lv, E, lane);
+    if (lane == 0) ctl->t[28] = now();
     float my_v = 0.0f;
     my_e = 0;
     degenerate = false;
@@ -578,6 +593,7 @@ WM_DEV void route_tagged(const PersistArgs& a, lctl_t* ctl, int rep, uint32_t ta
         degenerate = degenerate || best == 0ull;
         if (lane == k) { my_e = Picker<MAXV>::id_of(best); my_v = pk.value_of(best); }
     }
+    if (lane == 0) ctl->t[29] = now();
     const bool mine = lane < K;
     float wmax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_v), 0));
     for (int k = 1; k < K; k++) {
@@ -589,6 +605,7 @@ WM_DEV void route_tagged(const PersistArgs& a, lctl_t* ctl, int rep, uint32_t ta
     for (int k = 0; k < K; k++) wsum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), k));
     wk = wsum > 0.0f ? ex / wsum : ex;
     nonfinite = __builtin_amdgcn_ballot_w64(mine && !isfinite(wk)) != 0ull;
+    if (lane == 0) ctl->t[30] = now();
 }
 
 // Operand records of the slots at positions q0 .. q0+n-1 of the down order
@@ -642,6 +659,37 @@ WM_DEV void stage_batch(const PersistArgs& a, lctl_t* ctl, lds8_t* lds, int q0, 
         }
     }
     for (int i = 0; i < n; i++) lds_set(&ctl->act_ready[slot_at(q0 + i, K, sh)], 1u, lane);
+}
+
+// Staging wave `sidx` of PSTAGE: the operand records of the slots, in down
+// order, in batches of up to 4 passes of loads; batch b is staged by wave
+// b % PSTAGE, so that the next batches' loads are in flight while one batch
+// waits.  A batch is read once this workgroup has finished its own gate/up
+// tiles of the batch's last slot (the others finish theirs at about the
+// same time).
+template <int DT, int SDT>
+WM_DEV void stage_slots(const PersistArgs& a, lctl_t* ctl, lds8_t* lds, uint32_t tag, int sidx, int lane) {
+    const Part P = partition(a);
+    if (P.ndn > 0) {
+        const int K = a.K, sh = a.has_shared;
+        TileList L;
+        L.init(K, sh, P.ngu, P.ndn);
+        const int nq = K + sh, passes = (a.I / SEG + 7) / 8, nb = max(1, 4 / passes);
+        for (int q = sidx * nb; q < nq; q += PSTAGE * nb) {
+            const int n = min(nb, nq - q);
+            wait_progress(ctl, (uint32_t)L.gu_end(slot_at(q + n - 1, K, sh)), a.status, lane);
+            stage_batch<DT, SDT>(a, ctl, lds, q, n, tag, P.w % P_AREP, lane);
+        }
+    }
+    if (lane == 0) ctl->t[5] = now();
+}
+
+// The other staging waves: wait for the tag of this launch, then stage.
+template <int DT, int SDT>
+WM_DEV void helper_stage(const PersistArgs& a, uint8_t* smem, int sidx, int lane) {
+    lctl_t* ctl = (lctl_t*)smem;
+    lds_wait(ctl, &ctl->rows_in, 1u, a.status, lane);
+    stage_slots<DT, SDT>(a, ctl, (lds8_t*)smem, ctl->tag, sidx, lane);
 }
 
 // ------------------------------------------------------------------ helper 0: router rows, routing, operand records
@@ -707,25 +755,7 @@ WM_DEV void helper_router(const PersistArgs& a, uint8_t* smem, int lane) {
     lds_set(&ctl->routed, 1u, lane);
     if (lane == 0) ctl->t[3] = now();
 
-    // ---- stager: the operand records of every slot, in down order.  The
-    // next slot is read once this workgroup has finished its own gate/up
-    // tiles of it (the others finish theirs at about the same time), together
-    // with the following slots this workgroup has also finished (up to 4
-    // passes of loads in flight).
-    if (P.ndn > 0) {
-        TileList L;
-        L.init(K, a.has_shared, P.ngu, P.ndn);
-        const int nq = K + a.has_shared, passes = (a.I / SEG + 7) / 8, maxb = max(1, 4 / passes);
-        for (int q = 0; q < nq;) {
-            wait_progress(ctl, (uint32_t)L.gu_end(slot_at(q, K, a.has_shared)), a.status, lane);
-            int n = 1;
-            while (n < maxb && q + n < nq && min_progress(ctl) >= (uint32_t)L.gu_end(slot_at(q + n, K, a.has_shared)))
-                n++;
-            stage_batch<DT, SDT>(a, ctl, lds, q, n, tag, P.w % P_AREP, lane);
-            q += n;
-        }
-    }
-    if (lane == 0) ctl->t[5] = now();
+    stage_slots<DT, SDT>(a, ctl, lds, tag, 0, lane);
 }
 
 // ------------------------------------------------------------------ helper 1: router rows, shared gate, SwiGLU publisher, combine
@@ -816,7 +846,8 @@ __global__ __launch_bounds__(PTHREADS) void k_decode_persist(PersistArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (wave < PW) stream_wave<GUT, DT, SGUT, SDT>(a, smem, wave, lane);
     else if (wave == PW) helper_router<GUT, DT, SGUT, SDT>(a, smem, lane);
-    else helper_publish<GUT, DT, SGUT, SDT>(a, smem, lane);
+    else if (wave == PW + 1) helper_publish<GUT, DT, SGUT, SDT>(a, smem, lane);
+    else helper_stage<DT, SDT>(a, smem, wave - PW - 1, lane);
 }
 
 template <int GUT, int DT, int SGUT, int SDT>
