@@ -2,17 +2,18 @@
 // persistent kernel: one workgroup per CU, and every workgroup takes an equal
 // share of every phase of the step.
 //
-// Workgroup w of nwg (PW streaming waves + 2 helper waves):
+// Workgroup w of nwg (PW compute waves, PISS issuer waves, 3 helper waves):
 //   * router rows [w*rr, (w+1)*rr): reference-order fp32 logits, stored with
 //     this launch's tag in the upper 32 bits, in P_REP replicas;
 //   * gate/up tiles [tw0, tw1) of the shared expert and of every routed slot
 //     (the same row range in every slot);
 //   * down rows of its own output range [d0, d1) for every slot, which it
 //     then combines itself: out[h] = sum_k w_k y_k[h] + shared, in k order.
-// The streaming waves walk one tile list: shared gate/up, routed gate/up slot
-// 0 .. K-1, shared down, routed down slot 0 .. K-1, each wave taking the next
-// entry from an LDS counter and keeping PRING tiles in flight (LDS-DMA ring).
-// Row sums go to LDS.
+// The workgroup's tiles form one list: shared gate/up, routed gate/up slot
+// 0 .. K-1, shared down, routed down slot 0 .. K-1.  The issuer waves stream
+// them into a shared ring of LDS buffers (LDS-DMA, PD tiles in flight each);
+// the compute waves take them in list order (wave c: entries c, c + PW, ...)
+// and write row sums to LDS.
 //
 // Hand-offs between workgroups carry the launch tag in every 64-bit word
 // (tag << 32 | value), so a reader needs one read of the data itself and no
@@ -25,8 +26,9 @@
 // every workgroup's start tag (so no workgroup can still read the old one).
 // Nothing is reset between launches; wm_workspace_reset zeroes the words.
 //
-// Helper 0: router DMA and rows 0/2, routing, operand records.  Helper 1:
-// rows 1/3, shared-expert gate, SwiGLU publishing, combine.
+// Helper 0: router DMA and rows 0/2, routing, operand records of half the
+// slots.  Helper 1: rows 1/3, shared-expert gate, SwiGLU publishing, combine.
+// Helper 2: operand records of the other half.
 //
 // Progress: every workgroup must be resident at once (the routing needs every
 // workgroup's router rows).  The host launches one workgroup per CU with more
@@ -46,7 +48,7 @@
 
 namespace wm {
 
-static_assert(PRING >= 1 && PRING <= 3, "the streaming FIFO below holds one to three tiles");
+static_assert(PD >= 1 && PD <= 12, "an issuer keeps at most 12 tiles (60 instructions) in flight");
 
 typedef __attribute__((address_space(3))) PersistCtl lctl_t;
 typedef __attribute__((address_space(3))) float lf32_t;
@@ -140,37 +142,35 @@ WM_DEV void wait_all(lctl_t* ctl, const lds32_t* p, int n, int32_t* status, int 
 
 WM_DEV uint64_t now() { return __builtin_amdgcn_s_memrealtime(); }
 
-// s_waitcnt vmcnt(n), n in [0, 10] (instructions of at most two later tiles).
+// s_waitcnt vmcnt(n), n in [0, 63] (the instructions of the later tiles in
+// flight).
 WM_DEV void wait_vm(int n) {
+#define WM_VM_CASE(k) case k: WM_WAIT_VMCNT(k); break;
+#define WM_VM_CASE8(k) WM_VM_CASE(k) WM_VM_CASE(k + 1) WM_VM_CASE(k + 2) WM_VM_CASE(k + 3) \
+    WM_VM_CASE(k + 4) WM_VM_CASE(k + 5) WM_VM_CASE(k + 6) WM_VM_CASE(k + 7)
     switch (n) {
-    case 0: WM_WAIT_VMCNT(0); break;
-    case 1: WM_WAIT_VMCNT(1); break;
-    case 2: WM_WAIT_VMCNT(2); break;
-    case 3: WM_WAIT_VMCNT(3); break;
-    case 4: WM_WAIT_VMCNT(4); break;
-    case 5: WM_WAIT_VMCNT(5); break;
-    case 6: WM_WAIT_VMCNT(6); break;
-    case 7: WM_WAIT_VMCNT(7); break;
-    case 8: WM_WAIT_VMCNT(8); break;
-    case 9: WM_WAIT_VMCNT(9); break;
-    default: WM_WAIT_VMCNT(10); break;
+        WM_VM_CASE8(0) WM_VM_CASE8(8) WM_VM_CASE8(16) WM_VM_CASE8(24)
+        WM_VM_CASE8(32) WM_VM_CASE8(40) WM_VM_CASE8(48) WM_VM_CASE(56) WM_VM_CASE(57) WM_VM_CASE(58)
+        WM_VM_CASE(59) WM_VM_CASE(60) WM_VM_CASE(61) WM_VM_CASE(62)
+    default: WM_WAIT_VMCNT(63); break;
     }
+#undef WM_VM_CASE8
+#undef WM_VM_CASE
 }
 
 // The DMA loads of one tile of type T into a ring buffer (as tile_dma; for
 // Q8_0 the lanes whose 16 bytes would fall past the buffer issue nothing, so
 // a buffer holds 4416 bytes instead of 5 KB).  Returns the instruction count.
-template <int T> WM_DEV int ring_dma(const uint8_t* W, int64_t off, int64_t nbytes, int lane, lds8_t* dst) {
+template <int T> WM_DEV int ring_dma(uint64_t G, int nbytes, int lane, lds8_t* dst) {
     constexpr int NI = tile_ni<T>(), CAP = ring_tile_bytes<T>() / 16;
-    const uintptr_t G = (uintptr_t)(W + off);
-    const uintptr_t A = G & ~(uintptr_t)15;
-    const int nch = (int)(((G - A) + (uintptr_t)nbytes + 15) >> 4);
+    const uint64_t A = G & ~(uint64_t)15;
+    const int nch = (int)(((G - A) + (uint64_t)nbytes + 15) >> 4);     // granules holding the tile's bytes
 #pragma unroll
     for (int k = 0; k < NI; k++) {
         int i = lane + 64 * k;
         if (64 * k + 63 < CAP || i < CAP) {     // lane 0 always issues: every instruction counts
             i = i < nch ? i : nch - 1;
-            __builtin_amdgcn_global_load_lds((const void*)(A + 16 * (uintptr_t)i),
+            __builtin_amdgcn_global_load_lds((const void*)(uintptr_t)(A + 16 * (uint64_t)i),
                                              (__attribute__((address_space(3))) void*)(dst + 1024 * k), 16, 0, CPOL_NT);
         }
     }
@@ -244,132 +244,228 @@ struct TileList {
 // Slot at position q of the order shared, 0 .. K-1 (shared first when present).
 WM_DEV int slot_at(int q, int K, int sh) { return sh ? (q == 0 ? K : q - 1) : q; }
 
-// ------------------------------------------------------------------ streaming waves
+// ------------------------------------------------------------------ streaming: issuers and compute waves
+// The workgroup's tiles (list entries s = 0, 1, ...) pass through one ring of
+// nbuf LDS buffers: tile s goes to buffer (s + n_rbuf) % nbuf (the first
+// n_rbuf buffers hold x and the router rows until the helpers are done with
+// them).  Issuer wave i sends tiles s = i, i + PISS, ... (at most PD in
+// flight); once a tile's bytes have landed it posts ready[b] = s + 1.
+// Compute wave c processes tiles s = c, c + PW, ... and posts done[b] = s + 1,
+// which frees the buffer for tile s + nbuf.  So the memory pipe stays full
+// whatever a tile costs to process.  An issuer posts everything it has in
+// flight before it waits for anything (a free buffer, the routing, the
+// router rows), so no wait can close a cycle.
+
+constexpr int PMAXT = 64;    // tiles per compute wave (one per lane)
+
+// A pointer / 64-bit argument as an opaque scalar value.
+WM_DEV uint64_t sval64(int64_t v) {
+    uint64_t r = (uint64_t)v;
+    asm volatile("" : "+s"(r));
+    return r;
+}
+WM_DEV uint64_t sval(const void* p) { return sval64((int64_t)(uintptr_t)p); }
+
+// A tile of the list: kind, slot, byte offset in its matrix, bytes, where its
+// row sums go (float index into the gate / up / down sums) and its rows.
+struct TileDesc {
+    int kind, slot, nb, out, rows;
+    int64_t off;
+};
 template <int GUT, int DT, int SGUT, int SDT>
-WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lane) {
+WM_DEV TileDesc tile_desc(const PersistArgs& a, const Part& P, const TileList& L, int j, int lg_gu, int lg_dn) {
+    const int K = a.K, H = a.H, I = a.I;
+    const TRef r = L.at(j < L.n ? j : 0);
+    const bool gu = r.kind <= K_RU;
+    const int rpt_gu = SEG >> lg_gu, rpt_dn = SEG >> lg_dn;
+    const int rpt = gu ? rpt_gu : rpt_dn, rows = gu ? I : H, abs_t = (gu ? P.tw0 : P.d0) + r.t;
+    const int tt = r.kind == K_SG || r.kind == K_SU ? SGUT : r.kind == K_SD ? SDT : gu ? GUT : DT;
+    const int64_t rb = matrix_bytes(tt, 1, gu ? H : I);
+    TileDesc d;
+    d.rows = min(rpt, rows - abs_t * rpt);
+    d.kind = r.kind;
+    d.slot = r.slot;
+    d.off = (int64_t)abs_t * rpt * rb;
+    d.nb = (int)((int64_t)d.rows * rb);
+    d.out = gu ? (r.kind == K_SG || r.kind == K_RG ? 0 : (K + 1) * a.gu_cap) + r.slot * a.gu_cap + r.t * rpt_gu
+               : r.slot * a.y_cap + r.t * rpt_dn;
+    return d;
+}
+
+WM_DEV int lg_tile_lanes(int n) { return 31 - __builtin_clz((unsigned)(n / SEG)); }
+WM_DEV bool routed_kind(int k) { return k == K_RG || k == K_RU || k == K_RD; }
+
+// ---- issuer wave i
+template <int GUT, int DT, int SGUT, int SDT>
+WM_DEV void issue_wave(const PersistArgs& a, uint8_t* smem, int i_v, int lane) {
     lctl_t* ctl = (lctl_t*)smem;
     lds8_t* lds = (lds8_t*)smem;
-    // the wave index is uniform: keep it (and every address derived from it,
-    // such as the LDS-DMA destinations that go to M0) in scalar registers
-    const int wave = __builtin_amdgcn_readfirstlane(wave_v);
+    const int iw = __builtin_amdgcn_readfirstlane(i_v);
+    const int K = a.K, sh = a.has_shared, nbuf = a.nbuf, n_rbuf = a.n_rbuf;
+    const int lg_gu = lg_tile_lanes(a.H), lg_dn = lg_tile_lanes(a.I);
     const Part P = partition(a);
-    const int K = a.K, sh = a.has_shared, H = a.H, I = a.I, E = a.E;
     TileList L;
     L.init(K, sh, P.ngu, P.ndn);
-    lds8_t* ring = lds + a.o_ring + wave * PRING * a.ring_buf;
-    lf32_t* garr = (lf32_t*)(lds + a.o_gu);
-    lf32_t* uarr = garr + (K + 1) * a.gu_cap;
-    lf32_t* yarr = (lf32_t*)(lds + a.o_y);
-    const int nseg_dn = I / SEG;
-    // geometry (rows per tile, lanes per row: powers of two; a tile is 64
-    // segments, so every lane holds one)
-    const int lg_gu = 31 - __builtin_clz((unsigned)(H / SEG)), lg_dn = 31 - __builtin_clz((unsigned)(I / SEG));
-    const int rpt_gu = SEG >> lg_gu, rpt_dn = SEG >> lg_dn;
-    const int sub_gu = lane & ((1 << lg_gu) - 1), rig_gu = lane >> lg_gu;
-    const int sub_dn = lane & ((1 << lg_dn) - 1), rig_dn = lane >> lg_dn;
-    const int64_t rb_sg = matrix_bytes(SGUT, 1, H), rb_g = matrix_bytes(GUT, 1, H);
-    const int64_t rb_sd = matrix_bytes(SDT, 1, I), rb_d = matrix_bytes(DT, 1, I);
+    const int ntile = (L.n - iw + PISS - 1) / PISS;
+    // lane t: this issuer's tiles t and t + 64 (s = iw + PISS * t)
+    int d_kind[2], d_slot[2], d_nb[2];
+    int64_t d_off[2];
+    uint64_t d_addr[2];
+    const uint64_t sg = sval(a.sh_gate), su = sval(a.sh_up), sd = sval(a.sh_down);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const TileDesc d = tile_desc<GUT, DT, SGUT, SDT>(a, P, L, iw + PISS * (lane + 64 * h), lg_gu, lg_dn);
+        d_kind[h] = d.kind; d_slot[h] = d.slot; d_nb[h] = d.nb; d_off[h] = d.off;
+        const uint64_t base = d.kind == K_SG ? sg : d.kind == K_SU ? su : sd;
+        d_addr[h] = routed_kind(d.kind) ? 0ull : base + (uint64_t)d.off;
+    }
+    bool routed = false, rfree = false;
+    int t_next = 0;
 
-    // routing in a register: lane k holds the expert id of slot k (-1 when
-    // invalid); read once, when the first routed tile comes up
-    int my_e = -1;
-    bool routed = false;
-
-    // Weights of a tile: matrix base (null for an invalid routed id), its
-    // rows, the tile index in the matrix, row bytes.
-    auto weights_of = [&](const TRef& r, int& rows, int& abs_t, int64_t& rb) -> const uint8_t* {
-        int e = 0;
-        if (r.kind == K_RG || r.kind == K_RU || r.kind == K_RD) {
-            e = __builtin_amdgcn_readlane(my_e, r.slot);
-            if (e < 0) return nullptr;
+    // The tiles in flight are this issuer's tiles tp .. t-1 (oldest first);
+    // lane t % 64 of v_ni / v_meta holds tile t's instruction count and meta
+    // word (0x100 | first byte's offset, 0: no weights).
+    int v_ni = 0, v_meta = 0;
+    int tp = 0, bp = n_rbuf + iw, outstanding = 0;      // oldest: tile, its buffer; instructions in flight
+    bp -= bp >= nbuf ? nbuf : 0;
+    auto post_oldest = [&]() {           // its bytes have landed
+        const int tl = tp & 63;
+        if (lane == 0) {
+            *(volatile lds32_t*)&ctl->bmeta[bp] = (uint32_t)__builtin_amdgcn_readlane(v_meta, tl);
+            *(volatile lds32_t*)&ctl->ready[bp] = (uint32_t)(iw + PISS * tp + 1);
         }
-        if (r.kind <= K_RU) {
-            rows = I; abs_t = P.tw0 + r.t;
-            switch (r.kind) {
-            case K_SG: rb = rb_sg; return a.sh_gate;
-            case K_SU: rb = rb_sg; return a.sh_up;
-            case K_RG: rb = rb_g; return a.gate + (int64_t)e * a.gstride;
-            default: rb = rb_g; return a.up + (int64_t)e * a.ustride;
-            }
-        }
-        rows = H; abs_t = P.d0 + r.t;
-        if (r.kind == K_SD) { rb = rb_sd; return a.sh_down; }
-        rb = rb_d;
-        return a.down + (int64_t)e * a.dstride;
+        outstanding -= __builtin_amdgcn_readlane(v_ni, tl);
+        tp++;
+        bp += PISS;
+        bp -= bp >= nbuf ? nbuf : 0;
+    };
+    // wait until the oldest tile has landed (at most the later ones'
+    // instructions outstanding), then post it
+    auto land_oldest = [&]() {
+        wait_vm(outstanding - __builtin_amdgcn_readlane(v_ni, tp & 63));
+        post_oldest();
+    };
+    auto flush = [&]() {
+        WM_WAIT_VMCNT(0);
+        while (tp < t_next) post_oldest();
     };
 
-    // ---- FIFO of issued tiles: entry 0 is the oldest; an entry keeps the
-    // list index, instruction count, ring buffer and the tile's first byte
-    // (null: no weights).  Wave w takes the entries w, w + PW, ... of the list.
-    int j0 = 0, j1 = 0, j2 = 0, ni0 = 0, ni1 = 0, ni2 = 0, b0 = 0, b1 = 0, b2 = 0, cnt = 0, seq = 0;
-    const uint8_t *t0p = nullptr, *t1p = nullptr, *t2p = nullptr;
-    int pend = wave;
-    uint64_t c_dma = 0;
-
-    // Issue the next tile of the list; false when the list is done, or (when
-    // !block) when the next tile needs the routing and it is not known yet.
-    auto try_issue = [&](bool block) -> bool {
-        if (pend >= L.n) return false;
-        const TRef r = L.at(pend);
-        if (!routed && (r.kind == K_RG || r.kind == K_RU || r.kind == K_RD)) {
-            if (lds_ld(&ctl->routed) == 0u) {
-                if (!block) return false;
-                lds_wait(ctl, &ctl->routed, 1u, a.status, lane);
+    int b = bp;                          // buffer of the next tile
+    for (t_next = 0; t_next < ntile; t_next++) {
+        const int t = t_next;
+        const int h = t >> 6, tl = t & 63;
+        const int s = iw + PISS * t;
+        const int kind = __builtin_amdgcn_readlane(h ? d_kind[1] : d_kind[0], tl);
+        if (!routed && routed_kind(kind)) {
+            flush();
+            lds_wait(ctl, &ctl->routed, 1u, a.status, lane);
+            // the expert of every routed tile (the shared ones keep theirs)
+            const uint64_t g = sval(a.gate), u = sval(a.up), dn = sval(a.down);
+            const uint64_t gs = sval64(a.gstride), us = sval64(a.ustride), ds = sval64(a.dstride);
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                const int sl = routed_kind(d_kind[hh]) ? d_slot[hh] : 0;
+                const int64_t e = (int)lds_ld((const lds32_t*)&ctl->ids[sl]);
+                const bool ok = lds_ld((const lds32_t*)&ctl->valid[sl]) != 0u;
+                const uint64_t base = d_kind[hh] == K_RG ? g : d_kind[hh] == K_RU ? u : dn;
+                const uint64_t stride = d_kind[hh] == K_RG ? gs : d_kind[hh] == K_RU ? us : ds;
+                if (routed_kind(d_kind[hh])) d_addr[hh] = ok ? base + (uint64_t)e * stride + (uint64_t)d_off[hh] : 0ull;
             }
             routed = true;
-            my_e = lane < K ? (ctl->valid[lane] ? ctl->ids[lane] : -1) : -1;
-            (void)E;
         }
-        const int b = seq % PRING;
-        lds8_t* buf = ring + b * a.ring_buf;
-        int rows = 0, abs_t = 0;
-        int64_t rb = 0;
-        const uint8_t* W = weights_of(r, rows, abs_t, rb);
-        int ni = 0;
-        const uint8_t* tp = nullptr;
-        if (W) {
-            const int rpt = r.kind <= K_RU ? rpt_gu : rpt_dn;
-            const int64_t off = (int64_t)abs_t * rpt * rb, nbytes = (int64_t)min(rpt, rows - abs_t * rpt) * rb;
-            tp = W + off;
-            const uint64_t d0 = __builtin_amdgcn_s_memtime();
-            switch (r.kind) {
-            case K_SG: case K_SU: ni = ring_dma<SGUT>(W, off, nbytes, lane, buf); break;
-            case K_RG: case K_RU: ni = ring_dma<GUT>(W, off, nbytes, lane, buf); break;
-            case K_SD: ni = ring_dma<SDT>(W, off, nbytes, lane, buf); break;
-            default: ni = ring_dma<DT>(W, off, nbytes, lane, buf); break;
+        if (b < n_rbuf && !rfree) {
+            if (lds_ld(&ctl->router_done[0]) == 0u || lds_ld(&ctl->router_done[1]) == 0u) {
+                flush();
+                wait_all(ctl, ctl->router_done, 2, a.status, lane);
             }
-            c_dma += __builtin_amdgcn_s_memtime() - d0;
+            rfree = true;
         }
-        // (selects, not a branch per entry: the entries stay in registers)
-        j0 = cnt == 0 ? pend : j0; ni0 = cnt == 0 ? ni : ni0; b0 = cnt == 0 ? b : b0; t0p = cnt == 0 ? tp : t0p;
-        j1 = cnt == 1 ? pend : j1; ni1 = cnt == 1 ? ni : ni1; b1 = cnt == 1 ? b : b1; t1p = cnt == 1 ? tp : t1p;
-        j2 = cnt == 2 ? pend : j2; ni2 = cnt == 2 ? ni : ni2; b2 = cnt == 2 ? b : b2; t2p = cnt == 2 ? tp : t2p;
-        cnt++;
-        seq++;
-        pend += PW;
-        return true;
-    };
+        // the buffer's previous tile must be processed; meanwhile post the
+        // tiles in flight one by one, oldest first (its wave may need one)
+        while (s >= nbuf && lds_ld(&ctl->done[b]) < (uint32_t)(s - nbuf + 1)) {
+            if (tp < t) {
+                land_oldest();
+            } else {
+                lds_wait(ctl, &ctl->done[b], (uint32_t)(s - nbuf + 1), a.status, lane);
+                break;
+            }
+        }
+        const uint64_t A = h ? d_addr[1] : d_addr[0];
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)A, tl);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(A >> 32), tl);
+        const uint64_t G = ((uint64_t)hi << 32) | lo;
+        lds8_t* buf = lds + a.o_ring + b * a.ring_buf;
+        int ni = 0;
+        if (G) {
+            const int nb = __builtin_amdgcn_readlane(h ? d_nb[1] : d_nb[0], tl);
+            switch (kind) {
+            case K_SG: case K_SU: ni = ring_dma<SGUT>(G, nb, lane, buf); break;
+            case K_RG: case K_RU: ni = ring_dma<GUT>(G, nb, lane, buf); break;
+            case K_SD: ni = ring_dma<SDT>(G, nb, lane, buf); break;
+            default: ni = ring_dma<DT>(G, nb, lane, buf); break;
+            }
+        }
+        v_ni = lane == tl ? ni : v_ni;
+        v_meta = lane == tl ? (G ? (int)(0x100u | (lo & 15u)) : 0) : v_meta;
+        outstanding += ni;
+        b += PISS;
+        b -= b >= nbuf ? nbuf : 0;
+        if (t + 1 - tp > PD) land_oldest();
+    }
+    flush();
+}
+
+// ---- compute wave c
+template <int GUT, int DT, int SGUT, int SDT>
+WM_DEV void consume_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lane) {
+    lctl_t* ctl = (lctl_t*)smem;
+    lds8_t* lds = (lds8_t*)smem;
+    const int wave = __builtin_amdgcn_readfirstlane(wave_v);
+    const int K = a.K, sh = a.has_shared, H = a.H, I = a.I, nbuf = a.nbuf, n_rbuf = a.n_rbuf;
+    const int nseg_dn = I / SEG;
+    // geometry (lanes per row: powers of two; a tile is 64 segments, so every
+    // lane holds one)
+    const int lg_gu = lg_tile_lanes(H), lg_dn = lg_tile_lanes(I);
+    const int sub_gu = lane & ((1 << lg_gu) - 1), rig_gu = lane >> lg_gu;
+    const int sub_dn = lane & ((1 << lg_dn) - 1), rig_dn = lane >> lg_dn;
+
+    // lane t: this wave's tile t (s = wave + PW * t)
+    int ntile, d_kind, d_slot, d_out, d_rows;
+    {
+        const Part P = partition(a);
+        TileList L;
+        L.init(K, sh, P.ngu, P.ndn);
+        ntile = (L.n - wave + PW - 1) / PW;
+        const TileDesc d = tile_desc<GUT, DT, SGUT, SDT>(a, P, L, wave + PW * lane, lg_gu, lg_dn);
+        d_kind = d.kind; d_slot = d.slot; d_out = d.out; d_rows = d.rows;
+    }
 
     // operand in registers and what it is: 1000 + type (x) or the slot (act)
     XOp xo;
     int xkey = -1;
     float sgate = 1.0f;
     bool have_sgate = false;
+    lf32_t* sums = (lf32_t*)(lds + a.o_gu);
+    lf32_t* yarr = (lf32_t*)(lds + a.o_y);
 
-    // Row sums of the tile at the head of the FIFO (tp: its first byte in
-    // memory, null when it has no weights).
-    auto process = [&](int j, int b, const uint8_t* tp) {
-        const TRef r = L.at(j);
-        const lds8_t* buf = ring + b * a.ring_buf + (((uintptr_t)tp) & 15u);
+    // Row sums of tile t in buffer b (meta: 0x100 | first byte's offset, 0:
+    // no weights).
+    auto process = [&](int t, int b, uint32_t meta) {
+        const int kind = __builtin_amdgcn_readlane(d_kind, t);
+        const int slot = __builtin_amdgcn_readlane(d_slot, t);
+        const int out = __builtin_amdgcn_readlane(d_out, t);
+        const int nrow = __builtin_amdgcn_readlane(d_rows, t);
+        const bool has_w = meta != 0u;
+        const lds8_t* buf = lds + a.o_ring + b * a.ring_buf + (meta & 15u);
         auto rowsum = [&](auto tag_t, int lpr) -> float {
             constexpr int T = decltype(tag_t)::value;
-            if (!tp) return 0.0f;
+            if (!has_w) return 0.0f;
             Seg<T> sg;
             sg.load(buf, lane);
             return row_reduce(seg_dot<T>(sg, xo), lpr);
         };
-        if (r.kind <= K_RU) {
-            const bool shared = r.kind <= K_SU;
+        if (kind <= K_RU) {
+            const bool shared = kind <= K_SU;
             const int key = 1000 + (shared ? SGUT : GUT);
             if (xkey != key) {
                 const int o = (shared && SGUT != GUT) ? a.o_xop2 : a.o_xop;
@@ -379,17 +475,13 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
             float p;
             if (SGUT == GUT || !shared) p = rowsum(std::integral_constant<int, GUT>(), 1 << lg_gu);
             else p = rowsum(std::integral_constant<int, SGUT>(), 1 << lg_gu);
-            const int local = r.t * rpt_gu + rig_gu, row = (P.tw0 + r.t) * rpt_gu + rig_gu;
-            if (sub_gu == (1 << lg_gu) - 1 && row < I) {
-                lf32_t* dst = (r.kind == K_SG || r.kind == K_RG) ? garr : uarr;
-                dst[r.slot * a.gu_cap + local] = p;
-            }
+            if (sub_gu == (1 << lg_gu) - 1 && rig_gu < nrow) sums[out + rig_gu] = p;
         } else {
-            const bool shared = r.kind == K_SD;
-            if (xkey != r.slot) {
-                lds_wait(ctl, &ctl->act_ready[r.slot], 1u, a.status, lane);
-                xop_read((const lds32_t*)(lds + a.o_reg) + ((int64_t)r.slot * nseg_dn + sub_dn) * XOP_DW, xo);
-                xkey = r.slot;
+            const bool shared = kind == K_SD;
+            if (xkey != slot) {
+                lds_wait(ctl, &ctl->act_ready[slot], 1u, a.status, lane);
+                xop_read((const lds32_t*)(lds + a.o_reg) + ((int64_t)slot * nseg_dn + sub_dn) * XOP_DW, xo);
+                xkey = slot;
             }
             float p;
             if (SDT == DT || !shared) p = rowsum(std::integral_constant<int, DT>(), 1 << lg_dn);
@@ -402,76 +494,48 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
                 }
                 p = p * sgate;
             }
-            const int local = r.t * rpt_dn + rig_dn, row = (P.d0 + r.t) * rpt_dn + rig_dn;
-            if (sub_dn == (1 << lg_dn) - 1 && row < H) yarr[r.slot * a.y_cap + local] = p;
+            if (sub_dn == (1 << lg_dn) - 1 && rig_dn < nrow) yarr[out + rig_dn] = p;
         }
     };
 
-    // ---- x operand records (8 lanes per segment, 8 segments per wave) and
-    // the first tiles.  Waves whose rings hold the router rows build first and
-    // then wait for the helpers to finish with the rows; the others send
-    // their first tiles at once and build while those are in flight.
+    // ---- x operand records (8 lanes per segment, 8 segments per wave)
     {
-        const int nseg = H / SEG, seg = wave * 8 + (lane >> 3), part = lane & 7;
+        const int nseg = H / SEG, part = lane & 7;
         const bool two = sh && SGUT != GUT;
-        const bool rwave = wave < a.n_rwaves;
         float v[8], v2[8];
-        if (seg < nseg) {
-            xop_part_fetch<GUT>(a.x, seg, part, v);
-            if (two) xop_part_fetch<SGUT>(a.x, seg, part, v2);
-        }
-        if (!rwave) while (cnt < PRING && try_issue(false)) {}
-        if (seg < nseg) {
-            xop_part<GUT>(v, part, (lds32_t*)(lds + a.o_xop) + seg * XOP_DW);
-            if (two) xop_part<SGUT>(v2, part, (lds32_t*)(lds + a.o_xop2) + seg * XOP_DW);
-        }
-        for (int sg = seg + PW * 8; sg < nseg; sg += PW * 8) {     // hidden sizes beyond PW * 8 segments
+        for (int sg = wave * 8 + (lane >> 3); sg < nseg; sg += PW * 8) {
             xop_part_fetch<GUT>(a.x, sg, part, v);
+            if (two) xop_part_fetch<SGUT>(a.x, sg, part, v2);
             xop_part<GUT>(v, part, (lds32_t*)(lds + a.o_xop) + sg * XOP_DW);
-            if (two) {
-                xop_part_fetch<SGUT>(a.x, sg, part, v2);
-                xop_part<SGUT>(v2, part, (lds32_t*)(lds + a.o_xop2) + sg * XOP_DW);
-            }
+            if (two) xop_part<SGUT>(v2, part, (lds32_t*)(lds + a.o_xop2) + sg * XOP_DW);
         }
         lds_set(&ctl->xop_built[wave], 1u, lane);
-        if (rwave) {
-            wait_all(ctl, ctl->router_done, 2, a.status, lane);
-            while (cnt < PRING && try_issue(false)) {}
-        }
     }
     wait_all(ctl, ctl->xop_built, PW, a.status, lane);
     if (wave == 0 && lane == 0) ctl->t[8] = now();
 
-    uint64_t c_wait = 0, c_proc = 0, c_issue = 0, n_tiles = 0, c_pgu = 0, n_gu = 0;
-    while (true) {
-        uint64_t c0 = __builtin_amdgcn_s_memtime();
-        if (cnt == 0) {
-            if (!try_issue(true)) break;
-            while (cnt < PRING && try_issue(false)) {}
+    int b = n_rbuf + wave;
+    b -= b >= nbuf ? nbuf : 0;
+    for (int t = 0; t < ntile; t++, b = b + PW - (b + PW >= nbuf ? nbuf : 0)) {
+        const int s = wave + PW * t;
+        // the tile's bytes (a short spin: this is the common wait)
+        uint32_t it = 0;
+        while (lds_ld(&ctl->ready[b]) < (uint32_t)(s + 1)) {
+            if (++it > PSPIN || aborted(ctl)) {
+                give_up(ctl, a.status, lane);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
         }
-        uint64_t c1 = __builtin_amdgcn_s_memtime();
-        wait_vm(cnt == 3 ? ni1 + ni2 : (cnt == 2 ? ni1 : 0));
-        uint64_t c2 = __builtin_amdgcn_s_memtime();
-        const int jp = j0;
-        process(j0, b0, t0p);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        process(t, b, lds_ld(&ctl->bmeta[b]));
         // progress after the row sums (LDS executes one wave's writes in order)
-        if (lane == 0) *(volatile lds32_t*)&ctl->progress[wave] = (uint32_t)(j0 + PW);
-        wave_lds_sync();          // every lane's reads of the buffer are done before it is refilled
-        uint64_t c3 = __builtin_amdgcn_s_memtime();
-        j0 = j1; ni0 = ni1; b0 = b1; t0p = t1p;
-        j1 = j2; ni1 = ni2; b1 = b2; t1p = t2p;
-        cnt--;
-        while (cnt < PRING && try_issue(false)) {}
-        uint64_t c4 = __builtin_amdgcn_s_memtime();
-        c_wait += c2 - c1; c_proc += c3 - c2; c_issue += (c1 - c0) + (c4 - c3); n_tiles++;
-        if (jp < L.na + L.nb) { c_pgu += c3 - c2; n_gu++; }
+        if (lane == 0) *(volatile lds32_t*)&ctl->progress[wave] = (uint32_t)(s + PW);
+        wave_lds_sync();          // every lane's reads of the buffer are done before it is released
+        if (lane == 0) *(volatile lds32_t*)&ctl->done[b] = (uint32_t)(s + 1);
     }
     lds_set(&ctl->progress[wave], 0xFFFFFFFFu, lane);
-    if (wave == 0 && lane == 0) {
-        ctl->t[9] = now();
-        ctl->t[12] = c_wait; ctl->t[13] = c_proc; ctl->t[14] = c_issue; ctl->t[15] = n_tiles;
-        ctl->t[31] = n_gu; (void)c_dma; (void)c_pgu;
-    }
+    if (wave == 0 && lane == 0) ctl->t[9] = now();
 }
 
 // ------------------------------------------------------------------ helpers: router rows
@@ -479,17 +543,22 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
 // x and router rows [r0, r0 + nr) into LDS regions of `region` bytes (x
 // first, then the rows; 16-byte aligned sources; x with the default policy,
 // the rows non-temporal), all in flight together.
-WM_DEV void router_dma(const float* x, const float* W, int H, int r0, int nr, lds8_t* dst0, int region, int lane) {
+WM_DEV void router_dma(const float* x, const float* W, int H, int r0, int qa, int qb, lds8_t* dst0, int region,
+                       int lane) {
+    // x (when given) into region 0, rows r0 + qa and r0 + qb (when >= 0) into
+    // regions 1 + qa and 1 + qb
     const int64_t nbytes = (int64_t)H * 4;
     const int units = (int)((nbytes + 1023) >> 10);
     const int nch = (int)((nbytes + 15) >> 4);
-    for (int q = 0; q <= nr; q++) {
-        const uint8_t* src = (const uint8_t*)(q == 0 ? x : W + (int64_t)(r0 + q - 1) * H);
-        lds8_t* dst = dst0 + q * region;
+    for (int n = 0; n < 3; n++) {
+        const int q = n == 0 ? (x ? -1 : -2) : (n == 1 ? qa : qb);
+        if (q == -2 || (n > 0 && q < 0)) continue;
+        const uint8_t* src = (const uint8_t*)(n == 0 ? x : W + (int64_t)(r0 + q) * H);
+        lds8_t* dst = dst0 + (n == 0 ? 0 : 1 + q) * region;
         for (int k = 0; k < units; k++) {
             int i = lane + 64 * k;
             i = i < nch ? i : nch - 1;
-            if (q == 0)
+            if (n == 0)
                 __builtin_amdgcn_global_load_lds((const void*)(src + 16 * i),
                                                  (__attribute__((address_space(3))) void*)(dst + 1024 * k), 16, 0, 0);
             else
@@ -582,7 +651,7 @@ WM_DEV void route_tagged(const PersistArgs& a, lctl_t* ctl, int rep, uint32_t ta
     float lv[MAXV];
 #pragma unroll
     for (int i = 0; i < MAXV; i++) lv[i] = __builtin_bit_cast(float, (uint32_t)tv[i]);
-    Picker<MAXV> pk;
+    SortedPicker<MAXV> pk;
     pk.init_vals(lv, E, lane);
     if (lane == 0) ctl->t[28] = now();
     float my_v = 0.0f;
@@ -712,7 +781,8 @@ WM_DEV void helper_router(const PersistArgs& a, uint8_t* smem, int lane) {
     bool valid = false;
     if (!a.forced) {
         const int r0 = P.w * a.rr, nr = max(0, min(a.rr, E - r0));
-        if (nr > 0) router_dma(a.x, a.router, a.H, r0, nr, lds + a.o_ring, a.x_region, lane);
+        // x and rows 0 and 2 here, rows 1 and 3 on the other helper
+        if (nr > 0) router_dma(a.x, a.router, a.H, r0, 0, nr > 2 ? 2 : -1, lds + a.o_ring, a.x_region, lane);
         lds_set(&ctl->rows_in, 1u, lane);          // (also when this workgroup has no router rows)
         if (lane == 0) ctl->t[1] = now();
         if (nr > 0)   // rows 0 and 2 here, rows 1 and 3 on the other helper
@@ -753,6 +823,7 @@ WM_DEV void helper_router(const PersistArgs& a, uint8_t* smem, int lane) {
         ctl->valid[lane] = valid ? 1 : 0;
     }
     lds_set(&ctl->routed, 1u, lane);
+    __builtin_amdgcn_s_setprio(0);
     if (lane == 0) ctl->t[3] = now();
 
     stage_slots<DT, SDT>(a, ctl, lds, tag, 0, lane);
@@ -766,6 +837,10 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
     lds8_t* lds = (lds8_t*)smem;
     const Part P = partition(a);
     const int K = a.K, sh = a.has_shared, nq = K + sh;
+    if (!a.forced) {
+        const int r0 = P.w * a.rr, nr = max(0, min(a.rr, a.E - r0));
+        if (nr > 1) router_dma(nullptr, a.router, a.H, r0, 1, nr > 3 ? 3 : -1, lds + a.o_ring, a.x_region, lane);
+    }
     lds_wait(ctl, &ctl->rows_in, 1u, a.status, lane);
     const uint32_t tag = ctl->tag;
     if (!a.forced) {
@@ -773,6 +848,7 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
         if (nr > 1) router_chains(lds + a.o_ring, a.x_region, a.H, r0, 1, nr > 3 ? 3 : -1, a.E, tag, a.tlogits, lane);
     }
     lds_set(&ctl->router_done[1], 1u, lane);
+    __builtin_amdgcn_s_setprio(0);
     if (sh && a.sh_gate_inp) {
         const float g = wave_shgate(a.x, a.sh_gate_inp, a.H, lane);
         if (lane == 0) ctl->sgate = g;
@@ -844,10 +920,15 @@ __global__ __launch_bounds__(PTHREADS) void k_decode_persist(PersistArgs a) {
         ((lds32_t*)(lds8_t*)smem)[i] = i < PW ? (uint32_t)i : 0u;     // progress[w] = w: wave w's first entry
     __syncthreads();
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (wave < PW) stream_wave<GUT, DT, SGUT, SDT>(a, smem, wave, lane);
-    else if (wave == PW) helper_router<GUT, DT, SGUT, SDT>(a, smem, lane);
-    else if (wave == PW + 1) helper_publish<GUT, DT, SGUT, SDT>(a, smem, lane);
-    else helper_stage<DT, SDT>(a, smem, wave - PW - 1, lane);
+    if (wave < PW) consume_wave<GUT, DT, SGUT, SDT>(a, smem, wave, lane);
+    // (the issuers re-issue as soon as a tile lands)
+    else if (wave < PW + PISS) { __builtin_amdgcn_s_setprio(2); issue_wave<GUT, DT, SGUT, SDT>(a, smem, wave - PW, lane); }
+    // the router rows and the routing are the critical path: the helper
+    // waves win the issue arbitration against the streaming waves until the
+    // routing is known (their later polling must not)
+    else if (wave == PW + PISS) { __builtin_amdgcn_s_setprio(3); helper_router<GUT, DT, SGUT, SDT>(a, smem, lane); }
+    else if (wave == PW + PISS + 1) { __builtin_amdgcn_s_setprio(3); helper_publish<GUT, DT, SGUT, SDT>(a, smem, lane); }
+    else helper_stage<DT, SDT>(a, smem, wave - PW - PISS - 1, lane);
 }
 
 template <int GUT, int DT, int SGUT, int SDT>
