@@ -492,27 +492,28 @@ static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
     int o = (int)((sizeof(PersistCtl) + 255) / 256 * 256);
     a.x_region = (H * 4 + 1023) / 1024 * 1024;
     const int router_bytes = forced ? 0 : (1 + rr) * a.x_region;
-    a.n_rbuf = (router_bytes + a.ring_buf - 1) / a.ring_buf;
-    {   // a compute wave keeps one descriptor per tile in a lane (at most 64
-        // tiles), an issuer two (at most 128)
-        const int ngu_max = (a.gu_tiles + nwg - 1) / nwg, ndn_max = (a.dn_tiles + nwg - 1) / nwg;
-        const int64_t nlist = (int64_t)(2 * ngu_max + ndn_max) * (K + (sh ? 1 : 0));
-        if ((nlist + PW - 1) / PW > 64 || (nlist + PISS - 1) / PISS > 128) return 1;
-    }
+    a.n_rwaves = (router_bytes + PRING * a.ring_buf - 1) / (PRING * a.ring_buf);
     const int rec = XOP_DW * 4;
     a.o_reg = o; o += (K + 1) * (I / SEG) * rec;
+    a.o_stage = o; o += PSTAGE * 4 * 4096;
     a.o_xop = o; o += (H / SEG) * rec;
     a.o_xop2 = a.o_xop;
     if (sh && sgut != gut) { a.o_xop2 = o; o += (H / SEG) * rec; }
     a.o_gu = o; o += 2 * (K + 1) * a.gu_cap * 4;
     a.o_y = o; o += (K + 1) * a.y_cap * 4;
     o = (o + 255) / 256 * 256;
-    // the ring takes what is left, up to PNB buffers
+    // the streaming waves' rings take what is left, up to PW of them
     a.o_ring = o;
-    a.nbuf = std::min(PNB, (max_lds_per_wg() - o) / a.ring_buf);
-    if (a.nbuf < a.n_rbuf + 2 * PISS || a.nbuf < 12) return 1;
+    a.nstream = std::min(PW, (max_lds_per_wg() - o) / (PRING * a.ring_buf));
+    if (a.nstream < a.n_rwaves + 1 || a.nstream < 4) return 1;
+    {   // a streaming wave keeps one descriptor per tile in a lane: at most 64 tiles
+        const int ngu_max = (a.gu_tiles + nwg - 1) / nwg, ndn_max = (a.dn_tiles + nwg - 1) / nwg;
+        const int64_t nlist = (int64_t)(2 * ngu_max + ndn_max) * (K + (sh ? 1 : 0));
+        if ((nlist + a.nstream - 1) / a.nstream > 64) return 1;
+    }
     // (and more than half of a CU's LDS, so that each CU holds one workgroup)
-    const int lds = std::max((o + a.nbuf * a.ring_buf + 255) / 256 * 256, (max_lds_per_wg() / 2 + 256) / 256 * 256);
+    const int lds = std::max((o + a.nstream * PRING * a.ring_buf + 255) / 256 * 256,
+                             (max_lds_per_wg() / 2 + 256) / 256 * 256);
     if (int rc = aligned_input(x, H, (float*)(ws + L.xin), s)) return rc;
     a.x = x; a.out = out; a.router = d->router;
     a.gate = (const uint8_t*)d->gate_exps; a.up = (const uint8_t*)d->up_exps; a.down = (const uint8_t*)d->down_exps;

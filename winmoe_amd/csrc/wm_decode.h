@@ -75,12 +75,10 @@ int launch_decode_step(const DecodeArgs& a, int gut, int dt, int sgut, int sdt, 
 // routing, operand staging, SwiGLU publishing, combine).  Internal.
 namespace wm {
 
-constexpr int PW = 8;                    // compute waves per workgroup (they process the weight tiles)
-constexpr int PISS = 4;                  // issuer waves (they stream the tiles into the shared LDS ring)
-constexpr int PD = 3;                    // tiles in flight per issuer wave
-constexpr int PNB = 32;                  // most ring buffers
+constexpr int PW = 13;                   // streaming waves per workgroup (each loads and processes tiles)
+constexpr int PRING = 1;                 // ring buffers per streaming wave
 constexpr int PSTAGE = 2;                // operand staging waves (the first is also the router wave)
-constexpr int PTHREADS = 64 * (PW + PISS + 1 + PSTAGE);  // + publisher
+constexpr int PTHREADS = 64 * (PW + 1 + PSTAGE);  // + publisher
 constexpr int PMAXK = 16;
 constexpr int P_TL = 32;                 // timeline words per workgroup
 constexpr int P_MAX_WG = 1024;           // workgroups (CUs) the workspace has start-tag words for
@@ -107,7 +105,7 @@ struct PersistCtl {
     uint32_t abort;                // a wait of this workgroup gave up: every later wait ends at once
     uint32_t rows_in;              // x and the router rows are in LDS
     uint32_t router_done[2];       // helper h is done with the router rows (their ring space is free)
-    uint32_t pad;
+    uint32_t npicked;              // picks 0 .. npicked-1 of the routing are in ids / valid
     uint32_t act_ready[PMAXK + 1]; // the slot's SwiGLU operand records are in LDS
     int32_t ids[PMAXK];
     float w[PMAXK];
@@ -115,18 +113,16 @@ struct PersistCtl {
     float sgate;
     uint32_t pad2[2];
     uint64_t t[P_TL];              // timeline (device clock)
-    uint32_t ready[PNB];           // ring buffer b holds tile s (its bytes have landed): s + 1
-    uint32_t bmeta[PNB];           // ... and 0x100 | (first byte's offset in the buffer), 0: no weights
-    uint32_t done[PNB];            // the tile s in ring buffer b has been processed: s + 1
 };
 
 struct PersistArgs {
     int32_t H, I, E, K, has_shared, forced, nwg, rr;
     int32_t gu_tiles, dn_tiles;        // tiles of one gate/up matrix (I rows) and of one down matrix (H rows)
-    int32_t n_rbuf;                    // ring buffers that hold x and the router rows at the start
-    int32_t o_ring, ring_buf, nbuf;    // LDS: the ring (nbuf buffers of ring_buf bytes)
+    int32_t n_rwaves;                  // streaming waves whose rings hold x and the router rows at the start
+    int32_t o_ring, ring_buf, nstream; // LDS: the rings of the nstream streaming waves (PRING buffers of ring_buf bytes each)
     int32_t x_region;                  // bytes of x / of one router row in the ring space
     int32_t o_reg;                     // LDS: SwiGLU operand records [K+1][I/64]
+    int32_t o_stage;                   // LDS: the staging waves' landing areas (PSTAGE x 16 KB)
     int32_t o_xop, o_xop2;             // LDS: x operand records of the routed / shared gate-up types
     int32_t o_gu, gu_cap;              // LDS: gate and up row sums [K+1][gu_cap] each
     int32_t o_y, y_cap;                // LDS: down row sums [K+1][y_cap]

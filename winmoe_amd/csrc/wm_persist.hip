@@ -48,7 +48,7 @@
 
 namespace wm {
 
-static_assert(PD >= 1 && PD <= 12, "an issuer keeps at most 12 tiles (60 instructions) in flight");
+static_assert(PRING >= 1 && PRING <= 8, "a streaming wave keeps at most PRING tiles in its ring");
 
 typedef __attribute__((address_space(3))) PersistCtl lctl_t;
 typedef __attribute__((address_space(3))) float lf32_t;
@@ -61,6 +61,13 @@ constexpr uint32_t PSPIN_G = 1u << 17;  // device-memory polls (~1 us each) befo
 WM_DEV uint32_t gld_agent(const uint32_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 WM_DEV uint64_t gld_agent64(const uint64_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// The first read of a tagged hand-off vector: through the XCD's L2, so the
+// workgroups of one XCD that read the same replica share one fetch.  A line
+// the L2 got before all its words were written shows an older tag; the
+// retries read with agent scope, past the L2.
+WM_DEV uint64_t gld_first64(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 WM_DEV void gst_agent(uint32_t* p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 WM_DEV void gst_agent64(uint64_t* p, uint64_t v) {
@@ -201,62 +208,74 @@ WM_DEV Part partition(const PersistArgs& a) {
     return p;
 }
 
-// The workgroup's tile list [shared gate/up] [routed gate/up, slot 0..K-1]
-// [shared down] [routed down, slot 0..K-1]; gate and up of a tile adjacent.
+// Slot at position q of the order shared, 0 .. K-1 (shared first when present).
+WM_DEV int slot_at(int q, int K, int sh) { return sh ? (q == 0 ? K : q - 1) : q; }
+
+// The workgroup's tile list.  With the slots in the order shared, 0 .. K-1,
+// G(q) = the gate/up tiles of slot q (gate and up of a row adjacent) and
+// D(q) = its down tiles, the list is
+//   G(0) .. G(PLAG), D(0), G(PLAG+1), D(1), G(PLAG+2), ..., D(nq-1-PLAG) .. D(nq-1):
+// the down tiles of a slot come PLAG slots of gate/up later, so the hand-off
+// of its SwiGLU outputs between workgroups overlaps the streaming of later
+// slots instead of waiting at the end.  Every D(q) comes after G(q).
+constexpr int PLAG = 16;
 struct TileList {
-    int K, sh, ngu, ndn, na, nb, nc, n;
-    uint32_t m2gu, mdn;
+    int K, sh, nq, g, d, npre, npair, n;
+    uint32_t mg, mgd, md;
     WM_DEV void init(int K_, int sh_, int ngu_, int ndn_) {
-        K = K_; sh = sh_; ngu = ngu_; ndn = ndn_;
-        na = sh ? 2 * ngu : 0;
-        nb = K * 2 * ngu;
-        nc = sh ? ndn : 0;
-        n = na + nb + nc + K * ndn;
-        m2gu = fdiv_magic(2 * ngu);
-        mdn = fdiv_magic(ndn);
+        K = K_; sh = sh_; nq = K + sh;
+        g = 2 * ngu_; d = ndn_;
+        npre = min(nq, PLAG + 1);
+        npair = max(0, nq - (PLAG + 1));
+        n = nq * (g + d);
+        mg = fdiv_magic(g); mgd = fdiv_magic(g + d); md = fdiv_magic(d);
     }
-    // list position after the gate/up tiles of `slot` (slot K: shared)
-    WM_DEV int gu_end(int slot) const { return slot == K ? na : na + (slot + 1) * 2 * ngu; }
+    // list position after the gate/up tiles of `slot`
+    WM_DEV int gu_end(int slot) const {
+        const int q = slot == K ? 0 : slot + sh;
+        return q <= PLAG ? (q + 1) * g : npre * g + (q - PLAG - 1) * (g + d) + d + g;
+    }
     WM_DEV TRef at(int j) const {
         TRef r;
-        if (j < na) {
-            r.kind = (j & 1) ? K_SU : K_SG; r.slot = K; r.t = j >> 1;
-            return r;
+        int q, t;
+        bool down;
+        if (j < npre * g) {
+            q = fdiv(j, g, mg); t = j - q * g; down = false;
+        } else {
+            j -= npre * g;
+            if (j < npair * (g + d)) {
+                const int pi = fdiv(j, g + d, mgd), rr = j - pi * (g + d);
+                down = rr < d;
+                q = down ? pi : PLAG + 1 + pi;
+                t = down ? rr : rr - d;
+            } else {
+                j -= npair * (g + d);
+                const int i = fdiv(j, d, md);
+                q = npair + i; t = j - i * d; down = true;
+            }
         }
-        j -= na;
-        if (j < nb) {
-            const int q = fdiv(j, 2 * ngu, m2gu), rr = j - q * 2 * ngu;
-            r.kind = (rr & 1) ? K_RU : K_RG; r.slot = q; r.t = rr >> 1;
-            return r;
+        const bool shared = sh && q == 0;
+        r.slot = slot_at(q, K, sh);
+        if (down) {
+            r.kind = shared ? K_SD : K_RD; r.t = t;
+        } else {
+            r.kind = (t & 1) ? (shared ? K_SU : K_RU) : (shared ? K_SG : K_RG); r.t = t >> 1;
         }
-        j -= nb;
-        if (j < nc) {
-            r.kind = K_SD; r.slot = K; r.t = j;
-            return r;
-        }
-        j -= nc;
-        const int q = fdiv(j, ndn, mdn);
-        r.kind = K_RD; r.slot = q; r.t = j - q * ndn;
         return r;
     }
 };
 
-// Slot at position q of the order shared, 0 .. K-1 (shared first when present).
-WM_DEV int slot_at(int q, int K, int sh) { return sh ? (q == 0 ? K : q - 1) : q; }
 
-// ------------------------------------------------------------------ streaming: issuers and compute waves
-// The workgroup's tiles (list entries s = 0, 1, ...) pass through one ring of
-// nbuf LDS buffers: tile s goes to buffer (s + n_rbuf) % nbuf (the first
-// n_rbuf buffers hold x and the router rows until the helpers are done with
-// them).  Issuer wave i sends tiles s = i, i + PISS, ... (at most PD in
-// flight); once a tile's bytes have landed it posts ready[b] = s + 1.
-// Compute wave c processes tiles s = c, c + PW, ... and posts done[b] = s + 1,
-// which frees the buffer for tile s + nbuf.  So the memory pipe stays full
-// whatever a tile costs to process.  An issuer posts everything it has in
-// flight before it waits for anything (a free buffer, the routing, the
-// router rows), so no wait can close a cycle.
+// ------------------------------------------------------------------ streaming waves
+// Streaming wave w of nstream takes the list entries s = w, w + nstream, ...
+// and both loads them (LDS-DMA into its own ring of PRING buffers) and
+// processes them.  The LDS-DMA bandwidth of a CU grows with the number of
+// waves that issue it (each wave's loads complete in order), not with the
+// loads one wave keeps in flight, so every streaming wave issues its own.
+// The first n_rwaves rings hold x and the router rows at the start; those
+// waves send nothing before the router helpers are done with them.
 
-constexpr int PMAXT = 64;    // tiles per compute wave (one per lane)
+constexpr int PMAXT = 64;    // tiles per streaming wave (one per lane)
 
 // A pointer / 64-bit argument as an opaque scalar value.
 WM_DEV uint64_t sval64(int64_t v) {
@@ -295,109 +314,80 @@ WM_DEV TileDesc tile_desc(const PersistArgs& a, const Part& P, const TileList& L
 WM_DEV int lg_tile_lanes(int n) { return 31 - __builtin_clz((unsigned)(n / SEG)); }
 WM_DEV bool routed_kind(int k) { return k == K_RG || k == K_RU || k == K_RD; }
 
-// ---- issuer wave i
 template <int GUT, int DT, int SGUT, int SDT>
-WM_DEV void issue_wave(const PersistArgs& a, uint8_t* smem, int i_v, int lane) {
+WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lane) {
     lctl_t* ctl = (lctl_t*)smem;
     lds8_t* lds = (lds8_t*)smem;
-    const int iw = __builtin_amdgcn_readfirstlane(i_v);
-    const int K = a.K, sh = a.has_shared, nbuf = a.nbuf, n_rbuf = a.n_rbuf;
-    const int lg_gu = lg_tile_lanes(a.H), lg_dn = lg_tile_lanes(a.I);
-    const Part P = partition(a);
-    TileList L;
-    L.init(K, sh, P.ngu, P.ndn);
-    const int ntile = (L.n - iw + PISS - 1) / PISS;
-    // lane t: this issuer's tiles t and t + 64 (s = iw + PISS * t)
-    int d_kind[2], d_slot[2], d_nb[2];
-    int64_t d_off[2];
-    uint64_t d_addr[2];
-    const uint64_t sg = sval(a.sh_gate), su = sval(a.sh_up), sd = sval(a.sh_down);
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-        const TileDesc d = tile_desc<GUT, DT, SGUT, SDT>(a, P, L, iw + PISS * (lane + 64 * h), lg_gu, lg_dn);
-        d_kind[h] = d.kind; d_slot[h] = d.slot; d_nb[h] = d.nb; d_off[h] = d.off;
+    const int wave = __builtin_amdgcn_readfirstlane(wave_v);
+    const int K = a.K, sh = a.has_shared, H = a.H, I = a.I, ns = a.nstream;
+    const int nseg_dn = I / SEG;
+    // geometry (lanes per row: powers of two; a tile is 64 segments, so every
+    // lane holds one)
+    const int lg_gu = lg_tile_lanes(H), lg_dn = lg_tile_lanes(I);
+    const int sub_gu = lane & ((1 << lg_gu) - 1), rig_gu = lane >> lg_gu;
+    const int sub_dn = lane & ((1 << lg_dn) - 1), rig_dn = lane >> lg_dn;
+    const bool active = wave < ns;
+    lds8_t* ring = lds + a.o_ring + wave * PRING * a.ring_buf;
+
+    // ---- descriptors, lane t: this wave's tile t (s = wave + ns * t)
+    int ntile = 0, d_kind, d_slot, d_out, d_rows, d_nb;
+    int64_t d_off;
+    uint64_t d_addr;
+    {
+        const Part P = partition(a);
+        TileList L;
+        L.init(K, sh, P.ngu, P.ndn);
+        if (active) ntile = (L.n - wave + ns - 1) / ns;
+        const TileDesc d = tile_desc<GUT, DT, SGUT, SDT>(a, P, L, wave + ns * lane, lg_gu, lg_dn);
+        d_kind = d.kind; d_slot = d.slot; d_out = d.out; d_rows = d.rows; d_nb = d.nb; d_off = d.off;
+        const uint64_t sg = sval(a.sh_gate), su = sval(a.sh_up), sd = sval(a.sh_down);
         const uint64_t base = d.kind == K_SG ? sg : d.kind == K_SU ? su : sd;
-        d_addr[h] = routed_kind(d.kind) ? 0ull : base + (uint64_t)d.off;
+        d_addr = routed_kind(d.kind) ? 0ull : base + (uint64_t)d.off;
     }
-    bool routed = false, rfree = false;
-    int t_next = 0;
+    int picked = 0;                      // picks whose tiles have addresses
+    bool rfree = wave >= a.n_rwaves;     // this wave's ring is free of the router rows
 
-    // The tiles in flight are this issuer's tiles tp .. t-1 (oldest first);
-    // lane t % 64 of v_ni / v_meta holds tile t's instruction count and meta
-    // word (0x100 | first byte's offset, 0: no weights).
-    int v_ni = 0, v_meta = 0;
-    int tp = 0, bp = n_rbuf + iw, outstanding = 0;      // oldest: tile, its buffer; instructions in flight
-    bp -= bp >= nbuf ? nbuf : 0;
-    auto post_oldest = [&]() {           // its bytes have landed
-        const int tl = tp & 63;
-        if (lane == 0) {
-            *(volatile lds32_t*)&ctl->bmeta[bp] = (uint32_t)__builtin_amdgcn_readlane(v_meta, tl);
-            *(volatile lds32_t*)&ctl->ready[bp] = (uint32_t)(iw + PISS * tp + 1);
-        }
-        outstanding -= __builtin_amdgcn_readlane(v_ni, tl);
-        tp++;
-        bp += PISS;
-        bp -= bp >= nbuf ? nbuf : 0;
-    };
-    // wait until the oldest tile has landed (at most the later ones'
-    // instructions outstanding), then post it
-    auto land_oldest = [&]() {
-        wait_vm(outstanding - __builtin_amdgcn_readlane(v_ni, tp & 63));
-        post_oldest();
-    };
-    auto flush = [&]() {
-        WM_WAIT_VMCNT(0);
-        while (tp < t_next) post_oldest();
-    };
+    // the tiles in flight are th .. ti-1; lane t % 64 of v_ni / v_meta: tile
+    // t's instruction count and meta word (0x100 | first byte's offset in the
+    // buffer, 0: no weights)
+    int v_ni = 0, v_meta = 0, th = 0, ti = 0, outstanding = 0;
 
-    int b = bp;                          // buffer of the next tile
-    for (t_next = 0; t_next < ntile; t_next++) {
-        const int t = t_next;
-        const int h = t >> 6, tl = t & 63;
-        const int s = iw + PISS * t;
-        const int kind = __builtin_amdgcn_readlane(h ? d_kind[1] : d_kind[0], tl);
-        if (!routed && routed_kind(kind)) {
-            flush();
-            lds_wait(ctl, &ctl->routed, 1u, a.status, lane);
-            // the expert of every routed tile (the shared ones keep theirs)
-            const uint64_t g = sval(a.gate), u = sval(a.up), dn = sval(a.down);
-            const uint64_t gs = sval64(a.gstride), us = sval64(a.ustride), ds = sval64(a.dstride);
-#pragma unroll
-            for (int hh = 0; hh < 2; hh++) {
-                const int sl = routed_kind(d_kind[hh]) ? d_slot[hh] : 0;
+    // Send tile t (= ti); false (nothing sent) when it needs a pick that is not
+    // known yet and !block.
+    auto try_issue = [&](int t, bool block) -> bool {
+        const int tl = t & 63;
+        const int kind = __builtin_amdgcn_readlane(d_kind, tl);
+        if (routed_kind(kind)) {
+            const int slot = __builtin_amdgcn_readlane(d_slot, tl);
+            if (slot >= picked) {
+                if ((int)lds_ld(&ctl->npicked) <= slot) {
+                    if (!block) return false;
+                    lds_wait(ctl, &ctl->npicked, (uint32_t)(slot + 1), a.status, lane);
+                }
+                picked = (int)lds_ld(&ctl->npicked);
+                // the addresses of the routed tiles whose expert is now known
+                const uint64_t g = sval(a.gate), u = sval(a.up), dn = sval(a.down);
+                const uint64_t gs = sval64(a.gstride), us = sval64(a.ustride), ds = sval64(a.dstride);
+                const bool now_known = routed_kind(d_kind) && d_slot < picked;
+                const int sl = now_known ? d_slot : 0;
                 const int64_t e = (int)lds_ld((const lds32_t*)&ctl->ids[sl]);
                 const bool ok = lds_ld((const lds32_t*)&ctl->valid[sl]) != 0u;
-                const uint64_t base = d_kind[hh] == K_RG ? g : d_kind[hh] == K_RU ? u : dn;
-                const uint64_t stride = d_kind[hh] == K_RG ? gs : d_kind[hh] == K_RU ? us : ds;
-                if (routed_kind(d_kind[hh])) d_addr[hh] = ok ? base + (uint64_t)e * stride + (uint64_t)d_off[hh] : 0ull;
+                const uint64_t base = d_kind == K_RG ? g : d_kind == K_RU ? u : dn;
+                const uint64_t stride = d_kind == K_RG ? gs : d_kind == K_RU ? us : ds;
+                if (now_known) d_addr = ok ? base + (uint64_t)e * stride + (uint64_t)d_off : 0ull;
             }
-            routed = true;
         }
-        if (b < n_rbuf && !rfree) {
-            if (lds_ld(&ctl->router_done[0]) == 0u || lds_ld(&ctl->router_done[1]) == 0u) {
-                flush();
-                wait_all(ctl, ctl->router_done, 2, a.status, lane);
-            }
+        if (!rfree) {
+            wait_all(ctl, ctl->router_done, 2, a.status, lane);
             rfree = true;
         }
-        // the buffer's previous tile must be processed; meanwhile post the
-        // tiles in flight one by one, oldest first (its wave may need one)
-        while (s >= nbuf && lds_ld(&ctl->done[b]) < (uint32_t)(s - nbuf + 1)) {
-            if (tp < t) {
-                land_oldest();
-            } else {
-                lds_wait(ctl, &ctl->done[b], (uint32_t)(s - nbuf + 1), a.status, lane);
-                break;
-            }
-        }
-        const uint64_t A = h ? d_addr[1] : d_addr[0];
-        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)A, tl);
-        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(A >> 32), tl);
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)d_addr, tl);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(d_addr >> 32), tl);
         const uint64_t G = ((uint64_t)hi << 32) | lo;
-        lds8_t* buf = lds + a.o_ring + b * a.ring_buf;
+        lds8_t* buf = ring + (t % PRING) * a.ring_buf;
         int ni = 0;
         if (G) {
-            const int nb = __builtin_amdgcn_readlane(h ? d_nb[1] : d_nb[0], tl);
+            const int nb = __builtin_amdgcn_readlane(d_nb, tl);
             switch (kind) {
             case K_SG: case K_SU: ni = ring_dma<SGUT>(G, nb, lane, buf); break;
             case K_RG: case K_RU: ni = ring_dma<GUT>(G, nb, lane, buf); break;
@@ -408,37 +398,8 @@ WM_DEV void issue_wave(const PersistArgs& a, uint8_t* smem, int i_v, int lane) {
         v_ni = lane == tl ? ni : v_ni;
         v_meta = lane == tl ? (G ? (int)(0x100u | (lo & 15u)) : 0) : v_meta;
         outstanding += ni;
-        b += PISS;
-        b -= b >= nbuf ? nbuf : 0;
-        if (t + 1 - tp > PD) land_oldest();
-    }
-    flush();
-}
-
-// ---- compute wave c
-template <int GUT, int DT, int SGUT, int SDT>
-WM_DEV void consume_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lane) {
-    lctl_t* ctl = (lctl_t*)smem;
-    lds8_t* lds = (lds8_t*)smem;
-    const int wave = __builtin_amdgcn_readfirstlane(wave_v);
-    const int K = a.K, sh = a.has_shared, H = a.H, I = a.I, nbuf = a.nbuf, n_rbuf = a.n_rbuf;
-    const int nseg_dn = I / SEG;
-    // geometry (lanes per row: powers of two; a tile is 64 segments, so every
-    // lane holds one)
-    const int lg_gu = lg_tile_lanes(H), lg_dn = lg_tile_lanes(I);
-    const int sub_gu = lane & ((1 << lg_gu) - 1), rig_gu = lane >> lg_gu;
-    const int sub_dn = lane & ((1 << lg_dn) - 1), rig_dn = lane >> lg_dn;
-
-    // lane t: this wave's tile t (s = wave + PW * t)
-    int ntile, d_kind, d_slot, d_out, d_rows;
-    {
-        const Part P = partition(a);
-        TileList L;
-        L.init(K, sh, P.ngu, P.ndn);
-        ntile = (L.n - wave + PW - 1) / PW;
-        const TileDesc d = tile_desc<GUT, DT, SGUT, SDT>(a, P, L, wave + PW * lane, lg_gu, lg_dn);
-        d_kind = d.kind; d_slot = d.slot; d_out = d.out; d_rows = d.rows;
-    }
+        return true;
+    };
 
     // operand in registers and what it is: 1000 + type (x) or the slot (act)
     XOp xo;
@@ -448,15 +409,16 @@ WM_DEV void consume_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int la
     lf32_t* sums = (lf32_t*)(lds + a.o_gu);
     lf32_t* yarr = (lf32_t*)(lds + a.o_y);
 
-    // Row sums of tile t in buffer b (meta: 0x100 | first byte's offset, 0:
-    // no weights).
-    auto process = [&](int t, int b, uint32_t meta) {
-        const int kind = __builtin_amdgcn_readlane(d_kind, t);
-        const int slot = __builtin_amdgcn_readlane(d_slot, t);
-        const int out = __builtin_amdgcn_readlane(d_out, t);
-        const int nrow = __builtin_amdgcn_readlane(d_rows, t);
+    // Row sums of tile t.
+    auto process = [&](int t) {
+        const int tl = t & 63;
+        const int kind = __builtin_amdgcn_readlane(d_kind, tl);
+        const int slot = __builtin_amdgcn_readlane(d_slot, tl);
+        const int out = __builtin_amdgcn_readlane(d_out, tl);
+        const int nrow = __builtin_amdgcn_readlane(d_rows, tl);
+        const uint32_t meta = (uint32_t)__builtin_amdgcn_readlane(v_meta, tl);
         const bool has_w = meta != 0u;
-        const lds8_t* buf = lds + a.o_ring + b * a.ring_buf + (meta & 15u);
+        const lds8_t* buf = ring + (t % PRING) * a.ring_buf + (meta & 15u);
         auto rowsum = [&](auto tag_t, int lpr) -> float {
             constexpr int T = decltype(tag_t)::value;
             if (!has_w) return 0.0f;
@@ -498,7 +460,10 @@ WM_DEV void consume_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int la
         }
     };
 
-    // ---- x operand records (8 lanes per segment, 8 segments per wave)
+    if (!active) lds_set(&ctl->progress[wave], 0xFFFFFFFFu, lane);
+    // ---- the first tiles (waves whose rings are free), then the x operand
+    // records (8 lanes per segment, 8 segments per wave) while they fly
+    if (rfree) while (ti < ntile && ti < PRING && try_issue(ti, false)) ti++;
     {
         const int nseg = H / SEG, part = lane & 7;
         const bool two = sh && SGUT != GUT;
@@ -514,25 +479,17 @@ WM_DEV void consume_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int la
     wait_all(ctl, ctl->xop_built, PW, a.status, lane);
     if (wave == 0 && lane == 0) ctl->t[8] = now();
 
-    int b = n_rbuf + wave;
-    b -= b >= nbuf ? nbuf : 0;
-    for (int t = 0; t < ntile; t++, b = b + PW - (b + PW >= nbuf ? nbuf : 0)) {
-        const int s = wave + PW * t;
-        // the tile's bytes (a short spin: this is the common wait)
-        uint32_t it = 0;
-        while (lds_ld(&ctl->ready[b]) < (uint32_t)(s + 1)) {
-            if (++it > PSPIN || aborted(ctl)) {
-                give_up(ctl, a.status, lane);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        process(t, b, lds_ld(&ctl->bmeta[b]));
+    while (th < ntile) {
+        while (ti < ntile && ti - th < PRING && try_issue(ti, ti == th)) ti++;
+        // the head's bytes have landed once at most the later tiles'
+        // instructions are outstanding
+        wait_vm(outstanding - __builtin_amdgcn_readlane(v_ni, th & 63));
+        process(th);
         // progress after the row sums (LDS executes one wave's writes in order)
-        if (lane == 0) *(volatile lds32_t*)&ctl->progress[wave] = (uint32_t)(s + PW);
-        wave_lds_sync();          // every lane's reads of the buffer are done before it is released
-        if (lane == 0) *(volatile lds32_t*)&ctl->done[b] = (uint32_t)(s + 1);
+        if (lane == 0) *(volatile lds32_t*)&ctl->progress[wave] = (uint32_t)(wave + ns * (th + 1));
+        wave_lds_sync();          // every lane's reads of the buffer are done before it is refilled
+        outstanding -= __builtin_amdgcn_readlane(v_ni, th & 63);
+        th++;
     }
     lds_set(&ctl->progress[wave], 0xFFFFFFFFu, lane);
     if (wave == 0 && lane == 0) ctl->t[9] = now();
@@ -581,6 +538,7 @@ WM_DEV void router_chains(const lds8_t* lx, int region, int H, int r0, int ra, i
                           uint64_t* tlogits, int lane) {
     const int q = lane >> 4, c = lane & 15;
     const int row = q == 0 ? ra : (q == 1 ? rb : -1);
+    if (row < 0) return;                            // (idle lanes take no LDS bandwidth)
     const lf32_t* xr = (const lf32_t*)lx;
     const lf32_t* wr = (const lf32_t*)(lx + (1 + (row >= 0 ? row : 0)) * region);
     const int H16 = H - (H & 15), nsteps = H16 / 16;
@@ -615,7 +573,7 @@ WM_DEV void router_chains(const lds8_t* lx, int region, int H, int r0, int ra, i
     if (c == 0)
         for (int col = H16; col < H; col++) acc = fmaf(wr[col], xr[col], acc);
     acc = __shfl(acc, lane & ~15);                  // the row's total (lane 0 of the row) in all its lanes
-    if (row >= 0 && c < P_REP) gst_agent64(tlogits + (int64_t)c * E + r0 + row, tagged(tag, acc));
+    if (c < P_REP) gst_agent64(tlogits + (int64_t)c * E + r0 + row, tagged(tag, acc));
 }
 
 // Routing from replica `rep` of the tagged logits (polled, with a pause
@@ -631,7 +589,7 @@ WM_DEV void route_tagged(const PersistArgs& a, lctl_t* ctl, int rep, uint32_t ta
     // workgroup would take bandwidth from the weight streams)
     uint64_t tv[MAXV];
 #pragma unroll
-    for (int i = 0; i < MAXV; i++) tv[i] = gld_agent64(src + min(lane + 64 * i, E - 1));
+    for (int i = 0; i < MAXV; i++) tv[i] = gld_first64(src + min(lane + 64 * i, E - 1));
     uint32_t it = 0;
     while (true) {
         bool ok = true;
@@ -653,39 +611,51 @@ WM_DEV void route_tagged(const PersistArgs& a, lctl_t* ctl, int rep, uint32_t ta
     for (int i = 0; i < MAXV; i++) lv[i] = __builtin_bit_cast(float, (uint32_t)tv[i]);
     SortedPicker<MAXV> pk;
     pk.init_vals(lv, E, lane);
-    if (lane == 0) ctl->t[28] = now();
-    float my_v = 0.0f;
-    my_e = 0;
+    // lane k keeps pick k's key; ids and values are decoded after the loop
+    uint64_t kb = 0ull;
     degenerate = false;
     for (int k = 0; k < K; k++) {
         const uint64_t best = pk.next();
         degenerate = degenerate || best == 0ull;
-        if (lane == k) { my_e = Picker<MAXV>::id_of(best); my_v = pk.value_of(best); }
+        kb = lane == k ? best : kb;
+        // each pick goes out at once: its slot's weights can start streaming
+        if (lane == 0) {
+            ctl->ids[k] = Picker<MAXV>::id_of(best);
+            ctl->valid[k] = 1;
+        }
+        lds_set(&ctl->npicked, (uint32_t)(k + 1), lane);
     }
-    if (lane == 0) ctl->t[29] = now();
+    my_e = Picker<MAXV>::id_of(kb);
+    const float my_v = pk.value_of(kb);
     const bool mine = lane < K;
-    float wmax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_v), 0));
-    for (int k = 1; k < K; k++) {
-        const float vk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_v), k));
-        if (vk > wmax) wmax = vk;
-    }
+    // the sequential maximum over the picks in k order is pick 0's value: the
+    // picks come in descending order, and a degenerate pick's value
+    // (logits[0], itself invalid or already picked) never compares greater
+    const float wmax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_v), 0));
     const float ex = mine ? expf(my_v - wmax) : 0.0f;
     float wsum = 0.0f;
     for (int k = 0; k < K; k++) wsum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), k));
     wk = wsum > 0.0f ? ex / wsum : ex;
     nonfinite = __builtin_amdgcn_ballot_w64(mine && !isfinite(wk)) != 0ull;
-    if (lane == 0) ctl->t[30] = now();
 }
 
 // Operand records of the slots at positions q0 .. q0+n-1 of the down order
 // (n * passes <= 4, a pass = 8 segments, 8 lanes per segment, 8 values per
-// lane): reads replica `rep` of their tagged SwiGLU outputs, all loads in
-// flight together, until every word carries `tag`, then builds the records.
+// lane) from replica `rep` of their tagged SwiGLU outputs.  Each pass's 4 KB
+// of tagged words comes into this staging wave's LDS area with LDS-DMA (1 KB
+// per instruction, so every request is a whole run of cache lines; the first
+// read through the L2, re-reads at agent scope) until every word carries
+// `tag`; then each lane takes its 8 values from LDS and builds its part of
+// the records.
 template <int DT, int SDT>
 WM_DEV void stage_batch(const PersistArgs& a, lctl_t* ctl, lds8_t* lds, int q0, int n, uint32_t tag, int rep,
-                        int lane) {
+                        int sidx, int lane) {
     const int K = a.K, sh = a.has_shared, I = a.I, nseg = I / SEG, passes = (nseg + 7) / 8;
     const int part = lane & 7;
+    lds8_t* stg = lds + a.o_stage + sidx * 4 * 4096;
+    // the records are on the critical path of every wave's down tiles: this
+    // wave goes ahead of the streaming waves while it stages
+    __builtin_amdgcn_s_setprio(2);
     uint64_t tv[4][8];
     int slot[4], seg[4];
 #pragma unroll
@@ -698,23 +668,43 @@ WM_DEV void stage_batch(const PersistArgs& a, lctl_t* ctl, lds8_t* lds, int q0, 
     while (true) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const bool on = i < n * passes && seg[i] < nseg;
-            const int col = on ? (slot[i] == K ? seg_col(SDT, seg[i], 8 * part) : seg_col(DT, seg[i], 8 * part)) : 0;
-            const uint64_t* src = a.tact + ((int64_t)slot[i] * P_AREP + rep) * I + col;
+            if (i < n * passes) {
+                const int c0 = (i % passes) * 512;                     // first column of the pass
+                const int nch = min(256, ((I - c0) * 8) >> 4);          // granules of the pass inside the row
+                const uint8_t* src = (const uint8_t*)(a.tact + ((int64_t)slot[i] * P_AREP + rep) * I + c0);
 #pragma unroll
-            for (int j = 0; j < 8; j++) tv[i][j] = on ? gld_agent64(src + j) : tagged(tag, 0.0f);
+                for (int k = 0; k < 4; k++) {
+                    const int g = min(lane + 64 * k, nch - 1);
+                    if (it == 0)
+                        __builtin_amdgcn_global_load_lds((const void*)(src + 16 * g),
+                                                         (__attribute__((address_space(3))) void*)(stg + i * 4096 + 1024 * k),
+                                                         16, 0, 0);
+                    else
+                        __builtin_amdgcn_global_load_lds((const void*)(src + 16 * g),
+                                                         (__attribute__((address_space(3))) void*)(stg + i * 4096 + 1024 * k),
+                                                         16, 0, CPOL_SC1);
+                }
+            }
         }
+        WM_WAIT_VMCNT(0);
         bool ok = true;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < 4; i++) {
+            const bool on = i < n * passes && seg[i] < nseg;
+            const int col = on ? (slot[i] == K ? seg_col(SDT, seg[i], 8 * part) : seg_col(DT, seg[i], 8 * part)) : 0;
+            const lds64_t* w = (const lds64_t*)(stg + i * 4096) + (col - (i % passes) * 512);
+#pragma unroll
+            for (int j = 0; j < 8; j++) tv[i][j] = on ? w[j] : tagged(tag, 0.0f);
 #pragma unroll
             for (int j = 0; j < 8; j++) ok = ok && (uint32_t)(tv[i][j] >> 32) == tag;
+        }
         if (__builtin_amdgcn_ballot_w64(!ok) == 0ull) break;
         if (++it > PSPIN_G || aborted(ctl)) {
             give_up(ctl, a.status, lane);
             break;
         }
-        __builtin_amdgcn_s_sleep(8);
+        __builtin_amdgcn_s_sleep(4);
+        wave_lds_sync();      // every lane has read the area before it is loaded again
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -728,6 +718,8 @@ WM_DEV void stage_batch(const PersistArgs& a, lctl_t* ctl, lds8_t* lds, int q0, 
         }
     }
     for (int i = 0; i < n; i++) lds_set(&ctl->act_ready[slot_at(q0 + i, K, sh)], 1u, lane);
+    __builtin_amdgcn_s_setprio(0);
+    wave_lds_sync();
 }
 
 // Staging wave `sidx` of PSTAGE: the operand records of the slots, in down
@@ -747,7 +739,7 @@ WM_DEV void stage_slots(const PersistArgs& a, lctl_t* ctl, lds8_t* lds, uint32_t
         for (int q = sidx * nb; q < nq; q += PSTAGE * nb) {
             const int n = min(nb, nq - q);
             wait_progress(ctl, (uint32_t)L.gu_end(slot_at(q + n - 1, K, sh)), a.status, lane);
-            stage_batch<DT, SDT>(a, ctl, lds, q, n, tag, P.w % P_AREP, lane);
+            stage_batch<DT, SDT>(a, ctl, lds, q, n, tag, P.w % P_AREP, sidx, lane);
         }
     }
     if (lane == 0) ctl->t[5] = now();
@@ -822,6 +814,7 @@ WM_DEV void helper_router(const PersistArgs& a, uint8_t* smem, int lane) {
         ctl->w[lane] = valid ? wk : 0.0f;
         ctl->valid[lane] = valid ? 1 : 0;
     }
+    lds_set(&ctl->npicked, (uint32_t)K, lane);     // (forced routing: all at once)
     lds_set(&ctl->routed, 1u, lane);
     __builtin_amdgcn_s_setprio(0);
     if (lane == 0) ctl->t[3] = now();
@@ -866,6 +859,7 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
         for (int q = 0; q < nq; q++) {
             const int slot = slot_at(q, K, sh);
             wait_progress(ctl, (uint32_t)L.gu_end(slot), a.status, lane);
+            __builtin_amdgcn_s_setprio(2);
             if (lane == 0 && q < 12) ctl->t[16 + q] = now();
             const bool valid = slot == K || ctl->valid[slot] != 0;
             uint64_t* dst = a.tact + (int64_t)slot * P_AREP * a.I + row0;
@@ -875,11 +869,13 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
                 const float v = valid ? silu_mul(garr[slot * a.gu_cap + r], uarr[slot * a.gu_cap + r]) : 0.0f;
                 gst_agent64(dst + (int64_t)rp * a.I + r, tagged(tag, v));
             }
+            __builtin_amdgcn_s_setprio(0);
         }
     }
     if (lane == 0) ctl->t[4] = now();
     if (P.ndn > 0) {
         wait_progress(ctl, (uint32_t)L.n, a.status, lane);
+        lds_wait(ctl, &ctl->routed, 1u, a.status, lane);     // the weights come after the last pick
         if (lane == 0) ctl->t[6] = now();
         const int rpt = geometry(DT, a.I).rpt;
         const int h0 = P.d0 * rpt, nrows = min(a.H, (P.d0 + P.ndn) * rpt) - h0;
@@ -920,15 +916,13 @@ __global__ __launch_bounds__(PTHREADS) void k_decode_persist(PersistArgs a) {
         ((lds32_t*)(lds8_t*)smem)[i] = i < PW ? (uint32_t)i : 0u;     // progress[w] = w: wave w's first entry
     __syncthreads();
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (wave < PW) consume_wave<GUT, DT, SGUT, SDT>(a, smem, wave, lane);
-    // (the issuers re-issue as soon as a tile lands)
-    else if (wave < PW + PISS) { __builtin_amdgcn_s_setprio(2); issue_wave<GUT, DT, SGUT, SDT>(a, smem, wave - PW, lane); }
+    if (wave < PW) stream_wave<GUT, DT, SGUT, SDT>(a, smem, wave, lane);
     // the router rows and the routing are the critical path: the helper
     // waves win the issue arbitration against the streaming waves until the
     // routing is known (their later polling must not)
-    else if (wave == PW + PISS) { __builtin_amdgcn_s_setprio(3); helper_router<GUT, DT, SGUT, SDT>(a, smem, lane); }
-    else if (wave == PW + PISS + 1) { __builtin_amdgcn_s_setprio(3); helper_publish<GUT, DT, SGUT, SDT>(a, smem, lane); }
-    else helper_stage<DT, SDT>(a, smem, wave - PW - PISS - 1, lane);
+    else if (wave == PW) { __builtin_amdgcn_s_setprio(3); helper_router<GUT, DT, SGUT, SDT>(a, smem, lane); }
+    else if (wave == PW + 1) { __builtin_amdgcn_s_setprio(3); helper_publish<GUT, DT, SGUT, SDT>(a, smem, lane); }
+    else helper_stage<DT, SDT>(a, smem, wave - PW - 1, lane);
 }
 
 template <int GUT, int DT, int SGUT, int SDT>

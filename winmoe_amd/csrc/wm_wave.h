@@ -99,6 +99,9 @@ template <int T> WM_HD constexpr int tile_buf() { return tile_ni<T>() * 1024; }
 // ~14 % faster than with the default policy (6.9 vs 6.1 TB/s, 4352-byte tiles,
 // 3 in flight per wave).
 constexpr int CPOL_NT = 2;
+// Agent-scope coherent read (the sc1 bit): past the XCD's L2, for data other
+// XCDs write during the launch.
+constexpr int CPOL_SC1 = 16;
 template <int NI>
 WM_DEV void tile_dma(const uint8_t* W, int64_t off, int64_t nbytes, int lane, lds8_t* dst) {
     const uintptr_t G = (uintptr_t)(W + off);
@@ -595,35 +598,55 @@ template <int T> WM_DEV void xop_part(const float (&v)[8], int part, lds32_t* re
     constexpr bool Q8 = (T == Q8_0);
     constexpr int RUNLEN = (T == Q8_0 || T == Q4_K || T == Q5_K) ? 32 : 16;
     float amax = 0.0f;
-    int fin = 1;
+    uint32_t fin = 1u;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         amax = fmaxf(amax, fabsf(v[i]));
-        fin &= isfinite(v[i]) ? 1 : 0;
+        fin &= isfinite(v[i]) ? 1u : 0u;
     }
-#pragma unroll
-    for (int m = 1; m <= 4; m <<= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, m));
-        fin &= __shfl_xor(fin, m);
-    }
-    const bool finite = fin != 0;
+    // maximum / all-finite over the segment's 8 lanes (DPP within groups of
+    // 8: xor 1, xor 2, then the mirror of the two quads)
+    amax = fmaxf(amax, dpp_f32<DPP_XOR1>(amax));
+    amax = fmaxf(amax, dpp_f32<DPP_XOR2>(amax));
+    amax = fmaxf(amax, dpp_f32<DPP_HALF_MIRROR>(amax));
+    fin = min(fin, dpp_u32<DPP_XOR1>(fin));
+    fin = min(fin, dpp_u32<DPP_XOR2>(fin));
+    fin = min(fin, dpp_u32<DPP_HALF_MIRROR>(fin));
+    const bool finite = fin != 0u;
     const float inv = amax > 0.0f ? 32639.0f / amax : 0.0f;
-    lds8_t* rb = (lds8_t*)rec;
+    // the 8 hi and 8 lo digit bytes, packed little-endian in two dwords each
+    uint32_t hb[2] = {0u, 0u}, lb[2] = {0u, 0u};
     int psum = 0;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const int j = 8 * part + i;
         int xi = finite ? (int)rintf(v[i] * inv) : 0;
         xi = xi > 32639 ? 32639 : (xi < -32639 ? -32639 : xi);
         const int l = ((xi + 128) & 255) - 128;
         const int h = (xi - l) >> 8;
-        const int p = Q8 ? j + 2 + ((j >> 5) << 1) : j;
-        rb[4 * XOP_HI + p] = (uint8_t)(h & 0xFF);
-        rb[4 * XOP_LO + p] = (uint8_t)(l & 0xFF);
+        hb[i >> 2] |= (uint32_t)(h & 0xFF) << (8 * (i & 3));
+        lb[i >> 2] |= (uint32_t)(l & 0xFF) << (8 * (i & 3));
         psum += xi;
     }
-    psum += __shfl_xor(psum, 1);
-    if (RUNLEN == 32) psum += __shfl_xor(psum, 2);
+    lds8_t* rb = (lds8_t*)rec;
+    if (Q8) {
+        // weights j = 8p .. 8p+7 sit at bytes j + 2 (+ 2 more from j = 32): a
+        // 16-bit, a 32-bit and a 16-bit store per digit array
+        const int p0 = 8 * part + 2 + (part >= 4 ? 2 : 0);
+        typedef __attribute__((address_space(3))) uint16_t lds16_t;
+        *(lds16_t*)(rb + 4 * XOP_HI + p0) = (uint16_t)hb[0];
+        *(lds32_t*)(rb + 4 * XOP_HI + p0 + 2) = (hb[0] >> 16) | (hb[1] << 16);
+        *(lds16_t*)(rb + 4 * XOP_HI + p0 + 6) = (uint16_t)(hb[1] >> 16);
+        *(lds16_t*)(rb + 4 * XOP_LO + p0) = (uint16_t)lb[0];
+        *(lds32_t*)(rb + 4 * XOP_LO + p0 + 2) = (lb[0] >> 16) | (lb[1] << 16);
+        *(lds16_t*)(rb + 4 * XOP_LO + p0 + 6) = (uint16_t)(lb[1] >> 16);
+    } else {
+        rec[XOP_HI + 2 * part] = hb[0];
+        rec[XOP_HI + 2 * part + 1] = hb[1];
+        rec[XOP_LO + 2 * part] = lb[0];
+        rec[XOP_LO + 2 * part + 1] = lb[1];
+    }
+    psum += (int)dpp_u32<DPP_XOR1>((uint32_t)psum);
+    if (RUNLEN == 32) psum += (int)dpp_u32<DPP_XOR2>((uint32_t)psum);
     constexpr int LPR = RUNLEN / 8;                  // lanes per run
     if (part % LPR == 0) rec[XOP_SUM + part / LPR] = (uint32_t)psum;
     if (part == 0) {
