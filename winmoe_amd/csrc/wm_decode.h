@@ -111,7 +111,8 @@ struct PersistCtl {
     float w[PMAXK];
     int32_t valid[PMAXK];
     float sgate;
-    uint32_t pad2[2];
+    uint32_t x_in;                 // x is in LDS (the second staging wave loads it)
+    uint32_t pad2;
     uint64_t t[P_TL];              // timeline (device clock)
 };
 

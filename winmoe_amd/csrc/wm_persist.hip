@@ -49,6 +49,7 @@
 namespace wm {
 
 static_assert(PRING >= 1 && PRING <= 8, "a streaming wave keeps at most PRING tiles in its ring");
+static_assert(PSTAGE >= 2, "the second staging wave loads x for the router");
 
 typedef __attribute__((address_space(3))) PersistCtl lctl_t;
 typedef __attribute__((address_space(3))) float lf32_t;
@@ -749,6 +750,12 @@ WM_DEV void stage_slots(const PersistArgs& a, lctl_t* ctl, lds8_t* lds, uint32_t
 template <int DT, int SDT>
 WM_DEV void helper_stage(const PersistArgs& a, uint8_t* smem, int sidx, int lane) {
     lctl_t* ctl = (lctl_t*)smem;
+    if (sidx == 1) {
+        __builtin_amdgcn_s_setprio(3);
+        if (!a.forced) router_dma(a.x, nullptr, a.H, 0, -1, -1, (lds8_t*)smem + a.o_ring, a.x_region, lane);
+        lds_set(&ctl->x_in, 1u, lane);
+        __builtin_amdgcn_s_setprio(0);
+    }
     lds_wait(ctl, &ctl->rows_in, 1u, a.status, lane);
     stage_slots<DT, SDT>(a, ctl, (lds8_t*)smem, ctl->tag, sidx, lane);
 }
@@ -773,8 +780,10 @@ WM_DEV void helper_router(const PersistArgs& a, uint8_t* smem, int lane) {
     bool valid = false;
     if (!a.forced) {
         const int r0 = P.w * a.rr, nr = max(0, min(a.rr, E - r0));
-        // x and rows 0 and 2 here, rows 1 and 3 on the other helper
-        if (nr > 0) router_dma(a.x, a.router, a.H, r0, 0, nr > 2 ? 2 : -1, lds + a.o_ring, a.x_region, lane);
+        // rows 0 and 2 here, rows 1 and 3 on the publishing helper, x on the
+        // second staging wave: three waves' loads land together
+        if (nr > 0) router_dma(nullptr, a.router, a.H, r0, 0, nr > 2 ? 2 : -1, lds + a.o_ring, a.x_region, lane);
+        lds_wait(ctl, &ctl->x_in, 1u, a.status, lane);
         lds_set(&ctl->rows_in, 1u, lane);          // (also when this workgroup has no router rows)
         if (lane == 0) ctl->t[1] = now();
         if (nr > 0)   // rows 0 and 2 here, rows 1 and 3 on the other helper
