@@ -463,3 +463,49 @@ def test_prefill_c5_full(wm, orc):
         worst = max(worst, rel_l2(out[t], od))
     assert worst <= 1e-4, worst
     assert sl.layer.prefill_status() == 0
+
+
+# ------------------------------------------------------------------ GGUF boundary
+
+@pytest.mark.parametrize("name", ["c1", "c3"])
+def test_layer_from_gguf_matches_direct(wm, tmp_path, name):
+    """A layer written as a GGUF file (stacked [H, I, E] / [I, H, E] expert
+    tensors, F32 router [H, E], shared expert) and mapped back with
+    moe_layer_from_gguf decodes bit for bit like the same tensors handed over
+    directly; the per-expert strides come from the tensor sizes."""
+    from winmoe_amd import gguf, synth
+    cfg = synth.CONFIGS[name]
+    E = 24
+    sl = synth.build_layer(cfg, E=E, max_tokens=4)
+    H, I = cfg.H, cfg.I
+    gt, ut, dt = cfg.types
+    tensors = [("blk.3.ffn_gate_exps.weight", (H, I, E), gt, host(sl.gate).tobytes()),
+               ("blk.3.ffn_up_exps.weight", (H, I, E), ut, host(sl.up).tobytes()),
+               ("blk.3.ffn_down_exps.weight", (I, H, E), dt, host(sl.down).tobytes())]
+    if sl.router is not None:
+        tensors.append(("blk.3.ffn_gate_inp.weight", (H, E), 0, host(sl.router).tobytes()))
+    if sl.shared is not None:
+        sh = sl.shared
+        Is = sh.inter
+        tensors += [("blk.3.ffn_gate_shexp.weight", (H, Is), sh.types[0], host(sh.gate).tobytes()),
+                    ("blk.3.ffn_up_shexp.weight", (H, Is), sh.types[1], host(sh.up).tobytes()),
+                    ("blk.3.ffn_down_shexp.weight", (Is, H), sh.types[2], host(sh.down).tobytes())]
+        if sh.gate_inp is not None:
+            tensors.append(("blk.3.ffn_gate_inp_shexp.weight", (H,), 0, host(sh.gate_inp).tobytes()))
+    p = str(tmp_path / "layer.gguf")
+    gguf.write_gguf(p, {"general.architecture": "winmoe", "winmoe.expert_used_count": cfg.K}, tensors,
+                    alignment=64)
+    g = gguf.GGUFFile(p)
+    L = gguf.moe_layer_from_gguf(g, 3, max_tokens=4)
+    assert (L.H, L.I, L.E, L.K) == (H, I, E, cfg.K)
+    X = synth.make_hidden(cfg, tokens=3)
+    routes = synth.forced_routes(cfg, E=E, tokens=3) if cfg.routing != "router" else None
+    for t in range(3):
+        case(f"gguf {name} token={t}")
+        if routes is None:
+            a, b = host(L.decode(X[t])), host(sl.layer.decode(X[t]))
+        else:
+            ids, w = dev(routes[0][t]), dev(routes[1][t])
+            a, b = host(L.decode_forced(X[t], ids, w)), host(sl.layer.decode_forced(X[t], ids, w))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), t
+    assert L.status() == 0
