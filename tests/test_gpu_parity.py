@@ -314,13 +314,14 @@ _KERNEL_FLAGS = {"persist": 8, "item": 4}
 
 
 @pytest.mark.parametrize("kernel", ["persist", "item"])
-@pytest.mark.parametrize("name,E,tokens", [("c1", 64, 4), ("c2", 40, 6), ("c2", 512, 3), ("c3", 24, 4),
-                                           ("c4", 24, 4)])
+@pytest.mark.parametrize("name,E,tokens", [("c1", 64, 4), ("c1", 1000, 3), ("c1", 700, 3), ("c2", 40, 6),
+                                           ("c2", 512, 3), ("c3", 24, 4), ("c4", 24, 4)])
 def test_fused_step_matches_multi_kernel(wm, name, E, tokens, kernel):
     """One fused launch per token (persistent or work-item-list kernel) == the
     per-phase kernel sequence, bit for bit, over several consecutive tokens
     (the counters and hand-off tags carry over between launches).  E=512 puts
-    two router rows on each workgroup of the persistent kernel."""
+    two router rows on each workgroup of the persistent kernel, E=1000 four
+    (the last workgroups have fewer or none), E=700 three."""
     from winmoe_amd import synth
     cfg = synth.CONFIGS[name]
     sl = synth.build_layer(cfg, E=E, max_tokens=8)
