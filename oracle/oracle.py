@@ -64,6 +64,7 @@ def lib():
         L.wmo_dequant.argtypes = [C.c_int, _vp, C.c_int64, _fp]
         L.wmo_router_logits.argtypes = [_fp, _fp, C.c_int, C.c_int, _fp]
         L.wmo_topk_softmax.argtypes = [_fp, C.c_int, C.c_int, _ip, _fp]
+        L.wmo_rmsnorm.argtypes = [_fp, _fp, _fp, C.c_int, C.c_float]
         L.wmo_sigmoid.restype = C.c_double
         L.wmo_sigmoid.argtypes = [C.c_double]
         L.wmo_matvec.argtypes = [C.c_int, _vp, _dp, C.c_int, C.c_int, _dp]
@@ -100,6 +101,7 @@ def ref():
         R.ref_sigmoid_stable.argtypes = [C.c_float]
         R.ref_router_topk.argtypes = [_fp, _fp, C.c_int, C.c_int, C.c_int, _ip, _fp]
         R.ref_moe_layer_cpu.argtypes = [C.POINTER(WmoLayer), _fp, _ip, _fp, _ip, _fp, _fp]
+        R.wmref_rmsnorm.argtypes = [_fp, _fp, _fp, C.c_int]
         _ref = R
     return _ref
 
@@ -118,6 +120,15 @@ def dequant(qtype: int, blocks: np.ndarray) -> np.ndarray:
     out = np.empty(nb * BLOCK_ELEMS[qtype], dtype=np.float32)
     rc = lib().wmo_dequant(qtype, _ptr(b), nb, _ptr(out, _fp))
     assert rc == 0, rc
+    return out
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    """attention.h:29-44 (wmo_rmsnorm)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    lib().wmo_rmsnorm(_ptr(out, _fp), _ptr(x, _fp), _ptr(w, _fp), x.shape[0], eps)
     return out
 
 

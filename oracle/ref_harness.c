@@ -31,6 +31,7 @@
 #include "gguf_parser.h"     /* GGML_TYPE_* ids used by transformer.h */
 #include "transformer.h"     /* router_topk :107-152 */
 #include "deltanet_impl.h"   /* sigmoid_stable :108-115 */
+#include "attention.h"       /* rmsnorm :29-44 */
 
 #include "wm_oracle.h"       /* wmo_layer descriptor, Q2_K/Q3_K dequant (port) */
 
@@ -283,3 +284,6 @@ REF_API int ref_moe_layer_cpu(const wmo_layer* L, const float* normed, const int
     free(normed_q8k);
     return g_used_port;
 }
+
+/* attention.h:29-44, as compiled from the reference (eps fixed at 1e-6 there). */
+void wmref_rmsnorm(float* out, const float* x, const float* w, int dim) { rmsnorm(out, x, w, dim); }

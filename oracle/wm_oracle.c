@@ -18,6 +18,10 @@
  *                 them); pinned by hand-built per-field blocks and quantise ->
  *                 dequantise round trips
  *   router        bit-exact vs reference router_topk (oracle/_ref), planted ties
+ *   rmsnorm       closed forms (constant and one-hot rows: exact results) and
+ *                 a sequential fp64 sum in numpy (the order matters only in
+ *                 the last bits of ss); not compiled from the reference
+ *                 (attention.h is an AVX2 header of the attention layer)
  *   expert / MoE  brute-force fp64 on tiny shapes vs an independent dense path
  */
 #include "wm_oracle.h"
@@ -348,4 +352,11 @@ int wmo_moe_layer(const wmo_layer* L, const float* x, const int32_t* forced_ids,
     }
     free(xd);
     return rc ? rc : degenerate;
+}
+
+void wmo_rmsnorm(float* out, const float* x, const float* w, int dim, float eps) {
+    double ss = 0.0;
+    for (int i = 0; i < dim; i++) ss += (double)x[i] * (double)x[i];
+    const float scale = 1.0f / sqrtf((float)(ss / dim) + eps);
+    for (int i = 0; i < dim; i++) out[i] = (x[i] * scale) * w[i];
 }

@@ -50,6 +50,9 @@ void  wmo_router_logits(const float* x, const float* W, int H, int E, float* log
 int   wmo_topk_softmax(const float* logits, int E, int K, int32_t* ids, float* w);
 
 /* Branch-stable sigmoid of deltanet_impl.h:108-115, evaluated in double. */
+/* RMSNorm (attention.h:29-44): ss = sum of (double)x[i]^2 in index order,
+ * scale = 1 / sqrtf((float)(ss / dim) + eps), out[i] = (x[i] * scale) * w[i]. */
+void  wmo_rmsnorm(float* out, const float* x, const float* w, int dim, float eps);
 double wmo_sigmoid(double x);
 
 /* y[r] = sum_c dequant(W)[r][c] * x[c]: fp32 dequantised weights, fp64

@@ -356,3 +356,38 @@ def test_moe_layer_vs_reference_cpu_path(orc):
     assert ids.tolist() == rids.tolist() and same_bits(w, rw)
     rel = np.linalg.norm(rout - out) / np.linalg.norm(out)
     assert rel < 3e-2, rel      # Q8_K activation quantisation in the reference path (~7e-3 typical)
+
+
+# ------------------------------------------------------------------ RMSNorm (the step's producer)
+
+def test_rmsnorm_vs_live_reference(orc):
+    """wmo_rmsnorm == the reference's rmsnorm (attention.h:29-44, compiled from
+    source), bit for bit, including dims with a scalar tail."""
+    R = orc.ref()
+    if R is None:
+        pytest.skip("reference build not available on this host")
+    rng = np.random.default_rng(5)
+    fp = C.POINTER(C.c_float)
+    for dim in (8, 13, 256, 1000, 2048, 4096):
+        for scale in (1e-3, 1.0, 30.0):
+            x = (rng.standard_normal(dim) * scale).astype(np.float32)
+            w = (1.0 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+            got = orc.rmsnorm(x, w)
+            ref = np.empty(dim, np.float32)
+            R.wmref_rmsnorm(ref.ctypes.data_as(fp), x.ctypes.data_as(fp), w.ctypes.data_as(fp), dim)
+            assert same_bits(got, ref), (dim, scale)
+
+
+def test_rmsnorm_closed_forms(orc):
+    """Rows whose fp64 sum of squares is exact: a constant row (ss = dim c^2)
+    and a one-hot row (ss = v^2), with the float scale formed as written."""
+    dim = 4096
+    w = np.linspace(0.5, 1.5, dim, dtype=np.float32)
+    for c in (0.5, 3.0, -2.0):
+        x = np.full(dim, c, np.float32)
+        scale = np.float32(1.0) / np.sqrt(np.float32(np.float64(dim) * c * c / dim) + np.float32(1e-6))
+        assert same_bits(orc.rmsnorm(x, w), (x * scale) * w)
+    x = np.zeros(dim, np.float32)
+    x[17] = 8.0
+    scale = np.float32(1.0) / np.sqrt(np.float32(64.0 / dim) + np.float32(1e-6))
+    assert same_bits(orc.rmsnorm(x, w), (x * scale) * w)
