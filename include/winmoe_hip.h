@@ -93,6 +93,13 @@ typedef struct wm_layer_desc {
     const void* sh_up;
     const void* sh_down;     /* [H][I_s/QK] */
     const float* sh_gate_inp;/* [H] fp32 sigmoid gate of the shared expert, or NULL */
+    /* The step either side of the layer (fused decode step, persistent
+     * kernel only; other paths return WM_EINVAL when norm_w is set): */
+    const float* norm_w;     /* [H] fp32: the decode input is the residual stream h and the
+                                layer's x = rmsnorm(h) (attention.h:29-44: fp64 sum of squares,
+                                scale = 1/sqrtf(ss/H + norm_eps), (h*scale)*w); NULL: x is given */
+    float norm_eps;          /* 1e-6 in the reference */
+    int32_t add_residual;    /* with norm_w: out = h + moe_out (winmoe_inference.c:2041) */
 } wm_layer_desc;
 
 /* ---------------------------------------------------------------- library */

@@ -510,3 +510,63 @@ def test_layer_from_gguf_matches_direct(wm, tmp_path, name):
             a, b = host(L.decode_forced(X[t], ids, w)), host(sl.layer.decode_forced(X[t], ids, w))
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), t
     assert L.status() == 0
+
+
+# ------------------------------------------------------------------ RMSNorm in, residual out
+
+@pytest.mark.parametrize("name,E", [("c1", 64), ("c2", 40), ("c4", 24)])
+def test_fused_rmsnorm_and_residual(wm, orc, name, E):
+    """decode(h) with norm_w and add_residual == h + decode(rmsnorm(h)), the
+    RMSNorm by the oracle (pinned to the reference's rmsnorm), bit for bit,
+    with the same routing trace.  The kernel sums the squares in a different
+    order than the reference (index order), which could move the last bits of
+    ss; (float)(ss / H) is the same on these seeds."""
+    import torch
+    from winmoe_amd import synth
+    from winmoe_amd.moe import MoELayer
+    cfg = synth.CONFIGS[name]
+    sl = synth.build_layer(cfg, E=E, max_tokens=8)
+    c = sl.cfg
+    g = torch.Generator(device="cuda").manual_seed(11)
+    w = (1.0 + 0.1 * torch.randn(c.H, generator=g, device="cuda")).float()
+    normed = MoELayer(c.H, c.I, E, c.K, sl.router, sl.gate, sl.up, sl.down, c.types, shared=sl.shared, max_tokens=8,
+                      norm_w=w, add_residual=True)
+    plain = synth.twin_layer(sl, multi_kernel=False)
+    Hs = 3.0 * torch.randn(4, c.H, generator=g, device="cuda")
+    routes = synth.forced_routes(cfg, E=E, tokens=4) if cfg.routing != "router" else None
+    for t in range(4):
+        case(f"rmsnorm {name} E={E} token={t}")
+        h = Hs[t].contiguous()
+        x = orc.rmsnorm(host(h), host(w))
+        if routes is None:
+            a = host(normed.decode(h))
+            b = host(plain.decode(dev(x)))
+        else:
+            ids, wt = dev(routes[0][t]), dev(routes[1][t])
+            a = host(normed.decode_forced(h, ids, wt))
+            b = host(plain.decode_forced(dev(x), ids, wt))
+        assert np.array_equal(a.view(np.uint32), (host(h) + b).view(np.uint32)), t
+    ta, _ = normed.trace()
+    tb, _ = plain.trace()
+    assert np.array_equal(host(ta[:4]), host(tb[:4]))
+    assert normed.status() == 0
+
+
+def test_rmsnorm_rejected_off_the_persistent_path(wm):
+    """The fused RMSNorm / residual belong to the persistent decode step: the
+    per-phase and item-list paths and prefill refuse them (WM_EINVAL)."""
+    import torch
+    from winmoe_amd import _lib, synth
+    from winmoe_amd.moe import MoELayer
+    cfg = synth.CONFIGS["c1"]
+    sl = synth.build_layer(cfg, max_tokens=4)
+    c = sl.cfg
+    w = torch.ones(c.H, device="cuda")
+    for flags in (_lib.FLAG_MULTI_KERNEL, _lib.FLAG_ITEM_KERNEL):
+        L = MoELayer(c.H, c.I, c.E, c.K, sl.router, sl.gate, sl.up, sl.down, c.types, max_tokens=4, norm_w=w)
+        L.desc.flags |= flags
+        with pytest.raises(Exception):
+            L.decode(torch.randn(c.H, device="cuda"))
+    L = MoELayer(c.H, c.I, c.E, c.K, sl.router, sl.gate, sl.up, sl.down, c.types, max_tokens=4, add_residual=True)
+    with pytest.raises(Exception):
+        L.decode(torch.randn(c.H, device="cuda"))

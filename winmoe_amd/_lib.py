@@ -42,6 +42,7 @@ class LayerDesc(C.Structure):
         ("router", _vp), ("gate_exps", _vp), ("up_exps", _vp), ("down_exps", _vp),
         ("gate_stride", _i64), ("up_stride", _i64), ("down_stride", _i64),
         ("sh_gate", _vp), ("sh_up", _vp), ("sh_down", _vp), ("sh_gate_inp", _vp),
+        ("norm_w", _vp), ("norm_eps", C.c_float), ("add_residual", C.c_int32),
     ]
 
 

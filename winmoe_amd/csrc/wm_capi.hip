@@ -491,7 +491,8 @@ static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
     // SwiGLU operand records | x operand records | gate/up row sums | down row sums
     int o = (int)((sizeof(PersistCtl) + 255) / 256 * 256);
     a.x_region = (H * 4 + 1023) / 1024 * 1024;
-    const int router_bytes = forced ? 0 : (1 + rr) * a.x_region;
+    // (with the RMSNorm, x is normalised in LDS also under forced routing)
+    const int router_bytes = forced ? (d->norm_w ? a.x_region : 0) : (1 + rr) * a.x_region;
     a.n_rwaves = (router_bytes + PRING * a.ring_buf - 1) / (PRING * a.ring_buf);
     const int rec = XOP_DW * 4;
     a.o_reg = o; o += (K + 1) * (I / SEG) * rec;
@@ -516,6 +517,7 @@ static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
                              (max_lds_per_wg() / 2 + 256) / 256 * 256);
     if (int rc = aligned_input(x, H, (float*)(ws + L.xin), s)) return rc;
     a.x = x; a.out = out; a.router = d->router;
+    a.norm_w = d->norm_w; a.norm_eps = d->norm_eps; a.add_res = d->norm_w && d->add_residual ? 1 : 0;
     a.gate = (const uint8_t*)d->gate_exps; a.up = (const uint8_t*)d->up_exps; a.down = (const uint8_t*)d->down_exps;
     a.gstride = d->gate_stride ? d->gate_stride : matrix_bytes(gut, I, H);
     a.ustride = d->up_stride ? d->up_stride : matrix_bytes(gut, I, H);
@@ -634,6 +636,12 @@ extern "C" int wm_moe_decode(const wm_layer_desc* d, const float* x, float* out,
     int32_t* ids = (int32_t*)(w8 + L.tr_ids) + (int64_t)slot * d->top_k;
     float* wts = (float*)(w8 + L.tr_w) + (int64_t)slot * d->top_k;
     float* logits = (float*)(w8 + L.logits);
+    if (d->norm_w) {      // RMSNorm in, residual out: the persistent kernel only
+        WM_CHECK_ARG(!(d->flags & (WM_FLAG_MULTI_KERNEL | WM_FLAG_ITEM_KERNEL)));
+        const int rc = run_persist(d, L, w8, x, out, nullptr, nullptr, ids, wts, s);
+        return rc == 1 ? WM_EINVAL : rc;
+    }
+    WM_CHECK_ARG(!d->add_residual);
     if (!(d->flags & WM_FLAG_MULTI_KERNEL)) {
         int rc = run_fused(d, L, w8, x, out, nullptr, nullptr, ids, wts, s);
         if (rc <= 0) return rc;
@@ -663,6 +671,12 @@ extern "C" int wm_moe_decode_forced(const wm_layer_desc* d, const float* x, cons
     int slot = step % max_tokens;
     int32_t* ids = (int32_t*)(w8 + L.tr_ids) + (int64_t)slot * d->top_k;
     float* wts = (float*)(w8 + L.tr_w) + (int64_t)slot * d->top_k;
+    if (d->norm_w) {      // RMSNorm in, residual out: the persistent kernel only
+        WM_CHECK_ARG(!(d->flags & (WM_FLAG_MULTI_KERNEL | WM_FLAG_ITEM_KERNEL)));
+        const int rc = run_persist(d, L, w8, x, out, ids_in, w_in, ids, wts, s);
+        return rc == 1 ? WM_EINVAL : rc;
+    }
+    WM_CHECK_ARG(!d->add_residual);
     if (!(d->flags & WM_FLAG_MULTI_KERNEL)) {
         int rc = run_fused(d, L, w8, x, out, ids_in, w_in, ids, wts, s);
         if (rc <= 0) return rc;
@@ -771,6 +785,7 @@ extern "C" int wm_prefill_workspace_routing(const wm_layer_desc* d, int max_toke
 static int run_prefill(const wm_layer_desc* d, const uint16_t* x, int T, const int32_t* fids, const float* fw,
                        float* out, void* ws, int64_t ws_bytes, int max_tokens, void* stream) {
     if (int rc = validate_desc(d, fids == nullptr)) return rc;
+    WM_CHECK_ARG(!d->norm_w && !d->add_residual);     // the fused RMSNorm is a decode-step feature
     WM_CHECK_ARG(x && out && ws && al(ws, 256) && al(x, 16) && al(out, 16) && T > 0 && T <= max_tokens);
     PfLayout L = pf_layout(d, max_tokens);
     WM_CHECK_ARG(ws_bytes >= L.total);

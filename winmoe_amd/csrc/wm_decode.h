@@ -127,9 +127,12 @@ struct PersistArgs {
     int32_t o_xop, o_xop2;             // LDS: x operand records of the routed / shared gate-up types
     int32_t o_gu, gu_cap;              // LDS: gate and up row sums [K+1][gu_cap] each
     int32_t o_y, y_cap;                // LDS: down row sums [K+1][y_cap]
-    const float* x;
+    const float* x;                    // x, or the residual stream h when norm_w is set
     float* out;
     const float* router;
+    const float* norm_w;               // RMSNorm weight [H] or null
+    float norm_eps;
+    int32_t add_res;                   // out = h + moe_out
     const uint8_t* gate;
     const uint8_t* up;
     const uint8_t* down;

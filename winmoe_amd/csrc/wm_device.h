@@ -26,6 +26,7 @@ typedef __attribute__((address_space(3))) uint8_t lds8_t;
 typedef __attribute__((address_space(3))) uint16_t lds16_t;
 typedef __attribute__((address_space(3))) uint32_t lds32_t;
 typedef __attribute__((address_space(3))) uint64_t lds64_t;
+typedef __attribute__((address_space(3))) float lf32_t;
 
 WM_DEV float h2f(uint32_t bits) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits & 0xFFFFu)); }
 

@@ -52,7 +52,6 @@ static_assert(PRING >= 1 && PRING <= 8, "a streaming wave keeps at most PRING ti
 static_assert(PSTAGE >= 2, "the second staging wave loads x for the router");
 
 typedef __attribute__((address_space(3))) PersistCtl lctl_t;
-typedef __attribute__((address_space(3))) float lf32_t;
 
 constexpr uint32_t PSPIN = 1u << 20;    // LDS polls (~0.2 us each after the first few) before a wait gives up
 constexpr uint32_t PSPIN_G = 1u << 17;  // device-memory polls (~1 us each) before a wait gives up
@@ -469,9 +468,18 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
         const int nseg = H / SEG, part = lane & 7;
         const bool two = sh && SGUT != GUT;
         float v[8], v2[8];
+        // the normalised x lives in LDS (the router's x region) until the
+        // router helpers are done, which needs this wave's records first
+        if (a.norm_w) lds_wait(ctl, &ctl->x_in, 1u, a.status, lane);
+        const lf32_t* xl = (const lf32_t*)(lds + a.o_ring);
         for (int sg = wave * 8 + (lane >> 3); sg < nseg; sg += PW * 8) {
-            xop_part_fetch<GUT>(a.x, sg, part, v);
-            if (two) xop_part_fetch<SGUT>(a.x, sg, part, v2);
+            if (a.norm_w) {
+                xop_part_fetch_lds<GUT>(xl, sg, part, v);
+                if (two) xop_part_fetch_lds<SGUT>(xl, sg, part, v2);
+            } else {
+                xop_part_fetch<GUT>(a.x, sg, part, v);
+                if (two) xop_part_fetch<SGUT>(a.x, sg, part, v2);
+            }
             xop_part<GUT>(v, part, (lds32_t*)(lds + a.o_xop) + sg * XOP_DW);
             if (two) xop_part<SGUT>(v2, part, (lds32_t*)(lds + a.o_xop2) + sg * XOP_DW);
         }
@@ -723,6 +731,24 @@ WM_DEV void stage_batch(const PersistArgs& a, lctl_t* ctl, lds8_t* lds, int q0, 
     wave_lds_sync();
 }
 
+// RMSNorm of the residual stream h in LDS, in place (attention.h:29-44):
+// ss = sum of (double)h[i]^2 (each lane a strided part, then the lanes; the
+// reference adds in index order, which can differ in the last bits of ss),
+// scale = 1 / sqrtf((float)(ss / H) + eps) correctly rounded, x[i] =
+// (h[i] * scale) * w[i].
+WM_DEV void rmsnorm_lds(lf32_t* xl, const float* __restrict__ w, int H, float eps, int lane) {
+    double ss = 0.0;
+    for (int i = lane; i < H; i += 64) {
+        const double v = (double)xl[i];
+        ss = fma(v, v, ss);          // v * v is exact in fp64: the same as a product then a sum
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
+    const float scale = __fdiv_rn(1.0f, __fsqrt_rn((float)(ss / (double)H) + eps));
+    for (int i = lane; i < H; i += 64) xl[i] = (xl[i] * scale) * w[i];
+    WM_WAIT_LGKM0();
+}
+
 // Staging wave `sidx` of PSTAGE: the operand records of the slots, in down
 // order, in batches of up to 4 passes of loads; batch b is staged by wave
 // b % PSTAGE, so that the next batches' loads are in flight while one batch
@@ -752,7 +778,9 @@ WM_DEV void helper_stage(const PersistArgs& a, uint8_t* smem, int sidx, int lane
     lctl_t* ctl = (lctl_t*)smem;
     if (sidx == 1) {
         __builtin_amdgcn_s_setprio(3);
-        if (!a.forced) router_dma(a.x, nullptr, a.H, 0, -1, -1, (lds8_t*)smem + a.o_ring, a.x_region, lane);
+        lds8_t* xl = (lds8_t*)smem + a.o_ring;
+        if (!a.forced || a.norm_w) router_dma(a.x, nullptr, a.H, 0, -1, -1, xl, a.x_region, lane);
+        if (a.norm_w) rmsnorm_lds((lf32_t*)xl, a.norm_w, a.H, a.norm_eps, lane);
         lds_set(&ctl->x_in, 1u, lane);
         __builtin_amdgcn_s_setprio(0);
     }
@@ -849,9 +877,16 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
         const int r0 = P.w * a.rr, nr = max(0, min(a.rr, a.E - r0));
         if (nr > 1) router_chains(lds + a.o_ring, a.x_region, a.H, r0, 1, nr > 3 ? 3 : -1, a.E, tag, a.tlogits, lane);
     }
+    // the shared gate: from the normalised x in LDS before the x region is
+    // given up, or from x in memory after
+    if (sh && a.sh_gate_inp && a.norm_w) {
+        lds_wait(ctl, &ctl->x_in, 1u, a.status, lane);
+        const float g = wave_shgate_lds((const lf32_t*)(lds + a.o_ring), a.sh_gate_inp, a.H, lane);
+        if (lane == 0) ctl->sgate = g;
+    }
     lds_set(&ctl->router_done[1], 1u, lane);
     __builtin_amdgcn_s_setprio(0);
-    if (sh && a.sh_gate_inp) {
+    if (sh && a.sh_gate_inp && !a.norm_w) {
         const float g = wave_shgate(a.x, a.sh_gate_inp, a.H, lane);
         if (lane == 0) ctl->sgate = g;
     }
@@ -894,6 +929,7 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
             for (int k = 0; k < K; k++)
                 if (ctl->valid[k]) acc = fmaf(ctl->w[k], yarr[k * a.y_cap + r], acc);
             if (sh) acc = acc + yarr[K * a.y_cap + r];
+            if (a.add_res) acc = a.x[h0 + r] + acc;          // residual + moe_out
             a.out[h0 + r] = acc;
         }
     }

@@ -576,6 +576,26 @@ WM_DEV float wave_shgate(const float* __restrict__ x, const float* __restrict__ 
     return sigmoid_stable((float)acc);
 }
 
+// wave_shgate with x in LDS (same order of operations).
+WM_DEV float wave_shgate_lds(const lf32_t* x, const float* __restrict__ g, int H, int lane) {
+    double acc = 0.0;
+    for (int base = 0; base < H; base += 64 * 16) {
+        float gv[16], xv[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int h = min(base + lane + 64 * i, H - 1);
+            gv[i] = g[h];
+            xv[i] = x[h];
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            if (base + lane + 64 * i < H) acc += (double)gv[i] * (double)xv[i];
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
+    return sigmoid_stable((float)acc);
+}
+
 // wave_shgate for a whole workgroup (all threads call it; wave 0 computes,
 // thread 0 writes *out).
 template <bool COH = false>
@@ -667,6 +687,13 @@ template <int T> WM_DEV void xop_part_fetch(const float* src, int seg, int part,
     const f32x4* p = (const f32x4*)(src + seg_col(T, seg, 8 * part));
     const f32x4 a = p[0], b = p[1];
     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+// As xop_part_fetch, from an fp32 vector in LDS.
+template <int T> WM_DEV void xop_part_fetch_lds(const lf32_t* src, int seg, int part, float (&v)[8]) {
+    const lf32_t* p = src + seg_col(T, seg, 8 * part);
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = p[i];
 }
 
 // An operand record from LDS into registers.

@@ -185,7 +185,8 @@ class MoELayer:
     def __init__(self, H: int, I: int, E: int, K: int, router: Optional[torch.Tensor], gate_exps: torch.Tensor,
                  up_exps: torch.Tensor, down_exps: torch.Tensor, types: Sequence[int],
                  shared: Optional[SharedExpert] = None, max_tokens: int = 256, strides=(0, 0, 0),
-                 multi_kernel: bool = False, timeline: bool = False):
+                 multi_kernel: bool = False, timeline: bool = False, norm_w: Optional[torch.Tensor] = None,
+                 norm_eps: float = 1e-6, add_residual: bool = False):
         self.H, self.I, self.E, self.K = H, I, E, K
         self.types = tuple(types)
         self.max_tokens = max_tokens
@@ -209,6 +210,12 @@ class MoELayer:
             d.inter_shared = shared.inter
             if shared.gate_inp is not None:
                 d.sh_gate_inp = _p(_need(shared.gate_inp, torch.float32, "shared.gate_inp"))
+        # the step either side: decode(h) normalises h itself (attention.h:29-44)
+        # and, with add_residual, returns h + moe_out (winmoe_inference.c:2041)
+        self.norm_w = None if norm_w is None else _need(norm_w, torch.float32, "norm_w")
+        d.norm_w = _p(self.norm_w)
+        d.norm_eps = norm_eps
+        d.add_residual = 1 if add_residual else 0
         self.desc = d
         L = load()
         nbytes = L.wm_workspace_size(C.byref(d), max_tokens)
