@@ -1,12 +1,25 @@
 """Benchmark of the MoE expert-layer hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--config c2] [--gpus 1] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--config c2] [--gpus 1]
+                    [--no-cpu-baseline] [--only]
 
-A step is one decode token through the layer (router -> top-K -> K experts ->
-combine + shared expert), inputs resident in HBM, no host synchronisation
-inside the timed region.  Prints ONE JSON line.  Default workload: 512
-experts, top-10 + shared expert, hidden 4096, intermediate 1024, Q8_0, batch-1
-decode over 256 distinct hidden states (cycled).
+Prints ONE JSON line.  The headline (default) is batch-1 decode of the
+512-expert, top-10 + shared expert, hidden 4096, intermediate 1024 Q8_0 layer
+over 256 distinct hidden states (cycled): a step is one decode token through
+the layer (router -> top-K -> K experts -> combine + shared expert), inputs
+resident in HBM, no host synchronisation inside the timed region.  The line's
+``configs`` object measures the other workloads the same way, each with its
+own roofline and CPU baseline:
+
+  c1  64 experts, top-4, hidden 2048, intermediate 512, Q8_0, 1 token
+  c3  512 experts, top-3, Q4_K gate/up, Q6_K down, Q8_0 shared expert, decode
+  c4  8 consecutive 512-expert top-3 Q2_K/Q3_K layers chained through the
+      fused RMSNorm and residual add, forced Zipf(0.456) routing with 37.5 %
+      overlap, 512 decode tokens (a step = one token through all 8 layers)
+  c5  prefill of 512 bf16 tokens through the 512-expert top-10 Q8_0 layer,
+      Zipf routing (a step = the whole batch)
+
+``--only`` measures the chosen --config alone (used under the profiler).
 """
 from __future__ import annotations
 
@@ -15,6 +28,7 @@ import ctypes as C
 import json
 import os
 import platform
+import statistics
 import subprocess
 import sys
 import time
@@ -26,6 +40,8 @@ sys.path.insert(0, ROOT)
 
 METRIC = "MoE layer tokens/s at batch 1 and 512; achieved HBM GB/s vs peak"
 PEAK_HBM_GBPS = 8000.0
+CPU_REPS = 5                 # timed repetitions of the CPU baseline (median reported), after one warm-up
+CPU_REP_TARGET_S = 0.6       # wall time one repetition aims at
 
 
 def log(msg):
@@ -33,32 +49,42 @@ def log(msg):
 
 
 def host_info():
-    model = ""
+    model, tpc = "", 1
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
         for line in out.splitlines():
             if line.startswith("Model name"):
                 model = line.split(":", 1)[1].strip()
-    except OSError:
+            if line.startswith("Thread(s) per core"):
+                tpc = int(line.split(":", 1)[1].strip() or 1)
+    except (OSError, ValueError):
         pass
-    return {"cpu_model": model or platform.processor(), "nproc": os.cpu_count(),
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = os.cpu_count() or 1
+    return {"cpu_model": model or platform.processor(), "nproc": os.cpu_count(), "cpus_allowed": allowed,
+            "threads_per_core": tpc, "physical_cores_allowed": max(1, allowed // max(tpc, 1)),
             "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
 
 
-def step_bytes(cfg) -> int:
-    """Algorithmic bytes of one decode step: every expert weight byte touched
-    (K routed + shared), router, shared gate vector, activation in/out."""
+# ------------------------------------------------------------------ algorithmic bytes (rooflines)
+
+def decode_layer_bytes(cfg) -> int:
+    """One decode token through one layer: every expert weight byte touched (K
+    routed + shared), the router when it routes, the shared gate vector, x in
+    and out."""
     b = cfg.K * cfg.expert_bytes() + cfg.shared_bytes() + 2 * cfg.H * 4
     if cfg.routing == "router":
         b += cfg.E * cfg.H * 4
     if cfg.shared_gate_inp:
         b += cfg.H * 4
-    return b * cfg.n_layers
+    return b
 
 
 def prefill_bytes(cfg, ids) -> int:
-    """Algorithmic bytes of one prefill batch: every expert touched once,
-    the shared expert, x (bf16) in, out (fp32) out, the router when it routes."""
+    """One prefill batch: every expert touched once, the shared expert, x (bf16)
+    in, out (fp32) out, the router when it routes."""
     uniq = len(np.unique(ids[(ids >= 0) & (ids < cfg.E)]))
     b = uniq * cfg.expert_bytes() + cfg.shared_bytes() + cfg.tokens * cfg.H * (2 + 4)
     if cfg.routing == "router":
@@ -67,8 +93,8 @@ def prefill_bytes(cfg, ids) -> int:
 
 
 def prefill_gateup_bytes(cfg, ids) -> int:
-    """Algorithmic bytes of the prefill gate/up launch: gate and up of every
-    expert touched (and the shared one), x rows read once, SwiGLU rows written."""
+    """The prefill gate/up launch: gate and up of every expert touched, x rows
+    read once, SwiGLU rows written."""
     from winmoe_amd.moe import matrix_bytes
     gt, ut, _ = cfg.types
     uniq = len(np.unique(ids[(ids >= 0) & (ids < cfg.E)]))
@@ -77,22 +103,10 @@ def prefill_gateup_bytes(cfg, ids) -> int:
     return b
 
 
-def gateup_bytes(cfg) -> int:
-    """Algorithmic bytes of one launch of the gate/up + SwiGLU kernel (weights + act out)."""
-    from winmoe_amd.moe import matrix_bytes
-    gt, ut, _ = cfg.types
-    per = matrix_bytes(gt, cfg.I, cfg.H) + matrix_bytes(ut, cfg.I, cfg.H) + cfg.I * 4
-    n = cfg.K
-    if cfg.shared_types and tuple(cfg.shared_types) == tuple(cfg.types) and (cfg.shared_inter or cfg.I) == cfg.I:
-        n += 1
-    return n * per
-
-
-def measured_traffic(cfg):
-    """HBM bytes per launch of the fused kernel from the committed rocprofv3
-    PMC summary for this workload (FETCH_SIZE + WRITE_SIZE, scaled by the copy
-    kernel calibration), or None when there is none."""
-    path = os.path.join(ROOT, "profiles", f"k_decode_persist_{cfg.name}_traffic.json")
+def committed_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` on `workload` from the committed
+    rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, calibrated), or None."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_traffic.json")
     try:
         with open(path) as f:
             return json.load(f).get("traffic_bytes_per_launch")
@@ -100,148 +114,121 @@ def measured_traffic(cfg):
         return None
 
 
-def cpu_baseline(layers, X, routes, budget_s: float):
-    """Reference CPU path (oracle/_ref, compiled from the reference sources) on
-    the same layer, weights copied to host RAM; falls back to the oracle port."""
-    from oracle import oracle
-    R = oracle.ref()
-    kind = "reference" if R is not None else "port"
-    host_layers = []
-    for sl in layers:
-        cfg = sl.cfg
-        sh = sl.shared
-        L = oracle.make_layer(cfg.H, cfg.I, sl.layer.E, cfg.K, cfg.types,
-                              router=None if sl.router is None else sl.router.cpu().numpy(),
-                              gate=sl.gate.cpu().numpy(), up=sl.up.cpu().numpy(), down=sl.down.cpu().numpy(),
-                              shared=None if sh is None else (sh.gate.cpu().numpy(), sh.up.cpu().numpy(),
-                                                              sh.down.cpu().numpy()),
-                              sh_types=None if sh is None else sh.types,
-                              sh_gate_inp=None if (sh is None or sh.gate_inp is None) else sh.gate_inp.cpu().numpy(),
-                              I_shared=0 if sh is None else sh.inter)
-        host_layers.append(L)
-    Xh = X.float().cpu().numpy()
-    fn = oracle.ref_moe_layer_cpu if R is not None else oracle.moe_layer
-    n = 0
-    used_port = False
-    t0 = time.perf_counter()
-    while True:
-        t = n % Xh.shape[0]
-        for li, L in enumerate(host_layers):
-            fi = fw = None
-            if routes is not None:
-                fi, fw = routes[li][0][t], routes[li][1][t]
-            res = fn(L, Xh[t], fi, fw)
-            if R is not None and res[3] == 1:
-                used_port = True
-        n += 1
-        el = time.perf_counter() - t0
-        if (el >= budget_s and n >= 2) or n >= 4096:
-            break
-    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1) if R is not None else 1
-    if used_port:
-        kind = "port"
-    return {"value": n / el, "unit": "tokens/s", "cores": threads, "kind": kind,
-            "sample": f"{n} decode tokens of the same layer(s) ({el:.1f} s), weights resident in host RAM, "
-                      f"{'reference kernels compiled from the reference sources' if kind == 'reference' else 'oracle port'}",
-            "host": host_info()}
+def roofline(kernel_desc, kernel, workload, per_launch, launch_us):
+    ach = per_launch / (launch_us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+            "frac": round(ach / PEAK_HBM_GBPS, 4), "traffic": committed_traffic(kernel, workload),
+            "kernel": kernel_desc, "bytes_per_launch": per_launch, "avg_launch_us": round(launch_us, 2)}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2048)
-    ap.add_argument("--warmup", type=int, default=64)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=15.0)
-    ap.add_argument("--multi-kernel", action="store_true",
-                    help="run each step as per-phase kernel launches instead of the single fused launch")
-    ap.add_argument("--copy-calibration-mib", type=int, default=0,
-                    help="first run 4 plain device copies of this many MiB (reference kernel of known traffic "
-                         "for rocprofv3 FETCH_SIZE / WRITE_SIZE calibration)")
-    args = ap.parse_args()
+# ------------------------------------------------------------------ workloads on the GPU
 
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
-        sys.exit(2)
+class Workload:
+    """A synthetic workload resident in HBM and its step function."""
 
-    import torch
-    import winmoe_amd as wm
-    from winmoe_amd import synth
-
-    if not torch.cuda.is_available():
-        print("bench.py needs a HIP device", file=sys.stderr)
-        sys.exit(1)
-    L = wm.load()
-    cfg = synth.CONFIGS[args.config]
-    log(f"building {cfg.name} on {torch.cuda.get_device_name(0)}")
-    t_build = time.perf_counter()
-    layers = [synth.build_layer(cfg, layer_index=i, max_tokens=cfg.tokens, multi_kernel=args.multi_kernel)
-              for i in range(cfg.n_layers)]
-    X = synth.make_hidden(cfg)
-    routes = None
-    if cfg.routing != "router":
-        routes = []
+    def __init__(self, name, multi_kernel=False):
+        import torch
+        from winmoe_amd import synth
+        from winmoe_amd.moe import MoELayer
+        self.cfg = cfg = synth.CONFIGS[name]
+        self.prefill = cfg.x_dtype == "bf16" and cfg.tokens > 1
+        self.chained = cfg.n_layers > 1
+        self.layers, self.norms = [], []
+        g = torch.Generator(device="cuda").manual_seed(2024)
         for i in range(cfg.n_layers):
-            ids, w = synth.forced_routes(cfg, layer_index=i)
-            routes.append((ids, w, torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda()))
-    outs = torch.empty(cfg.tokens, cfg.H, dtype=torch.float32, device="cuda")
-    torch.cuda.synchronize()
-    log(f"built in {time.perf_counter() - t_build:.1f} s")
+            sl = synth.build_layer(cfg, layer_index=i, max_tokens=cfg.tokens, multi_kernel=multi_kernel)
+            if self.chained:
+                # h_{l+1} = h_l + moe_l(rmsnorm(h_l)) (winmoe_inference.c:1659-1668,2041): the norm and the
+                # residual add run inside each layer's decode step
+                c = sl.cfg
+                nw = (1.0 + 0.1 * torch.randn(c.H, generator=g, device="cuda")).float()
+                sl.layer = MoELayer(c.H, c.I, sl.layer.E, c.K, sl.router, sl.gate, sl.up, sl.down, c.types,
+                                    shared=sl.shared, max_tokens=cfg.tokens, norm_w=nw, add_residual=True)
+                self.norms.append(nw)
+            self.layers.append(sl)
+        self.X = synth.make_hidden(cfg)
+        self.routes = None
+        if cfg.routing != "router":
+            self.routes = []
+            for i in range(cfg.n_layers):
+                ids, w = synth.forced_routes(cfg, layer_index=i)
+                self.routes.append((ids, w, torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda()))
+        # decode outputs [T][H]; a chained stack keeps every layer's stream [L+1][T][H]
+        if self.chained:
+            self.hs = torch.empty(cfg.n_layers + 1, cfg.tokens, cfg.H, device="cuda")
+            self.hs[0] = self.X
+        self.outs = torch.empty(cfg.tokens, cfg.H, dtype=torch.float32, device="cuda")
 
-    prefill = cfg.x_dtype == "bf16" and cfg.tokens > 1     # one step = the whole batch through the layer
-
-    def step(i):
-        if prefill:
-            for li, sl in enumerate(layers):
-                if routes is None:
-                    sl.layer.prefill(X, out=outs)
+    def step(self, i):
+        cfg = self.cfg
+        if self.prefill:
+            for li, sl in enumerate(self.layers):
+                if self.routes is None:
+                    sl.layer.prefill(self.X, out=self.outs)
                 else:
-                    sl.layer.prefill_forced(X, routes[li][2], routes[li][3], out=outs)
+                    sl.layer.prefill_forced(self.X, self.routes[li][2], self.routes[li][3], out=self.outs)
             return
         t = i % cfg.tokens
-        x = X[t]
-        for li, sl in enumerate(layers):
-            o = outs[t]
-            if routes is None:
+        for li, sl in enumerate(self.layers):
+            if self.chained:
+                x, o = self.hs[li, t], self.hs[li + 1, t]
+            else:
+                x, o = self.X[t], self.outs[t]
+            if self.routes is None:
                 sl.layer.decode(x, out=o, step=i)
             else:
-                sl.layer.decode_forced(x, routes[li][2][t], routes[li][3][t], out=o, step=i)
+                sl.layer.decode_forced(x, self.routes[li][2][t], self.routes[li][3][t], out=o, step=i)
 
-    if args.copy_calibration_mib > 0:
-        n = args.copy_calibration_mib << 18              # floats
-        src = torch.ones(n, dtype=torch.float32, device="cuda")
-        dst = torch.empty_like(src)
-        for _ in range(4):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
-        log(f"ran 4 device copies of {args.copy_calibration_mib} MiB")
+    def status(self):
+        return max(sl.layer.prefill_status() if self.prefill else sl.layer.check() for sl in self.layers)
 
-    for i in range(args.warmup):
-        step(i)
+    def tokens_per_step(self):
+        return self.cfg.tokens if self.prefill else 1
+
+    def step_bytes(self):
+        if self.prefill:
+            return prefill_bytes(self.cfg, self.routes[0][0]) * self.cfg.n_layers
+        return decode_layer_bytes(self.cfg) * self.cfg.n_layers
+
+
+def measure(wl, L, steps, warmup, graph):
+    """Warm-up, then `steps` steps issued one by one from Python and timed with
+    HIP events on the launch stream; with `graph`, the same `steps` steps are
+    also captured into one HIP graph and one replay is timed the same way
+    (the GPU's own rate, without the host's per-call launch cost); then a
+    profiled pass (per-launch events recorded by the library)."""
+    import torch
+    for i in range(warmup):
+        wl.step(i)
     torch.cuda.synchronize()
-
-    # ---- timed region: K steps back to back, inputs resident, no profiling
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     start.record()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(args.warmup + i)
+    for i in range(steps):
+        wl.step(warmup + i)
     stop.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ev_ms = start.elapsed_time(stop)
-
-    # ---- roofline pass: per-launch duration of the dominant kernel from HIP
-    # events recorded by the library around each launch, on its stream
-    n_prof = min(args.steps, 256)
+    graph_ms = None
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(steps):
+                wl.step(warmup + steps + i)
+        g.replay()                                      # warm replay
+        torch.cuda.synchronize()
+        start.record()
+        g.replay()
+        stop.record()
+        torch.cuda.synchronize()
+        graph_ms = start.elapsed_time(stop)
+        del g
+    n_prof = min(steps, 256)
     L.wm_profile_read(None, None, 0)
     L.wm_profile_enable(1)
     for i in range(n_prof):
-        step(args.warmup + args.steps + i)
+        wl.step(warmup + steps + i)
     torch.cuda.synchronize()
     L.wm_profile_enable(0)
     ms_arr = (C.c_double * 8)()
@@ -252,65 +239,235 @@ def main():
         if cnt_arr[p]:
             phases[L.wm_profile_phase_name(p).decode()] = {"avg_us": round(1000.0 * ms_arr[p] / cnt_arr[p], 3),
                                                            "launches": int(cnt_arr[p])}
-    st = max(sl.layer.prefill_status() if prefill else sl.layer.status() for sl in layers)
-    ms_per_step = ev_ms / args.steps
-    tokens_per_s = args.steps * (cfg.tokens if prefill else 1) / (ev_ms / 1000.0)
-    sbytes = prefill_bytes(cfg, routes[0][0]) * cfg.n_layers if prefill else step_bytes(cfg)
+    return ev_ms, graph_ms, wall, phases
+
+
+def entry(wl, L, steps, warmup, multi_kernel=False):
+    """Measured record of one workload (without its CPU baseline).  Decode
+    steps are timed as a replayed HIP graph of the steps (the launch cost of
+    one Python call per layer per token would otherwise be measured instead
+    of the GPU at the small workloads); the eager figure is kept beside it."""
+    cfg = wl.cfg
+    use_graph = not wl.prefill and not multi_kernel
+    ev_ms, graph_ms, wall, phases = measure(wl, L, steps, warmup, use_graph)
+    eager_ms_per_step = ev_ms / steps
+    if graph_ms is not None:
+        ev_ms = graph_ms
+    ms_per_step = ev_ms / steps
+    tokens_per_s = steps * wl.tokens_per_step() / (ev_ms / 1000.0)
+    sbytes = wl.step_bytes()
     step_gbps = sbytes / (ms_per_step * 1e-3) / 1e9
-    roofline = None
-    if prefill and "gate_up_swiglu" in phases:
+    rl = None
+    if wl.prefill and "gate_up_swiglu" in phases:
         gu = phases["gate_up_swiglu"]
-        per_launch = prefill_gateup_bytes(cfg, routes[0][0])
-        ach = per_launch / (gu["avg_us"] * 1e-6) / 1e9
-        roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                    "frac": round(ach / PEAK_HBM_GBPS, 4), "traffic": None,
-                    "kernel": "k_pf_gemm<2,1,1> (prefill gate+up+SwiGLU: fp16 MFMA over Q8_0 blocks, LDS-DMA ring)",
-                    "bytes_per_launch": per_launch, "avg_launch_us": round(gu["avg_us"], 2)}
-    elif prefill:
-        pass
-    elif not args.multi_kernel:
-        # one fused launch per layer per token moves the whole step's bytes;
-        # its average duration is the timed region's event time over the
-        # launches in it (they run back to back on this stream)
-        launch_us = 1000.0 * ev_ms / (args.steps * cfg.n_layers)
-        per_launch = sbytes // cfg.n_layers
-        ach = per_launch / (launch_us * 1e-6) / 1e9
-        roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                    "frac": round(ach / PEAK_HBM_GBPS, 4), "traffic": measured_traffic(cfg),
-                    "kernel": "k_decode_persist (fused decode step: one persistent workgroup per CU, "
-                              "1 launch per layer per token)",
-                    "bytes_per_launch": per_launch, "avg_launch_us": round(launch_us, 2)}
-    elif "gate_up_swiglu" in phases:
-        gu = phases["gate_up_swiglu"]
-        per_launch = gateup_bytes(cfg)
-        ach = per_launch / (gu["avg_us"] * 1e-6) / 1e9
-        roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                    "frac": round(ach / PEAK_HBM_GBPS, 4), "traffic": None,
-                    "kernel": "k_gateup (gate+up+SwiGLU)", "bytes_per_launch": per_launch,
-                    "avg_launch_us": round(gu["avg_us"], 2)}
-    result = {
-        "metric": METRIC, "value": round(tokens_per_s, 1), "unit": "tokens/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": ("fp16 MFMA (int8 weights exact in fp16, x fp16 per-token scaled, SwiGLU output fp16 hi+lo) -> fp32"
-                  if prefill else "int8 dot (quantised weights x int8 activation digits) -> int32, fp32 scales/accumulation"),
-        "data": "synthetic (seeded N(0,0.02) weights quantised on device, N(0,1) hidden states)",
-        "config": {"workload": cfg.name, "experts": cfg.E, "top_k": cfg.K, "hidden": cfg.H, "inter": cfg.I,
-                   "types": [wm.TYPE_NAMES[t] for t in cfg.types],
-                   "shared_types": [wm.TYPE_NAMES[t] for t in cfg.shared_types] if cfg.shared_types else None,
-                   "layers": cfg.n_layers, "routing": cfg.routing, "batch": cfg.tokens if prefill else 1,
-                   "distinct_tokens": cfg.tokens,
-                   "path": "prefill" if prefill else ("multi-kernel" if args.multi_kernel else "fused")},
-        "roofline": roofline,
-        "step_algorithmic_bytes": sbytes, "step_GBps": round(step_gbps, 1),
-        "step_hbm_frac": round(step_gbps / PEAK_HBM_GBPS, 4),
-        "wall_s_timed": round(wall, 4), "phases_us": phases, "status": st,
+        rl = roofline("k_pf_gemm<2,1,1> (prefill gate+up+SwiGLU: fp16 MFMA over Q8_0 blocks, LDS-DMA ring)",
+                      "k_pf_gemm", cfg.name, prefill_gateup_bytes(cfg, wl.routes[0][0]), gu["avg_us"])
+    elif not wl.prefill and not multi_kernel:
+        # one fused launch per layer per token moves the step's bytes; its
+        # average duration is the timed region's event time over the launches
+        # in it (back to back on this stream)
+        launch_us = 1000.0 * ev_ms / (steps * cfg.n_layers)
+        rl = roofline("k_decode_persist (fused decode step: one persistent workgroup per CU, "
+                      "1 launch per layer per token)", "k_decode_persist", cfg.name,
+                      sbytes // cfg.n_layers, launch_us)
+    return {
+        "workload": cfg.name, "ms_per_step": round(ms_per_step, 5), "tokens_per_s": round(tokens_per_s, 1),
+        "timing": "one replay of a HIP graph of the steps" if graph_ms is not None else "steps issued from Python",
+        "eager_ms_per_step": round(eager_ms_per_step, 5),
+        "tokens_per_step": wl.tokens_per_step(), "layers": cfg.n_layers, "steps": steps, "warmup": warmup,
+        "roofline": rl, "step_algorithmic_bytes": sbytes, "step_GBps": round(step_gbps, 1),
+        "step_hbm_frac": round(step_gbps / PEAK_HBM_GBPS, 4), "wall_s_timed": round(wall, 4),
+        "phases_us": phases, "status": wl.status(),
     }
-    if not args.no_cpu_baseline:
-        log("timing the reference CPU path on this host")
-        result["cpu_baseline"] = cpu_baseline(layers, X, routes, args.cpu_budget)
-    else:
-        result["cpu_baseline"] = None
+
+
+# ------------------------------------------------------------------ CPU baseline
+
+def _host_layer(oracle, sl, experts):
+    """The layer in host RAM for the CPU path: router, shared expert and the
+    given experts copied from HBM into full-size stacked arrays whose other
+    experts are never touched (their pages are never committed)."""
+    from winmoe_amd.moe import matrix_bytes
+    cfg = sl.cfg
+    E, H, I = sl.layer.E, cfg.H, cfg.I
+    gt, ut, dt = cfg.types
+    per = (matrix_bytes(gt, I, H), matrix_bytes(ut, I, H), matrix_bytes(dt, H, I))
+    stacks = [np.zeros(E * p, np.uint8) for p in per]
+    for e in experts:
+        for arr, src, p in zip(stacks, (sl.gate, sl.up, sl.down), per):
+            arr[e * p:(e + 1) * p] = src[e * p:(e + 1) * p].cpu().numpy()
+    sh = sl.shared
+    return oracle.make_layer(H, I, E, cfg.K, cfg.types,
+                             router=None if sl.router is None else sl.router.cpu().numpy(),
+                             gate=stacks[0], up=stacks[1], down=stacks[2],
+                             shared=None if sh is None else (sh.gate.cpu().numpy(), sh.up.cpu().numpy(),
+                                                             sh.down.cpu().numpy()),
+                             sh_types=None if sh is None else sh.types,
+                             sh_gate_inp=None if (sh is None or sh.gate_inp is None) else sh.gate_inp.cpu().numpy(),
+                             I_shared=0 if sh is None else sh.inter)
+
+
+def cpu_baseline(wl, n_sample):
+    """The reference CPU path (oracle/_ref: the reference's own kernels compiled
+    from its sources; the oracle port for types the reference has no CPU
+    kernel for) on the first n_sample tokens of the workload, on this host.
+    One warm-up token, then CPU_REPS timed repetitions over the sample; the
+    median repetition gives tokens/s.  Prefill runs the decode path token by
+    token, as the reference does for a prompt (winmoe_inference.c:1079,
+    2286-2288)."""
+    from oracle import oracle
+    R = oracle.ref()
+    cfg = wl.cfg
+    n_sample = min(n_sample, cfg.tokens)
+    Xh = wl.X.float().cpu().numpy()
+    host = []
+    for li, sl in enumerate(wl.layers):
+        if wl.routes is not None:
+            experts = np.unique(wl.routes[li][0][:n_sample])
+        else:
+            ids, _ = sl.layer.trace()
+            experts = np.unique(ids[:n_sample].cpu().numpy())
+        host.append(_host_layer(oracle, sl, experts.tolist()))
+    norms = [n.cpu().numpy() for n in wl.norms]
+    fn = oracle.ref_moe_layer_cpu if R is not None else oracle.moe_layer
+    used_port = R is None
+
+    def one_token(t):
+        nonlocal used_port
+        h = Xh[t]
+        for li, L in enumerate(host):
+            fi = fw = None
+            if wl.routes is not None:
+                fi, fw = wl.routes[li][0][t], wl.routes[li][1][t]
+            x = h
+            if wl.chained:
+                x = oracle.ref_rmsnorm(h, norms[li])
+            res = fn(L, x, fi, fw)
+            if R is not None and res[3] == 1:
+                used_port = True
+            if wl.chained:
+                h = (h + np.asarray(res[2], np.float32)).astype(np.float32)
+
+    t0 = time.perf_counter()
+    one_token(0)                                                   # warm-up
+    per_tok = max(time.perf_counter() - t0, 1e-4)
+    n_rep = int(max(1, min(n_sample, round(CPU_REP_TARGET_S / per_tok))))
+    reps = []
+    for r in range(CPU_REPS):
+        t0 = time.perf_counter()
+        for i in range(n_rep):
+            one_token((r * n_rep + i) % n_sample)
+        reps.append(time.perf_counter() - t0)
+    med = statistics.median(reps)
+    info = host_info()
+    threads = int(os.environ.get("OMP_NUM_THREADS") or info["cpus_allowed"]) if R is not None else 1
+    kind = "port" if used_port else "reference"
+    what = ("the reference's kernels compiled from its sources" if kind == "reference" else
+            "the oracle port (the reference has no CPU kernel for these types)" if R is not None else
+            "the oracle port (reference build absent)")
+    sample = (f"{n_rep} decode tokens per repetition ({'through all ' + str(cfg.n_layers) + ' layers, ' if wl.chained else ''}"
+              f"{n_sample} distinct), 1 warm-up token, median of {CPU_REPS} repetitions "
+              f"({', '.join(f'{x:.3f}' for x in reps)} s); weights resident in host RAM; {what}")
+    if wl.prefill:
+        sample += f"; a prefill batch of {cfg.tokens} tokens is {cfg.tokens} decode tokens (no batched CPU path)"
+    return {"value": round(n_rep / med, 2), "unit": "tokens/s", "cores": threads, "kind": kind, "sample": sample,
+            "host": info}
+
+
+# ------------------------------------------------------------------ main
+
+EXTRA = ["c1", "c3", "c4", "c5"]
+CPU_SAMPLE = {"c1": 1, "c2": 16, "c3": 16, "c4": 4, "c5": 8}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2048)
+    ap.add_argument("--warmup", type=int, default=64)
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--only", action="store_true", help="measure --config alone (no `configs` object)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--multi-kernel", action="store_true",
+                    help="run each decode step as per-phase kernel launches instead of the single fused launch")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="first run 4 plain device copies and 4 read-only reductions of this many MiB (kernels of "
+                         "known traffic for the rocprofv3 FETCH_SIZE / WRITE_SIZE calibration)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import winmoe_amd as wm
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    L = wm.load()
+
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib << 18              # floats
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        acc = torch.zeros((), device="cuda")
+        for _ in range(4):
+            acc += src.sum()                             # reads n floats, writes a few bytes
+        torch.cuda.synchronize()
+        del src, dst, acc
+        log(f"ran 4 device copies and 4 reductions of {args.copy_calibration_mib} MiB")
+
+    def run(name, steps, warmup, headline):
+        log(f"building {name} on {torch.cuda.get_device_name(0)}")
+        t_build = time.perf_counter()
+        wl = Workload(name, multi_kernel=args.multi_kernel and headline)
+        torch.cuda.synchronize()
+        log(f"built in {time.perf_counter() - t_build:.1f} s")
+        e = entry(wl, L, steps, warmup, multi_kernel=args.multi_kernel and headline)
+        if not args.no_cpu_baseline:
+            log(f"timing the reference CPU path on this host ({name})")
+            e["cpu_baseline"] = cpu_baseline(wl, CPU_SAMPLE[name])
+        else:
+            e["cpu_baseline"] = None
+        cfg = wl.cfg
+        e["config"] = {"workload": cfg.name, "experts": cfg.E, "top_k": cfg.K, "hidden": cfg.H, "inter": cfg.I,
+                       "types": [wm.TYPE_NAMES[t] for t in cfg.types],
+                       "shared_types": [wm.TYPE_NAMES[t] for t in cfg.shared_types] if cfg.shared_types else None,
+                       "layers": cfg.n_layers, "routing": cfg.routing,
+                       "batch": cfg.tokens if wl.prefill else 1, "distinct_tokens": cfg.tokens,
+                       "path": "prefill" if wl.prefill else ("multi-kernel" if args.multi_kernel and headline
+                                                             else "fused")}
+        e["dtype"] = ("fp16 MFMA (int8 weights exact in fp16, x fp16 per-token scaled, SwiGLU output fp16 hi+lo) "
+                      "-> fp32" if wl.prefill else
+                      "int8 dot (quantised weights x int8 activation digits) -> int32, fp32 scales/accumulation")
+        del wl
+        torch.cuda.empty_cache()
+        return e
+
+    head = run(args.config, args.steps, args.warmup, True)
+    configs = None
+    if not args.only:
+        configs = {}
+        for name in EXTRA:
+            if name == args.config:
+                continue
+            configs[name] = run(name, args.steps, args.warmup, False)
+    result = {
+        "metric": METRIC, "value": head["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": head["dtype"],
+        "data": "synthetic (seeded N(0,0.02) weights quantised on device, N(0,1) hidden states)",
+        "config": head["config"], "roofline": head["roofline"], "cpu_baseline": head["cpu_baseline"],
+        "timing": head["timing"], "eager_ms_per_step": head["eager_ms_per_step"],
+        "step_algorithmic_bytes": head["step_algorithmic_bytes"], "step_GBps": head["step_GBps"],
+        "step_hbm_frac": head["step_hbm_frac"], "wall_s_timed": head["wall_s_timed"],
+        "phases_us": head["phases_us"], "status": head["status"],
+        "configs": configs,
+    }
     print(json.dumps(result), flush=True)
 
 

@@ -19,9 +19,18 @@
  * argument (unsupported type, misaligned pointer, shape outside the supported
  * set, undersized workspace).
  *
- * Threading: a workspace serves one stream at a time; distinct workspaces on
- * distinct streams may run concurrently.  The gpu_* shims keep global state
- * and are single-threaded like the reference.
+ * Threading: a workspace serves one stream at a time.  Calls on distinct
+ * workspaces may come from several host threads and streams; the library
+ * orders them where it must: the persistent decode kernel needs every CU at
+ * once, so persistent launches never overlap.  On one stream, stream order
+ * does it.  The first persistent launch on a second stream of a device waits
+ * once for the device to drain (a host wait); after that every persistent
+ * launch records an event and a launch on another stream than the last waits
+ * for it on the device (no host wait).  Work of other libraries on other
+ * streams only delays a step.  Under stream capture no ordering is added: do
+ * not replay a captured decode step concurrently with other decode steps.
+ * The gpu_* shims keep global state and are single-threaded like the
+ * reference.
  */
 #ifndef WINMOE_HIP_H
 #define WINMOE_HIP_H
@@ -68,6 +77,13 @@ enum {
  * stated explicitly. */
 #define WM_FLAG_ITEM_KERNEL 4
 #define WM_FLAG_PERSIST_KERNEL 8
+/* wm_layer_desc.flags, test hook of the persistent kernel: every wait of the
+ * step (on another workgroup's data or inside the workgroup) gives up at its
+ * first unsuccessful poll instead of after ~0.1 s.  The step then ends at
+ * once with WM_STATUS_SPIN_TIMEOUT set and invalid results;
+ * wm_workspace_reset makes the workspace usable again.  Lets a test drive the
+ * timeout path without anything waiting long. */
+#define WM_FLAG_SPIN_PROBE 16
 
 /* One MoE layer.  Expert tensors are the raw GGUF blocks, stacked by expert:
  * gate/up expert e = [inter rows][hidden/QK blocks] at gate_exps + e*gate_stride,

@@ -132,6 +132,19 @@ def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float = 1e-6) -> np.ndarray:
     return out
 
 
+def ref_rmsnorm(x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """The reference's rmsnorm (attention.h:29-44, eps 1e-6) compiled from its
+    sources; the oracle's restatement when that build is absent."""
+    R = ref()
+    if R is None:
+        return rmsnorm(x, w)
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    R.wmref_rmsnorm(_ptr(out, _fp), _ptr(x, _fp), _ptr(w, _fp), x.shape[0])
+    return out
+
+
 def router_logits(x: np.ndarray, W: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, np.float32)
     W = np.ascontiguousarray(W, np.float32)

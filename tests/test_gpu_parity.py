@@ -413,8 +413,9 @@ def test_prefill_rejects_unsupported_widths(wm):
     cfg = _pf_cfg(E=8, K=2, H=384, I=256)
     sl = synth.build_layer(cfg, max_tokens=4)
     X = synth.make_hidden(cfg, tokens=4)
-    with pytest.raises(Exception):
+    with pytest.raises(wm.WinMoEError) as ei:
         sl.layer.prefill(X)
+    assert ei.value.rc == wm._lib.WM_EINVAL
 
 
 def test_prefill_forced_multi_pass_and_bad_ids(wm, orc):
@@ -469,7 +470,7 @@ def test_prefill_c5_full(wm, orc):
 # ------------------------------------------------------------------ GGUF boundary
 
 @pytest.mark.parametrize("name", ["c1", "c3"])
-def test_layer_from_gguf_matches_direct(wm, tmp_path, name):
+def test_layer_from_gguf_matches_direct(wm, orc, tmp_path, name):
     """A layer written as a GGUF file (stacked [H, I, E] / [I, H, E] expert
     tensors, F32 router [H, E], shared expert) and mapped back with
     moe_layer_from_gguf decodes bit for bit like the same tensors handed over
@@ -509,18 +510,107 @@ def test_layer_from_gguf_matches_direct(wm, tmp_path, name):
             ids, w = dev(routes[0][t]), dev(routes[1][t])
             a, b = host(L.decode_forced(X[t], ids, w)), host(sl.layer.decode_forced(X[t], ids, w))
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), t
+        if t == 0:
+            # and against the oracle, on the bytes as read back from the file
+            case(f"gguf {name} oracle token=0")
+            xh = host(X[0])
+            raw = {n[len("blk.3."):]: np.asarray(g.data(n)) for n, *_ in tensors}
+            shared = None
+            if sl.shared is not None:
+                shared = (raw["ffn_gate_shexp.weight"], raw["ffn_up_shexp.weight"], raw["ffn_down_shexp.weight"])
+            OL = orc.make_layer(H, I, E, cfg.K, cfg.types,
+                                router=None if sl.router is None else
+                                raw["ffn_gate_inp.weight"].view(np.float32).reshape(E, H),
+                                gate=raw["ffn_gate_exps.weight"], up=raw["ffn_up_exps.weight"],
+                                down=raw["ffn_down_exps.weight"], shared=shared,
+                                sh_types=None if sl.shared is None else sl.shared.types,
+                                sh_gate_inp=None if sl.shared is None or sl.shared.gate_inp is None else
+                                raw["ffn_gate_inp_shexp.weight"].view(np.float32),
+                                I_shared=0 if sl.shared is None else sl.shared.inter)
+            fi = fw = None
+            if routes is not None:
+                fi, fw = routes[0][0], routes[1][0]
+            oid, _, ref, _ = orc.moe_layer(OL, xh, fi, fw)
+            if routes is None:
+                assert host(L.trace()[0][0]).tolist() == oid.tolist()
+            assert rel_l2(a, ref) <= LAYER_TOL, rel_l2(a, ref)
     assert L.status() == 0
+
+
+@pytest.mark.parametrize("rtype", [1, Q8_0])
+def test_gguf_router_f16_and_quantised(wm, orc, tmp_path, rtype):
+    """A router stored as F16 or Q8_0 in the GGUF file is widened / dequantised
+    exactly to fp32 at load; the layer then routes like the oracle on those
+    fp32 weights."""
+    import torch
+    from winmoe_amd import gguf, synth
+    cfg = synth.CONFIGS["c1"]
+    E = 32
+    sl = synth.build_layer(cfg, E=E, max_tokens=4)
+    H, I = cfg.H, cfg.I
+    W = host(sl.router)
+    if rtype == 1:
+        rbytes = W.astype(np.float16).tobytes()
+        W32 = W.astype(np.float16).astype(np.float32)
+    else:
+        q = wm.quantize(sl.router.reshape(-1).contiguous(), Q8_0)
+        rbytes = host(q).tobytes()
+        W32 = orc.dequant(Q8_0, host(q)).reshape(E, H)
+    gt, ut, dt = cfg.types
+    tensors = [("blk.0.ffn_gate_exps.weight", (H, I, E), gt, host(sl.gate).tobytes()),
+               ("blk.0.ffn_up_exps.weight", (H, I, E), ut, host(sl.up).tobytes()),
+               ("blk.0.ffn_down_exps.weight", (I, H, E), dt, host(sl.down).tobytes()),
+               ("blk.0.ffn_gate_inp.weight", (H, E), rtype, rbytes)]
+    p = str(tmp_path / "router.gguf")
+    gguf.write_gguf(p, {"general.architecture": "winmoe", "winmoe.expert_used_count": cfg.K}, tensors)
+    L = gguf.moe_layer_from_gguf(gguf.GGUFFile(p), 0, max_tokens=4)
+    assert np.array_equal(host(L.router).view(np.uint32), W32.view(np.uint32))
+    X = synth.make_hidden(cfg, tokens=2)
+    for t in range(2):
+        case(f"gguf router type={rtype} token={t}")
+        L.decode(X[t], step=t)
+        oid, ow, _ = orc.router_topk(host(X[t]), W32, cfg.K)
+        assert host(L.trace()[0][t]).tolist() == oid.tolist()
+    del torch
 
 
 # ------------------------------------------------------------------ RMSNorm in, residual out
 
-@pytest.mark.parametrize("name,E", [("c1", 64), ("c2", 40), ("c4", 24)])
-def test_fused_rmsnorm_and_residual(wm, orc, name, E):
-    """decode(h) with norm_w and add_residual == h + decode(rmsnorm(h)), the
-    RMSNorm by the oracle (pinned to the reference's rmsnorm), bit for bit,
-    with the same routing trace.  The kernel sums the squares in a different
-    order than the reference (index order), which could move the last bits of
-    ss; (float)(ss / H) is the same on these seeds."""
+def kernel_order_scale(h, H, eps=1e-6):
+    """The RMSNorm scale as the persistent kernel forms it: lane l of 64 sums
+    (double)h[i]^2 for i = l, l + 64, ... in order, then an xor butterfly over
+    the lanes (32, 16, ..., 1); scale = 1 / sqrtf((float)(ss / H) + eps)."""
+    v = np.asarray(h, np.float32).astype(np.float64)
+    lanes = np.zeros(64)
+    for l in range(64):
+        acc = 0.0
+        for x in v[l::64]:
+            acc += x * x
+        lanes[l] = acc
+    for m in (32, 16, 8, 4, 2, 1):
+        lanes = lanes + lanes[np.arange(64) ^ m]
+    return np.float32(1.0) / np.sqrt(np.float32(lanes[0] / H) + np.float32(eps), dtype=np.float32)
+
+
+def reference_order_scale(h, H, eps=1e-6):
+    """attention.h:31-33: ss in index order, scale = 1 / sqrtf((float)(ss/dim) + 1e-6f)."""
+    ss = 0.0
+    for x in np.asarray(h, np.float32).astype(np.float64):
+        ss += x * x
+    return np.float32(1.0) / np.sqrt(np.float32(ss / H) + np.float32(eps), dtype=np.float32)
+
+
+@pytest.mark.parametrize("name,E,residual", [("c1", 64, True), ("c2", 40, True), ("c4", 24, True), ("c3", 24, True),
+                                             ("c2", 512, True), ("c1", 1000, True), ("c2", 40, False)])
+def test_fused_rmsnorm_and_residual(wm, orc, name, E, residual):
+    """decode(h) with norm_w (and add_residual) == [h +] decode(rmsnorm(h)),
+    the RMSNorm by the oracle (pinned to the reference's rmsnorm), bit for
+    bit, with the same routing trace.  E=512 and E=1000 put two and four
+    router rows on a workgroup of the persistent kernel (rows read the
+    normalised x from LDS); c3 has a shared expert of another type (its x
+    operand records are built separately).  The kernel adds the squares in a
+    different order than the reference; the bit-for-bit bar holds when both
+    orders give the same scale, which the test checks first."""
     import torch
     from winmoe_amd import synth
     from winmoe_amd.moe import MoELayer
@@ -530,14 +620,18 @@ def test_fused_rmsnorm_and_residual(wm, orc, name, E):
     g = torch.Generator(device="cuda").manual_seed(11)
     w = (1.0 + 0.1 * torch.randn(c.H, generator=g, device="cuda")).float()
     normed = MoELayer(c.H, c.I, E, c.K, sl.router, sl.gate, sl.up, sl.down, c.types, shared=sl.shared, max_tokens=8,
-                      norm_w=w, add_residual=True)
+                      norm_w=w, add_residual=residual)
     plain = synth.twin_layer(sl, multi_kernel=False)
     Hs = 3.0 * torch.randn(4, c.H, generator=g, device="cuda")
     routes = synth.forced_routes(cfg, E=E, tokens=4) if cfg.routing != "router" else None
     for t in range(4):
         case(f"rmsnorm {name} E={E} token={t}")
         h = Hs[t].contiguous()
-        x = orc.rmsnorm(host(h), host(w))
+        hh = host(h)
+        ks, rs = kernel_order_scale(hh, c.H), reference_order_scale(hh, c.H)
+        assert ks.view(np.uint32) == rs.view(np.uint32), \
+            f"token {t}: the kernel's and the reference's sum orders give different scales ({ks!r} vs {rs!r})"
+        x = orc.rmsnorm(hh, host(w))
         if routes is None:
             a = host(normed.decode(h))
             b = host(plain.decode(dev(x)))
@@ -545,7 +639,8 @@ def test_fused_rmsnorm_and_residual(wm, orc, name, E):
             ids, wt = dev(routes[0][t]), dev(routes[1][t])
             a = host(normed.decode_forced(h, ids, wt))
             b = host(plain.decode_forced(dev(x), ids, wt))
-        assert np.array_equal(a.view(np.uint32), (host(h) + b).view(np.uint32)), t
+        want = hh + b if residual else b
+        assert np.array_equal(a.view(np.uint32), want.view(np.uint32)), t
     ta, _ = normed.trace()
     tb, _ = plain.trace()
     assert np.array_equal(host(ta[:4]), host(tb[:4]))
@@ -565,8 +660,13 @@ def test_rmsnorm_rejected_off_the_persistent_path(wm):
     for flags in (_lib.FLAG_MULTI_KERNEL, _lib.FLAG_ITEM_KERNEL):
         L = MoELayer(c.H, c.I, c.E, c.K, sl.router, sl.gate, sl.up, sl.down, c.types, max_tokens=4, norm_w=w)
         L.desc.flags |= flags
-        with pytest.raises(Exception):
+        with pytest.raises(wm.WinMoEError) as ei:
             L.decode(torch.randn(c.H, device="cuda"))
+        assert ei.value.rc == _lib.WM_EINVAL
     L = MoELayer(c.H, c.I, c.E, c.K, sl.router, sl.gate, sl.up, sl.down, c.types, max_tokens=4, add_residual=True)
-    with pytest.raises(Exception):
+    with pytest.raises(wm.WinMoEError) as ei:
         L.decode(torch.randn(c.H, device="cuda"))
+    assert ei.value.rc == _lib.WM_EINVAL
+    with pytest.raises(wm.WinMoEError) as ei:
+        L.prefill(torch.randn(4, c.H, device="cuda").to(torch.bfloat16))
+    assert ei.value.rc == _lib.WM_EINVAL

@@ -28,6 +28,7 @@ FLAG_MULTI_KERNEL = 1
 FLAG_TIMELINE = 2
 FLAG_ITEM_KERNEL = 4
 FLAG_PERSIST_KERNEL = 8
+FLAG_SPIN_PROBE = 16
 
 _vp, _i64 = C.c_void_p, C.c_int64
 
@@ -105,7 +106,12 @@ _lib = None
 
 
 class WinMoEError(RuntimeError):
-    pass
+    """A library call failed; ``rc`` is its return code (WM_ERR or WM_EINVAL,
+    None when the library itself could not be loaded)."""
+
+    def __init__(self, msg: str, rc=None):
+        super().__init__(msg)
+        self.rc = rc
 
 
 def load():
@@ -128,4 +134,4 @@ def check(rc: int, what: str = "") -> None:
     if rc == WM_OK:
         return
     kind = "invalid argument" if rc == WM_EINVAL else "HIP runtime error"
-    raise WinMoEError(f"{what or 'winmoe_hip'} failed: {kind} (rc={rc})")
+    raise WinMoEError(f"{what or 'winmoe_hip'} failed: {kind} (rc={rc})", rc)

@@ -8,33 +8,18 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 #include "../../include/winmoe_hip.h"
 #include "wm_decode.h"
+#include "wm_host.h"
 #include "wm_launch.h"
 #include "wm_prefill.h"
 #include "wm_quant.h"
 #include "wm_wave.h"
 
 using namespace wm;
-
-#define WM_FAIL_HIP(expr)                                                                                  \
-    do {                                                                                                   \
-        hipError_t e_ = (hipError_t)(expr);                                                                \
-        if (e_ != hipSuccess) {                                                                            \
-            fprintf(stderr, "winmoe_hip: HIP error at %s:%d: %s\n", __FILE__, __LINE__, hipGetErrorString(e_)); \
-            return WM_ERR;                                                                                 \
-        }                                                                                                  \
-    } while (0)
-
-#define WM_CHECK_ARG(cond)                                                                \
-    do {                                                                                  \
-        if (!(cond)) {                                                                    \
-            fprintf(stderr, "winmoe_hip: invalid argument (%s) in %s\n", #cond, __func__); \
-            return WM_EINVAL;                                                             \
-        }                                                                                 \
-    } while (0)
 
 static inline hipStream_t S(void* s) { return (hipStream_t)s; }
 static inline bool al(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
@@ -459,6 +444,53 @@ static int max_lds_per_wg() {
     return cached[dev];
 }
 
+// Persistent launches on different streams must not overlap: each needs one
+// workgroup on every CU at once, and two sharing the CUs would each wait for
+// workgroups that cannot start.  Per device, the stream of the last
+// persistent launch.  While every launch comes on one stream, stream order
+// is enough and nothing is added.  The first launch on a second stream waits
+// for the device to drain once (no other stream's handle is touched: it may
+// be gone); from then on an event is recorded after every persistent launch
+// and a launch on another stream than the last waits for it on the device.
+struct PersistOrder {
+    hipStream_t last = nullptr;
+    bool used = false, multi = false, recorded = false;
+    hipEvent_t ev = nullptr;
+};
+static std::mutex g_persist_mu;
+static PersistOrder g_persist_order[64];
+
+static bool capturing(hipStream_t s) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone;
+}
+
+// Launches `launch` on s after the last persistent launch of another stream.
+template <typename F> static int persistent_ordered(hipStream_t s, F&& launch) {
+    int dev = 0;
+    WM_FAIL_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64 || capturing(s)) return launch();
+    std::lock_guard<std::mutex> lock(g_persist_mu);
+    PersistOrder& po = g_persist_order[dev];
+    if (po.used && po.last != s) {
+        if (!po.multi) {
+            WM_FAIL_HIP(hipEventCreateWithFlags(&po.ev, hipEventDisableTiming));
+            WM_FAIL_HIP(hipDeviceSynchronize());
+            po.multi = true;
+        } else if (po.recorded) {
+            WM_FAIL_HIP(hipStreamWaitEvent(s, po.ev, 0));
+        }
+    }
+    if (int rc = launch()) return rc;
+    if (po.multi) {
+        WM_FAIL_HIP(hipEventRecord(po.ev, s));
+        po.recorded = true;
+    }
+    po.last = s;
+    po.used = true;
+    return WM_OK;
+}
+
 // One launch of the persistent step kernel (wm_persist.hip); returns 1 when
 // the layer does not fit it (the caller then uses the work-item-list kernel).
 static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, const float* x, float* out,
@@ -532,9 +564,12 @@ static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
     a.epoch = (uint32_t*)(ws + L.pctr);
     a.tact = (uint64_t*)(ws + L.tact);
     if (d->flags & WM_FLAG_TIMELINE) a.timeline = (uint64_t*)(ws + L.timeline);
+    a.probe = (d->flags & WM_FLAG_SPIN_PROBE) ? 1u : 0u;
     PhaseTimer pt(PH_STEP, s);
-    WM_FAIL_HIP(launch_persist(a, (size_t)lds, gut, dt, sgut, sdt, s));
-    return WM_OK;
+    return persistent_ordered(s, [&]() -> int {
+        WM_FAIL_HIP(launch_persist(a, (size_t)lds, gut, dt, sgut, sdt, s));
+        return WM_OK;
+    });
 }
 
 // One launch of the fused step kernel; returns 1 when the type combination has
@@ -849,302 +884,4 @@ extern "C" int wm_moe_prefill_forced(const wm_layer_desc* d, const uint16_t* x_b
                                      void* stream) {
     WM_CHECK_ARG(ids && w);
     return run_prefill(d, x_bf16, T, ids, w, out, ws, ws_bytes, max_tokens, stream);
-}
-
-// ------------------------------------------------------------------ gpu_offload.h shims
-
-namespace {
-
-struct Slot {
-    int layer = -1, eid = -1;
-    void* d[3] = {nullptr, nullptr, nullptr};   // gate, up, down
-    int size[3] = {0, 0, 0};
-    int type[3] = {-1, -1, -1};                 // -1 = infer from size
-};
-
-constexpr int kLookupLayers = 80, kLookupExperts = 1024, kMaxSlots = 16384;
-
-struct Legacy {
-    bool init = false;
-    hipStream_t stream = nullptr;
-    std::vector<Slot> slots;
-    std::vector<int> lookup;
-    int limit = 300;
-    int evict = 0;
-    double used_bytes = 0.0;
-    double ceiling_bytes = 0.0;
-    void* ws = nullptr;           // expert workspace
-    int64_t ws_bytes = 0;
-    float* dio = nullptr;         // device in/out staging
-    int64_t dio_floats = 0;
-    float* moe_acc = nullptr;     // batch API accumulator
-    int moe_h = 0;
-    float* router[64] = {nullptr};
-    int router_dims[64][2] = {{0}};
-};
-Legacy G;
-
-int ensure_ws(int H, int I) {
-    int64_t need = wm_expert_workspace_size(H, I);
-    // staging for input, output and gate/up copies; sized once for any shape
-    // up to 16384 so the batch API's uploaded input is never reallocated away
-    int64_t fl = 4 * (int64_t)std::max(std::max(H, I), 16384) + 1024;
-    if (need > G.ws_bytes) {
-        if (G.ws) (void)hipFree(G.ws);
-        G.ws = nullptr;
-        G.ws_bytes = 0;
-        WM_FAIL_HIP(hipMalloc(&G.ws, need));
-        G.ws_bytes = need;
-    }
-    if (fl > G.dio_floats) {
-        if (G.dio) (void)hipFree(G.dio);
-        G.dio = nullptr;
-        G.dio_floats = 0;
-        WM_FAIL_HIP(hipMalloc((void**)&G.dio, fl * sizeof(float)));
-        G.dio_floats = fl;
-    }
-    return WM_OK;
-}
-
-// Quant type of a cached matrix: recorded, or inferred from its byte size
-// (bytes per weight differ for every supported type).
-int slot_type(const Slot& sl, int k, int rows, int in) {
-    if (sl.type[k] >= 0) return sl.type[k];
-    const int cand[6] = {Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K};
-    for (int t : cand)
-        if (in % block_elems(t) == 0 && matrix_bytes(t, rows, in) == (int64_t)sl.size[k]) return t;
-    return -1;
-}
-
-}  // namespace
-
-extern "C" int gpu_init(void) {
-    if (G.init) return 0;
-    if (wm_init()) return -1;
-    WM_FAIL_HIP(hipStreamCreateWithFlags(&G.stream, hipStreamNonBlocking));
-    size_t free_b = 0, total_b = 0;
-    WM_FAIL_HIP(hipMemGetInfo(&free_b, &total_b));
-    G.ceiling_bytes = 0.9 * (double)total_b;
-    G.lookup.assign((size_t)kLookupLayers * kLookupExperts, -1);
-    G.slots.clear();
-    G.init = true;
-    return 0;
-}
-
-extern "C" void gpu_shutdown(void) {
-    if (!G.init) return;
-    (void)hipStreamSynchronize(G.stream);
-    for (Slot& sl : G.slots)
-        for (int k = 0; k < 3; k++)
-            if (sl.d[k]) (void)hipFree(sl.d[k]);
-    for (int l = 0; l < 64; l++)
-        if (G.router[l]) { (void)hipFree(G.router[l]); G.router[l] = nullptr; }
-    if (G.ws) (void)hipFree(G.ws);
-    if (G.dio) (void)hipFree(G.dio);
-    if (G.moe_acc) (void)hipFree(G.moe_acc);
-    (void)hipStreamDestroy(G.stream);
-    G = Legacy();
-}
-
-extern "C" int gpu_is_initialized(void) { return G.init ? 1 : 0; }
-extern "C" float gpu_vram_used_mb(void) { return (float)(G.used_bytes / (1024.0 * 1024.0)); }
-extern "C" int gpu_expert_cache_count(void) { return (int)G.slots.size(); }
-
-extern "C" void gpu_set_expert_limit(int limit) {
-    if (limit < 1) limit = 1;
-    if (limit > kMaxSlots) limit = kMaxSlots;
-    G.limit = limit;
-    fprintf(stderr, "GPU expert cache: limit set to %d (MAX_GPU_EXPERTS=%d)\n", G.limit, kMaxSlots);
-}
-
-extern "C" int gpu_upload_router(int layer, const float* weights, int hidden_dim, int num_experts) {
-    if (!G.init && gpu_init()) return -1;
-    if (layer < 0 || layer >= 64 || !weights || hidden_dim <= 0 || num_experts <= 0) return -1;
-    size_t bytes = (size_t)hidden_dim * num_experts * sizeof(float);
-    if (G.router[layer]) { (void)hipFree(G.router[layer]); G.used_bytes -= (double)G.router_dims[layer][0] * G.router_dims[layer][1] * 4; }
-    G.router[layer] = nullptr;
-    if (hipMalloc((void**)&G.router[layer], bytes) != hipSuccess) return -1;
-    if (hipMemcpy(G.router[layer], weights, bytes, hipMemcpyHostToDevice) != hipSuccess) return -1;
-    G.router_dims[layer][0] = hidden_dim;
-    G.router_dims[layer][1] = num_experts;
-    G.used_bytes += (double)bytes;
-    return 0;
-}
-
-extern "C" int gpu_router(int layer, const float* normed, int hidden_dim, float* logits_out, int num_experts) {
-    if (!G.init || layer < 0 || layer >= 64 || !G.router[layer]) return -1;
-    if (G.router_dims[layer][0] != hidden_dim || G.router_dims[layer][1] != num_experts) return -1;
-    if (router_rows_per_wg(hidden_dim, false) <= 0) return -1;
-    if (ensure_ws(hidden_dim, std::max(num_experts, 64))) return -1;
-    float* dx = G.dio;
-    float* dl = G.dio + ((hidden_dim + 255) & ~255);
-    WM_FAIL_HIP(hipMemcpyAsync(dx, normed, hidden_dim * sizeof(float), hipMemcpyHostToDevice, G.stream));
-    WM_FAIL_HIP(launch_router_logits(dx, G.router[layer], hidden_dim, num_experts, dl, G.stream));
-    WM_FAIL_HIP(hipMemcpyAsync(logits_out, dl, num_experts * sizeof(float), hipMemcpyDeviceToHost, G.stream));
-    WM_FAIL_HIP(hipStreamSynchronize(G.stream));
-    return 0;
-}
-
-static int cache_expert(int layer, int expert_id, const void* data[3], const int size[3], const int type[3]) {
-    if (!G.init && gpu_init()) return -1;
-    if (layer < 0 || expert_id < 0 || layer >= kLookupLayers || expert_id >= kLookupExperts) return -1;
-    for (int k = 0; k < 3; k++)
-        if (!data[k] || size[k] <= 0) return -1;
-    double nb = (double)size[0] + size[1] + size[2];
-    if (G.used_bytes + nb > G.ceiling_bytes) {
-        static int warned = 0;
-        if (!warned) {
-            fprintf(stderr, "GPU VRAM ceiling hit (%.0f MB used + %.0f MB new > %.0f MB)\n", G.used_bytes / 1048576.0,
-                    nb / 1048576.0, G.ceiling_bytes / 1048576.0);
-            warned = 1;
-        }
-        return -1;
-    }
-    int idx;
-    if ((int)G.slots.size() < G.limit) {
-        idx = (int)G.slots.size();
-        G.slots.emplace_back();
-    } else {
-        idx = G.evict;
-        G.evict = (G.evict + 1) % G.limit;
-        Slot& old = G.slots[idx];
-        if (old.layer >= 0) G.lookup[(size_t)old.layer * kLookupExperts + old.eid] = -1;
-        WM_FAIL_HIP(hipStreamSynchronize(G.stream));
-        for (int k = 0; k < 3; k++) {
-            if (old.d[k]) (void)hipFree(old.d[k]);
-            G.used_bytes -= old.size[k];
-            old.d[k] = nullptr;
-        }
-        old = Slot();
-    }
-    Slot& sl = G.slots[idx];
-    for (int k = 0; k < 3; k++) {
-        WM_FAIL_HIP(hipMalloc(&sl.d[k], (size_t)size[k]));
-        WM_FAIL_HIP(hipMemcpyAsync(sl.d[k], data[k], (size_t)size[k], hipMemcpyHostToDevice, G.stream));
-        sl.size[k] = size[k];
-        sl.type[k] = type[k];
-    }
-    WM_FAIL_HIP(hipStreamSynchronize(G.stream));
-    sl.layer = layer;
-    sl.eid = expert_id;
-    G.lookup[(size_t)layer * kLookupExperts + expert_id] = idx;
-    G.used_bytes += nb;
-    return idx;
-}
-
-extern "C" int gpu_cache_expert(int layer, int expert_id, const void* gate_data, int gate_size, const void* up_data,
-                                int up_size, const void* down_data, int down_size) {
-    const void* d[3] = {gate_data, up_data, down_data};
-    int sz[3] = {gate_size, up_size, down_size}, ty[3] = {-1, -1, -1};
-    return cache_expert(layer, expert_id, d, sz, ty);
-}
-
-extern "C" int gpu_cache_expert_typed(int layer, int expert_id, const void* gate_data, int gate_size, int gate_type,
-                                      const void* up_data, int up_size, int up_type, const void* down_data,
-                                      int down_size, int down_type) {
-    if (!supported(gate_type) || !supported(up_type) || !supported(down_type)) return -1;
-    const void* d[3] = {gate_data, up_data, down_data};
-    int sz[3] = {gate_size, up_size, down_size}, ty[3] = {gate_type, up_type, down_type};
-    return cache_expert(layer, expert_id, d, sz, ty);
-}
-
-extern "C" int gpu_find_cached_expert(int layer, int expert_id) {
-    if (!G.init || layer < 0 || expert_id < 0 || layer >= kLookupLayers || expert_id >= kLookupExperts) return -1;
-    return G.lookup[(size_t)layer * kLookupExperts + expert_id];
-}
-
-static const Slot* get_slot(int idx) {
-    if (!G.init || idx < 0 || idx >= (int)G.slots.size() || !G.slots[idx].d[0]) return nullptr;
-    return &G.slots[idx];
-}
-
-// Runs the expert of `sl` on device input G.dio (H floats) into dout (H floats).
-static int expert_on_device(const Slot& sl, int H, int I, float* dout) {
-    int gt = slot_type(sl, 0, I, H), ut = slot_type(sl, 1, I, H), dt = slot_type(sl, 2, H, I);
-    if (gt < 0 || ut < 0 || dt < 0) {
-        fprintf(stderr, "winmoe_hip: cached expert sizes do not match hidden %d / intermediate %d\n", H, I);
-        return -1;
-    }
-    int rc = wm_expert_ffn(sl.d[0], gt, sl.d[1], ut, sl.d[2], dt, G.dio, H, I, dout, G.ws, G.ws_bytes, G.stream);
-    return rc == WM_OK ? 0 : -1;
-}
-
-extern "C" int gpu_expert_ffn_fused(int cache_idx, const float* input, int hidden_dim, int intermediate,
-                                    float* expert_out) {
-    const Slot* sl = get_slot(cache_idx);
-    if (!sl || !input || !expert_out) return -1;
-    if (ensure_ws(hidden_dim, intermediate)) return -1;
-    float* dout = G.dio + ((std::max(hidden_dim, intermediate) + 255) & ~255);
-    WM_FAIL_HIP(hipMemcpyAsync(G.dio, input, hidden_dim * sizeof(float), hipMemcpyHostToDevice, G.stream));
-    if (expert_on_device(*sl, hidden_dim, intermediate, dout)) return -1;
-    WM_FAIL_HIP(hipMemcpyAsync(expert_out, dout, hidden_dim * sizeof(float), hipMemcpyDeviceToHost, G.stream));
-    WM_FAIL_HIP(hipStreamSynchronize(G.stream));
-    return 0;
-}
-
-extern "C" int gpu_expert_ffn(int cache_idx, const float* input, int hidden_dim, int intermediate, float* gate_out,
-                              float* up_out, float* expert_out, int gate_type, int down_type) {
-    (void)expert_out; (void)gate_type; (void)down_type;   // as gpu_offload.cu:675-698: types come from the slot
-    const Slot* sl = get_slot(cache_idx);
-    if (!sl || !input || !gate_out || !up_out) return -1;
-    int H = hidden_dim, I = intermediate;
-    int gt = slot_type(*sl, 0, I, H), ut = slot_type(*sl, 1, I, H);
-    if (gt < 0 || ut < 0) return -1;
-    if (ensure_ws(H, I)) return -1;
-    float* dg = G.dio + ((std::max(H, I) + 255) & ~255);
-    float* du = dg + ((I + 255) & ~255);
-    if ((int64_t)(du - G.dio) + I > G.dio_floats) return -1;
-    WM_FAIL_HIP(hipMemcpyAsync(G.dio, input, H * sizeof(float), hipMemcpyHostToDevice, G.stream));
-    if (wm_quant_matvec(gt, sl->d[0], G.dio, I, H, dg, G.ws, G.ws_bytes, G.stream)) return -1;
-    if (wm_quant_matvec(ut, sl->d[1], G.dio, I, H, du, G.ws, G.ws_bytes, G.stream)) return -1;
-    WM_FAIL_HIP(hipMemcpyAsync(gate_out, dg, I * sizeof(float), hipMemcpyDeviceToHost, G.stream));
-    WM_FAIL_HIP(hipMemcpyAsync(up_out, du, I * sizeof(float), hipMemcpyDeviceToHost, G.stream));
-    WM_FAIL_HIP(hipStreamSynchronize(G.stream));
-    return 0;
-}
-
-extern "C" int gpu_expert_down(int cache_idx, const float* act, int intermediate, float* output, int hidden_dim) {
-    const Slot* sl = get_slot(cache_idx);
-    if (!sl || !act || !output) return -1;
-    int H = hidden_dim, I = intermediate;
-    int dt = slot_type(*sl, 2, H, I);
-    if (dt < 0) return -1;
-    if (ensure_ws(H, I)) return -1;
-    float* dout = G.dio + ((std::max(H, I) + 255) & ~255);
-    WM_FAIL_HIP(hipMemcpyAsync(G.dio, act, I * sizeof(float), hipMemcpyHostToDevice, G.stream));
-    if (wm_quant_matvec(dt, sl->d[2], G.dio, H, I, dout, G.ws, G.ws_bytes, G.stream)) return -1;
-    WM_FAIL_HIP(hipMemcpyAsync(output, dout, H * sizeof(float), hipMemcpyDeviceToHost, G.stream));
-    WM_FAIL_HIP(hipStreamSynchronize(G.stream));
-    return 0;
-}
-
-extern "C" int gpu_expert_batch_start(const float* normed, int hidden_dim) {
-    if (!G.init || !normed || hidden_dim <= 0) return -1;
-    if (ensure_ws(hidden_dim, 64)) return -1;
-    if (G.moe_h < hidden_dim) {
-        if (G.moe_acc) (void)hipFree(G.moe_acc);
-        G.moe_acc = nullptr;
-        WM_FAIL_HIP(hipMalloc((void**)&G.moe_acc, hidden_dim * sizeof(float)));
-        G.moe_h = hidden_dim;
-    }
-    WM_FAIL_HIP(hipMemcpyAsync(G.dio, normed, hidden_dim * sizeof(float), hipMemcpyHostToDevice, G.stream));
-    WM_FAIL_HIP(launch_fill_i32((int32_t*)G.moe_acc, 0, hidden_dim, G.stream));
-    return 0;
-}
-
-extern "C" int gpu_expert_batch_add(int cache_idx, int hidden_dim, int intermediate, float weight) {
-    const Slot* sl = get_slot(cache_idx);
-    if (!sl || !G.moe_acc || hidden_dim > G.moe_h) return -1;
-    if (ensure_ws(hidden_dim, intermediate)) return -1;   // never reallocates dio once sized for hidden_dim
-    float* dout = G.dio + ((std::max(hidden_dim, intermediate) + 255) & ~255);
-    if (expert_on_device(*sl, hidden_dim, intermediate, dout)) return -1;
-    WM_FAIL_HIP(launch_axpy(G.moe_acc, dout, weight, hidden_dim, G.stream));
-    return 0;
-}
-
-extern "C" int gpu_expert_batch_finish(float* moe_out, int hidden_dim) {
-    if (!G.init || !G.moe_acc || !moe_out || hidden_dim > G.moe_h) return -1;
-    WM_FAIL_HIP(hipMemcpyAsync(moe_out, G.moe_acc, hidden_dim * sizeof(float), hipMemcpyDeviceToHost, G.stream));
-    WM_FAIL_HIP(hipStreamSynchronize(G.stream));
-    return 0;
 }

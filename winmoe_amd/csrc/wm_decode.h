@@ -84,6 +84,7 @@ constexpr int P_TL = 32;                 // timeline words per workgroup
 constexpr int P_MAX_WG = 1024;           // workgroups (CUs) the workspace has start-tag words for
 constexpr int P_REP = 8;                 // replicas of the tagged logits (each read by 1/8 of the workgroups)
 constexpr int P_AREP = 4;                // replicas of the tagged SwiGLU outputs
+constexpr uint32_t PSPIN_G = 1u << 17;   // device-memory polls (~1 us each) before a wait gives up
 
 // Ring buffer bytes of one tile of type T: NI DMA units of 1 KB, except Q8_0
 // whose 5th unit is cut to the 4352-byte tile + 16 B of alignment shift (the
@@ -152,6 +153,7 @@ struct PersistArgs {
     uint32_t* epoch;                   // launches completed since the workspace was reset
     uint64_t* tact;                    // [K+1][P_AREP][I] (tag << 32) | SwiGLU output bits
     uint64_t* timeline;                // NULL or [nwg][P_TL]
+    uint32_t probe;                    // nonzero: every wait of the step gives up at its first unsuccessful poll
 };
 
 bool persist_supported(int gut, int dt, int sgut, int sdt);

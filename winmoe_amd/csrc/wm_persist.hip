@@ -54,7 +54,6 @@ static_assert(PSTAGE >= 2, "the second staging wave loads x for the router");
 typedef __attribute__((address_space(3))) PersistCtl lctl_t;
 
 constexpr uint32_t PSPIN = 1u << 20;    // LDS polls (~0.2 us each after the first few) before a wait gives up
-constexpr uint32_t PSPIN_G = 1u << 17;  // device-memory polls (~1 us each) before a wait gives up
 
 #define WM_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xC07F)
 
@@ -641,7 +640,7 @@ WM_DEV void route_tagged(const PersistArgs& a, lctl_t* ctl, int rep, uint32_t ta
     // picks come in descending order, and a degenerate pick's value
     // (logits[0], itself invalid or already picked) never compares greater
     const float wmax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_v), 0));
-    const float ex = mine ? expf(my_v - wmax) : 0.0f;
+    const float ex = mine ? exp_rn(my_v - wmax) : 0.0f;
     float wsum = 0.0f;
     for (int k = 0; k < K; k++) wsum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), k));
     wk = wsum > 0.0f ? ex / wsum : ex;
@@ -959,6 +958,8 @@ __global__ __launch_bounds__(PTHREADS) void k_decode_persist(PersistArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     for (int i = threadIdx.x; i < (int)(sizeof(PersistCtl) / 4); i += PTHREADS)
         ((lds32_t*)(lds8_t*)smem)[i] = i < PW ? (uint32_t)i : 0u;     // progress[w] = w: wave w's first entry
+    // the timeout test hook: every wait gives up at its first unsuccessful poll
+    if (threadIdx.x == 0 && a.probe) ((PersistCtl*)smem)->abort = 1u;
     __syncthreads();
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (wave < PW) stream_wave<GUT, DT, SGUT, SDT>(a, smem, wave, lane);

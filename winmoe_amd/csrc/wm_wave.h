@@ -60,6 +60,13 @@ WM_DEV void tile_store(lds8_t* lt, const TileLoad& tl, int lane) {
     }
 }
 
+// e^x rounded to fp32 from the fp64 exponential: the correctly rounded value
+// except when the fp64 result falls within an fp64 ulp of an fp32 rounding
+// midpoint.  The routing softmax uses it so that its weights match a CPU
+// expf of at most ~0.5 ulp error (the reference's, transformer.h:146) bit for
+// bit in all but such corner cases.
+WM_DEV float exp_rn(float x) { return (float)exp((double)x); }
+
 WM_DEV float silu_mul(float g, float u) {
     // g * sigmoid(g) * u with the branch-stable sigmoid of deltanet_impl.h:108-115
     float sg;
@@ -499,7 +506,7 @@ WM_DEV void wave_topk_n(const float* logits, int E, int K, int32_t* ids, float* 
         const float vk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_v), k));
         if (vk > wmax) wmax = vk;
     }
-    const float ex = mine ? expf(my_v - wmax) : 0.0f;
+    const float ex = mine ? exp_rn(my_v - wmax) : 0.0f;
     float wsum = 0.0f;
     for (int k = 0; k < K; k++) wsum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), k));
     const float wk = wsum > 0.0f ? ex / wsum : ex;
@@ -540,8 +547,8 @@ WM_DEV float pick_weight(const float* v, int K, int k) {
     float wmax = v[0];
     for (int i = 1; i < K; i++) if (v[i] > wmax) wmax = v[i];
     float wsum = 0.0f;
-    for (int i = 0; i < K; i++) wsum += expf(v[i] - wmax);
-    const float ex = expf(v[k] - wmax);
+    for (int i = 0; i < K; i++) wsum += exp_rn(v[i] - wmax);
+    const float ex = exp_rn(v[k] - wmax);
     return wsum > 0.0f ? ex / wsum : ex;
 }
 

@@ -307,6 +307,29 @@ def expert_slice(g: GGUFFile, name: str, e: int) -> np.ndarray:
     return g.data(name)[e * stride:(e + 1) * stride]
 
 
+def _router_fp32(g: "GGUFFile", name: str, t, E: int, H: int, device) -> torch.Tensor:
+    """The router as fp32 [E][H] on the device.  F32 is taken as is; F16 is
+    widened exactly; quantised routers (Q8_0, Q2_K .. Q6_K) are dequantised
+    exactly by the library.  The reference dispatches a quantised router
+    through quant_matvec (transformer.h:120-123), whose Q8_0 / K-quant paths
+    round the activations to int8 first, so its logits for such a router can
+    differ from the fp32 logits of the dequantised weights in the last bits."""
+    import torch
+
+    from . import _lib
+    raw = np.array(g.data(name), copy=True)
+    if t.ggml_type == 0:
+        w = torch.from_numpy(raw.view(np.float32)).to(device)
+    elif t.ggml_type == 1:
+        w = torch.from_numpy(raw.view(np.float16).astype(np.float32)).to(device)
+    elif t.ggml_type in _lib.QUANT_TYPES:
+        from .moe import dequantize
+        w = dequantize(torch.from_numpy(raw).to(device), t.ggml_type)
+    else:
+        raise GGUFError(f"router type {t.ggml_type} is not supported (F32, F16, Q8_0, Q2_K .. Q6_K are)")
+    return w.view(E, H).contiguous()
+
+
 def moe_layer_from_gguf(g: GGUFFile, layer: int, K: Optional[int] = None, device="cuda", max_tokens: int = 256,
                         multi_kernel: bool = False):
     """Map layer ``layer``'s MoE block into HBM once and return a MoELayer.
@@ -350,10 +373,9 @@ def moe_layer_from_gguf(g: GGUFFile, layer: int, K: Optional[int] = None, device
     router = None
     tr = g.find(pre + "ffn_gate_inp.weight")
     if tr is not None:
-        if tr.ggml_type != 0 or tr.dims != (H, E):
-            raise GGUFError(f"router must be F32 [{H}, {E}]")
-        router = torch.from_numpy(np.array(g.data(pre + "ffn_gate_inp.weight"), copy=True).view(np.float32)).to(
-            device).view(E, H)
+        if tr.dims != (H, E):
+            raise GGUFError(f"router must be [{H}, {E}], got {tr.dims}")
+        router = _router_fp32(g, pre + "ffn_gate_inp.weight", tr, E, H, device)
     shared = None
     if g.find(pre + "ffn_gate_shexp.weight") is not None:
         sg, su, sd = need("ffn_gate_shexp.weight"), need("ffn_up_shexp.weight"), need("ffn_down_shexp.weight")

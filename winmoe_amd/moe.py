@@ -213,6 +213,8 @@ class MoELayer:
         # the step either side: decode(h) normalises h itself (attention.h:29-44)
         # and, with add_residual, returns h + moe_out (winmoe_inference.c:2041)
         self.norm_w = None if norm_w is None else _need(norm_w, torch.float32, "norm_w")
+        if self.norm_w is not None and self.norm_w.numel() != H:
+            raise ValueError(f"norm_w must hold H = {H} values, got {self.norm_w.numel()}")
         d.norm_w = _p(self.norm_w)
         d.norm_eps = norm_eps
         d.add_residual = 1 if add_residual else 0
@@ -228,6 +230,16 @@ class MoELayer:
         check(L.wm_workspace_trace(C.byref(d), max_tokens, C.byref(io), C.byref(wo), C.byref(ho)), "trace")
         self._trace_off = (io.value, wo.value, ho.value)
 
+    def _need_vec(self, x: torch.Tensor, out: Optional[torch.Tensor]) -> None:
+        """x (and out, when given) must be fp32 vectors of H values on the device."""
+        _need(x, torch.float32, "x")
+        if x.numel() != self.H:
+            raise ValueError(f"x must hold H = {self.H} values, got {x.numel()}")
+        if out is not None:
+            _need(out, torch.float32, "out")
+            if out.numel() != self.H:
+                raise ValueError(f"out must hold H = {self.H} values, got {out.numel()}")
+
     def reset(self, stream=None) -> None:
         """Clear the routing trace, hit counters and status bits."""
         check(load().wm_workspace_reset(C.byref(self.desc), self.max_tokens, _p(self.ws), self.ws.numel(),
@@ -236,8 +248,13 @@ class MoELayer:
 
     def decode(self, x: torch.Tensor, out: Optional[torch.Tensor] = None, step: Optional[int] = None,
                stream=None) -> torch.Tensor:
-        """moe_out (before the residual add) of one token; routing recorded in the trace."""
-        _need(x, torch.float32, "x")
+        """One token through the layer; routing recorded in the trace.
+
+        Returns moe_out (the layer output before the residual add), or, when
+        the layer was built with ``add_residual=True``, ``h + moe_out`` where x
+        is the residual stream h.  With ``norm_w`` the layer normalises x
+        itself before routing (RMSNorm, attention.h:29-44)."""
+        self._need_vec(x, out)
         if out is None:
             out = torch.empty(self.H, dtype=torch.float32, device=x.device)
         st = self.step if step is None else step
@@ -248,10 +265,13 @@ class MoELayer:
 
     def decode_forced(self, x: torch.Tensor, ids: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None,
                       step: Optional[int] = None, stream=None) -> torch.Tensor:
-        """One token with caller-supplied routing (ids int32[K], w fp32[K] on device)."""
-        _need(x, torch.float32, "x")
+        """One token with caller-supplied routing (ids int32[K], w fp32[K] on
+        device); the output is as for ``decode``."""
+        self._need_vec(x, out)
         _need(ids, torch.int32, "ids")
         _need(w, torch.float32, "w")
+        if ids.numel() != self.K or w.numel() != self.K:
+            raise ValueError(f"ids and w must hold K = {self.K} values")
         if out is None:
             out = torch.empty(self.H, dtype=torch.float32, device=x.device)
         st = self.step if step is None else step
@@ -317,8 +337,12 @@ class MoELayer:
         return ids, w
 
     # -- trace ---------------------------------------------------------------
-    def trace(self):
-        """(ids int32 [max_tokens][K], weights fp32 [max_tokens][K]) views of the device trace."""
+    def trace(self, check: bool = True):
+        """(ids int32 [max_tokens][K], weights fp32 [max_tokens][K]) views of
+        the device trace.  With ``check`` (the default) the queued steps are
+        waited for and a step that gave up raises (see ``check()``)."""
+        if check:
+            self.check()
         io, wo, _ = self._trace_off
         n = self.max_tokens * self.K * 4
         ids = self.ws[io:io + n].view(torch.int32).view(self.max_tokens, self.K)
@@ -340,7 +364,19 @@ class MoELayer:
         n = cap.value * 8 * 8
         return self.ws[off.value:off.value + n].view(torch.int64).view(cap.value, 8)
 
+    def check(self) -> int:
+        """Waits for the layer's queued work and returns its status bits;
+        raises WinMoEError when a decode step gave up waiting
+        (WM_STATUS_SPIN_TIMEOUT: its outputs are invalid, ``reset()`` before
+        the next call).  The other bits describe the routing, not a failure."""
+        st = self.status()
+        if st & _lib.STATUS_SPIN_TIMEOUT:
+            raise _lib.WinMoEError("a decode step gave up waiting for another workgroup (WM_STATUS_SPIN_TIMEOUT): "
+                                   "its outputs are invalid; reset() the layer", _lib.WM_ERR)
+        return st
+
     def status(self) -> int:
+        """Status bits of the decode workspace (synchronises the host)."""
         v = C.c_int32()
         check(load().wm_workspace_status(_p(self.ws), self.ws.numel(), C.byref(v)), "wm_workspace_status")
         return v.value
