@@ -230,6 +230,29 @@ int wm_expert_ffn(const void* gate, int gate_type, const void* up, int up_type, 
                   void* stream);
 int64_t wm_expert_workspace_size(int H, int I);
 
+/* ------------------------------------------------- decode without allocation */
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid hipMalloc).
+ * wm_moe_decode_noalloc is wm_moe_decode (routing by the router, one token)
+ * with its workspace in a fixed device array the library holds on every
+ * device it runs on until the process ends (WM_NOALLOC_SCRATCH_BYTES), so it
+ * calls no hipMalloc / hipFree and creates nothing once wm_noalloc_init has
+ * run on the device (it runs on the first call otherwise); the phase profiler
+ * must be off.  x fp32[H] in, out fp32[H]; ids_out int32[K] / w_out fp32[K]
+ * (device, may be NULL) receive the routing.  A layer whose decode workspace
+ * (wm_workspace_size(d, 1)) exceeds the array returns WM_EINVAL.  Every call
+ * on a device shares that device's array: calls that overlap on one device
+ * (other streams, other threads) race and give wrong results.  Each call
+ * clears the part it uses with a kernel before the step. */
+#define WM_NOALLOC_SCRATCH_BYTES (4 * 1024 * 1024)
+int wm_noalloc_init(void);
+int64_t wm_noalloc_scratch_bytes(void);
+int wm_moe_decode_noalloc(const wm_layer_desc* d, const float* x, float* out, int32_t* ids_out, float* w_out,
+                          void* stream);
+/* Host-synchronous read of the status bits of the last no-allocation call on
+ * the current device. */
+int wm_noalloc_status(int32_t* status_out);
+
 /* ------------------------------------------------------------ profiling */
 /* Per-phase device timers of wm_moe_decode / wm_moe_decode_forced /
  * wm_moe_prefill, the counterpart of the reference's per-phase

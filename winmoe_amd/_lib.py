@@ -70,6 +70,10 @@ SIGNATURES = {
     "wm_moe_decode": (C.c_int, [C.POINTER(LayerDesc), _vp, _vp, _vp, _i64, C.c_int, C.c_int, _vp]),
     "wm_moe_decode_forced": (C.c_int, [C.POINTER(LayerDesc), _vp, _vp, _vp, _vp, _vp, _i64, C.c_int, C.c_int,
                                        _vp]),
+    "wm_noalloc_init": (C.c_int, []),
+    "wm_noalloc_scratch_bytes": (_i64, []),
+    "wm_moe_decode_noalloc": (C.c_int, [C.POINTER(LayerDesc), _vp, _vp, _vp, _vp, _vp]),
+    "wm_noalloc_status": (C.c_int, [C.POINTER(C.c_int32)]),
     "wm_prefill_workspace_size": (_i64, [C.POINTER(LayerDesc), C.c_int]),
     "wm_moe_prefill": (C.c_int, [C.POINTER(LayerDesc), _vp, C.c_int, _vp, _vp, _i64, C.c_int, _vp]),
     "wm_moe_prefill_forced": (C.c_int, [C.POINTER(LayerDesc), _vp, C.c_int, _vp, _vp, _vp, _vp, _i64, C.c_int,

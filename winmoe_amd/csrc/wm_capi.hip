@@ -465,6 +465,18 @@ static bool capturing(hipStream_t s) {
     return hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone;
 }
 
+// The current device's ordering event, created ahead of time so that no
+// later launch has to create it (wm_moe_decode_noalloc's set-up calls this).
+int wm::persist_order_prepare() {
+    int dev = 0;
+    WM_FAIL_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return WM_OK;
+    std::lock_guard<std::mutex> lock(g_persist_mu);
+    PersistOrder& po = g_persist_order[dev];
+    if (!po.ev) WM_FAIL_HIP(hipEventCreateWithFlags(&po.ev, hipEventDisableTiming));
+    return WM_OK;
+}
+
 // Launches `launch` on s after the last persistent launch of another stream.
 template <typename F> static int persistent_ordered(hipStream_t s, F&& launch) {
     int dev = 0;
@@ -474,7 +486,7 @@ template <typename F> static int persistent_ordered(hipStream_t s, F&& launch) {
     PersistOrder& po = g_persist_order[dev];
     if (po.used && po.last != s) {
         if (!po.multi) {
-            WM_FAIL_HIP(hipEventCreateWithFlags(&po.ev, hipEventDisableTiming));
+            if (!po.ev) WM_FAIL_HIP(hipEventCreateWithFlags(&po.ev, hipEventDisableTiming));
             WM_FAIL_HIP(hipDeviceSynchronize());
             po.multi = true;
         } else if (po.recorded) {

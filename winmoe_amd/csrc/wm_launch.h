@@ -69,6 +69,10 @@ int launch_fill_i32(int32_t* p, int32_t v, int64_t n, hipStream_t s);
 int launch_count_hits(const int32_t* ids, int K, int E, uint32_t* hits, int32_t* status, hipStream_t s);
 int launch_axpy(float* acc, const float* y, float w, int n, hipStream_t s);
 
+// Creates the current device's event that orders persistent decode launches
+// across streams (otherwise made on first need).  WM_OK or WM_ERR.
+int persist_order_prepare();
+
 // Geometry of the segment mapping for a row of `in` weights.
 struct Geo {
     int lpr, rpt, active;
