@@ -540,20 +540,33 @@ static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
     a.n_rwaves = (router_bytes + PRING * a.ring_buf - 1) / (PRING * a.ring_buf);
     const int rec = XOP_DW * 4;
     a.o_reg = o; o += (K + 1) * (I / SEG) * rec;
-    a.o_stage = o; o += PSTAGE * 4 * 4096;
     a.o_xop = o; o += (H / SEG) * rec;
     a.o_xop2 = a.o_xop;
     if (sh && sgut != gut) { a.o_xop2 = o; o += (H / SEG) * rec; }
     a.o_gu = o; o += 2 * (K + 1) * a.gu_cap * 4;
     a.o_y = o; o += (K + 1) * a.y_cap * 4;
     o = (o + 255) / 256 * 256;
-    // the streaming waves' rings take what is left, up to PW of them
+    // the streaming waves' rings take what is left, up to PW of them; x and
+    // the router rows get a region of their own when it fits, else they sit
+    // in the first rings until the router helpers are done with them
     a.o_ring = o;
     a.nstream = std::min(PW, (max_lds_per_wg() - o) / (PRING * a.ring_buf));
+    a.o_router = o;
+    if (o + a.nstream * PRING * a.ring_buf + router_bytes <= max_lds_per_wg()) {
+        a.o_router = o + a.nstream * PRING * a.ring_buf;
+        o += router_bytes;
+        a.n_rwaves = 0;
+    }
     if (a.nstream < a.n_rwaves + 1 || a.nstream < 4) return 1;
+    // act tiles: the SwiGLU outputs of a slot come into the streaming waves'
+    // rings in tiles of aseg 64-value segments (8 B tagged words each; whole
+    // K-quant super-blocks, so every tile is a contiguous column range)
+    a.aseg = a.ring_buf >= 8 * SEG * 8 ? 8 : 4;
+    a.nact = (I / SEG + a.aseg - 1) / a.aseg;
+    if (a.nact > PMAXACT || a.aseg * SEG * 8 > a.ring_buf) return 1;
     {   // a streaming wave keeps one descriptor per tile in a lane: at most 64 tiles
         const int ngu_max = (a.gu_tiles + nwg - 1) / nwg, ndn_max = (a.dn_tiles + nwg - 1) / nwg;
-        const int64_t nlist = (int64_t)(2 * ngu_max + ndn_max) * (K + (sh ? 1 : 0));
+        const int64_t nlist = (int64_t)(2 * ngu_max + ndn_max + a.nact) * (K + (sh ? 1 : 0));
         if ((nlist + a.nstream - 1) / a.nstream > 64) return 1;
     }
     // (and more than half of a CU's LDS, so that each CU holds one workgroup)

@@ -77,9 +77,10 @@ namespace wm {
 
 constexpr int PW = 13;                   // streaming waves per workgroup (each loads and processes tiles)
 constexpr int PRING = 1;                 // ring buffers per streaming wave
-constexpr int PSTAGE = 2;                // operand staging waves (the first is also the router wave)
+constexpr int PSTAGE = 2;                // helper waves besides the publisher: the router wave and the x loader
 constexpr int PTHREADS = 64 * (PW + 1 + PSTAGE);  // + publisher
 constexpr int PMAXK = 16;
+constexpr int PMAXACT = 16;              // act tiles of one slot (64-value segments of I / segments per act tile)
 constexpr int P_TL = 32;                 // timeline words per workgroup
 constexpr int P_MAX_WG = 1024;           // workgroups (CUs) the workspace has start-tag words for
 constexpr int P_REP = 8;                 // replicas of the tagged logits (each read by 1/8 of the workgroups)
@@ -107,7 +108,7 @@ struct PersistCtl {
     uint32_t rows_in;              // x and the router rows are in LDS
     uint32_t router_done[2];       // helper h is done with the router rows (their ring space is free)
     uint32_t npicked;              // picks 0 .. npicked-1 of the routing are in ids / valid
-    uint32_t act_ready[PMAXK + 1]; // the slot's SwiGLU operand records are in LDS
+    uint32_t act_done[PMAXK + 1][PMAXACT]; // the slot's SwiGLU operand records of act tile t are in LDS
     int32_t ids[PMAXK];
     float w[PMAXK];
     int32_t valid[PMAXK];
@@ -122,9 +123,10 @@ struct PersistArgs {
     int32_t gu_tiles, dn_tiles;        // tiles of one gate/up matrix (I rows) and of one down matrix (H rows)
     int32_t n_rwaves;                  // streaming waves whose rings hold x and the router rows at the start
     int32_t o_ring, ring_buf, nstream; // LDS: the rings of the nstream streaming waves (PRING buffers of ring_buf bytes each)
-    int32_t x_region;                  // bytes of x / of one router row in the ring space
+    int32_t x_region;                  // bytes of x / of one router row in the router region
+    int32_t o_router;                  // LDS: x and the router rows (the first rings, or a region of its own)
     int32_t o_reg;                     // LDS: SwiGLU operand records [K+1][I/64]
-    int32_t o_stage;                   // LDS: the staging waves' landing areas (PSTAGE x 16 KB)
+    int32_t aseg, nact;                // act tiles: segments of the SwiGLU vector per tile, tiles per slot
     int32_t o_xop, o_xop2;             // LDS: x operand records of the routed / shared gate-up types
     int32_t o_gu, gu_cap;              // LDS: gate and up row sums [K+1][gu_cap] each
     int32_t o_y, y_cap;                // LDS: down row sums [K+1][y_cap]

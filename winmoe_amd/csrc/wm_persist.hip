@@ -2,33 +2,33 @@
 // persistent kernel: one workgroup per CU, and every workgroup takes an equal
 // share of every phase of the step.
 //
-// Workgroup w of nwg (PW compute waves, PISS issuer waves, 3 helper waves):
+// Workgroup w of nwg (PW streaming waves, 3 helper waves):
 //   * router rows [w*rr, (w+1)*rr): reference-order fp32 logits, stored with
 //     this launch's tag in the upper 32 bits, in P_REP replicas;
 //   * gate/up tiles [tw0, tw1) of the shared expert and of every routed slot
 //     (the same row range in every slot);
 //   * down rows of its own output range [d0, d1) for every slot, which it
 //     then combines itself: out[h] = sum_k w_k y_k[h] + shared, in k order.
-// The workgroup's tiles form one list: shared gate/up, routed gate/up slot
-// 0 .. K-1, shared down, routed down slot 0 .. K-1.  The issuer waves stream
-// them into a shared ring of LDS buffers (LDS-DMA, PD tiles in flight each);
-// the compute waves take them in list order (wave c: entries c, c + PW, ...)
-// and write row sums to LDS.
+// The workgroup's tiles form one list (TileList): gate/up of every slot, then
+// per slot its act tiles (the slot's SwiGLU outputs, read back from the other
+// workgroups into operand records) and its down tiles.  Streaming wave c
+// takes entries c, c + PW, ..., loads each into its LDS ring with LDS-DMA and
+// processes it.
 //
 // Hand-offs between workgroups carry the launch tag in every 64-bit word
 // (tag << 32 | value), so a reader needs one read of the data itself and no
 // counter: the routing (every workgroup reads one replica of the tagged
 // logits and runs the K-pass arg-max itself) and the SwiGLU outputs of each
 // slot (every workgroup writes its rows into P_AREP replicas; every workgroup
-// reads one replica back and builds the integer-dot operand records in LDS).
-// A stale word carries an older tag, so a reader never takes it.  The tag is
-// epoch + 1; workgroup 0 stores the new epoch at its end, after it has seen
-// every workgroup's start tag (so no workgroup can still read the old one).
-// Nothing is reset between launches; wm_workspace_reset zeroes the words.
+// reads one replica back in act tiles).  A stale word carries an older tag,
+// so a reader never takes it.  The tag is epoch + 1; workgroup 0 stores the
+// new epoch at its end, after it has seen every workgroup's start tag (so no
+// workgroup can still read the old one).  Nothing is reset between launches;
+// wm_workspace_reset zeroes the words.
 //
-// Helper 0: router DMA and rows 0/2, routing, operand records of half the
-// slots.  Helper 1: rows 1/3, shared-expert gate, SwiGLU publishing, combine.
-// Helper 2: operand records of the other half.
+// Helper 0: router DMA and rows 0/2, routing.  Helper 1: rows 1/3,
+// shared-expert gate, SwiGLU publishing, combine.  Helper 2: x into LDS (and
+// the RMSNorm when the layer has one).
 //
 // Progress: every workgroup must be resident at once (the routing needs every
 // workgroup's router rows).  The host launches one workgroup per CU with more
@@ -49,7 +49,7 @@
 namespace wm {
 
 static_assert(PRING >= 1 && PRING <= 8, "a streaming wave keeps at most PRING tiles in its ring");
-static_assert(PSTAGE >= 2, "the second staging wave loads x for the router");
+static_assert(PSTAGE == 2, "two helper waves besides the publisher: the router wave and the x loader");
 
 typedef __attribute__((address_space(3))) PersistCtl lctl_t;
 
@@ -122,7 +122,7 @@ WM_DEV void lds_wait(lctl_t* ctl, const lds32_t* p, uint32_t target, int32_t* st
 }
 
 // Smallest progress word of the streaming waves: every tile-list entry below
-// it has been processed.
+// it has been processed (a wave done with its entries shows 0xFFFFFFFF).
 WM_DEV uint32_t min_progress(lctl_t* ctl) {
     uint32_t m = lds_ld(&ctl->progress[0]);
 #pragma unroll
@@ -183,8 +183,20 @@ template <int T> WM_DEV int ring_dma(uint64_t G, int nbytes, int lane, lds8_t* d
     return NI;
 }
 
+// The DMA loads of an act tile (nbytes of tagged words, 16-byte aligned, a
+// multiple of 1 KB) into a ring buffer: the first read through the L2 (the
+// workgroups of an XCD reading one replica share its fetch), a re-read
+// (cpol CPOL_SC1) past it.  Returns the instruction count.
+template <int CPOL> WM_DEV int act_dma(uint64_t G, int nbytes, int lane, lds8_t* dst) {
+    const int ni = nbytes >> 10;
+    for (int k = 0; k < ni; k++)
+        __builtin_amdgcn_global_load_lds((const void*)(uintptr_t)(G + 16u * (uint32_t)(lane + 64 * k)),
+                                         (__attribute__((address_space(3))) void*)(dst + 1024 * k), 16, 0, CPOL);
+    return ni;
+}
+
 // ------------------------------------------------------------------ tile list
-enum : int { K_SG = 0, K_SU = 1, K_RG = 2, K_RU = 3, K_SD = 4, K_RD = 5 };
+enum : int { K_SG = 0, K_SU = 1, K_RG = 2, K_RU = 3, K_SD = 4, K_RD = 5, K_ACT = 6 };
 struct TRef {
     int kind, slot, t;    // t: tile within the workgroup's range
 };
@@ -212,18 +224,19 @@ WM_DEV int slot_at(int q, int K, int sh) { return sh ? (q == 0 ? K : q - 1) : q;
 
 // The workgroup's tile list.  With the slots in the order shared, 0 .. K-1,
 // G(q) = the gate/up tiles of slot q (gate and up of a row adjacent) and
-// D(q) = its down tiles, the list is
+// D(q) = its act tiles (the slot's SwiGLU outputs from every workgroup, into
+// operand records) then its down tiles, the list is
 //   G(0) .. G(PLAG), D(0), G(PLAG+1), D(1), G(PLAG+2), ..., D(nq-1-PLAG) .. D(nq-1):
-// the down tiles of a slot come PLAG slots of gate/up later, so the hand-off
-// of its SwiGLU outputs between workgroups overlaps the streaming of later
-// slots instead of waiting at the end.  Every D(q) comes after G(q).
+// the down tiles of a slot come PLAG slots of gate/up later.  Every D(q)
+// comes after G(q).  Streaming wave w takes entries w, w + nstream, ...
 constexpr int PLAG = 16;
 struct TileList {
-    int K, sh, nq, g, d, npre, npair, n;
+    int K, sh, nq, g, d, na, npre, npair, n;
     uint32_t mg, mgd, md;
-    WM_DEV void init(int K_, int sh_, int ngu_, int ndn_) {
+    WM_DEV void init(int K_, int sh_, int ngu_, int ndn_, int nact_) {
         K = K_; sh = sh_; nq = K + sh;
-        g = 2 * ngu_; d = ndn_;
+        na = ndn_ > 0 ? nact_ : 0;       // (a workgroup without down rows needs no records)
+        g = 2 * ngu_; d = na + ndn_;
         npre = min(nq, PLAG + 1);
         npair = max(0, nq - (PLAG + 1));
         n = nq * (g + d);
@@ -256,7 +269,7 @@ struct TileList {
         const bool shared = sh && q == 0;
         r.slot = slot_at(q, K, sh);
         if (down) {
-            r.kind = shared ? K_SD : K_RD; r.t = t;
+            r.kind = t < na ? K_ACT : (shared ? K_SD : K_RD); r.t = t < na ? t : t - na;
         } else {
             r.kind = (t & 1) ? (shared ? K_SU : K_RU) : (shared ? K_SG : K_RG); r.t = t >> 1;
         }
@@ -264,6 +277,51 @@ struct TileList {
     }
 };
 
+// Act tile `at` of `slot`, landed in `buf` (nb bytes loaded from G): segments
+// [at*aseg, (at+1)*aseg) of the slot's tagged SwiGLU outputs, 8 lanes per
+// segment, 8 values per lane.  While a word still carries an older tag (its
+// producer has not published it yet) the tile is loaded again past the L2;
+// then each lane builds its part of the segment's operand record and the
+// tile is marked done for the slot's down tiles.  Act tiles travel in the
+// streaming waves' own lists: a CU's memory pipeline serves its waves in
+// turn, so these 8 KB per slot move at the streaming waves' share instead of
+// one helper wave's.
+template <int DT, int SDT>
+WM_DEV void act_tile(const PersistArgs& a, lctl_t* ctl, lds8_t* lds, lds8_t* buf, uint64_t G, int nb, int slot, int at,
+                     int lane) {
+    const int K = a.K, nseg = a.I / SEG, part = lane & 7, s_in = lane >> 3, seg = at * a.aseg + s_in;
+    const bool on = s_in < a.aseg && seg < nseg;
+    lds_wait(ctl, &ctl->rows_in, 1u, a.status, lane);        // the tag is set before rows_in
+    const uint32_t tag = ctl->tag;
+    const int col = on ? (slot == K ? seg_col(SDT, seg, 8 * part) : seg_col(DT, seg, 8 * part)) : 0;
+    const lds64_t* w = (const lds64_t*)buf + (on ? col - at * a.aseg * SEG : 0);
+    uint32_t it = 0;
+    while (true) {
+        bool ok = true;
+        if (on) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) ok = ok && (uint32_t)(w[j] >> 32) == tag;
+        }
+        if (__builtin_amdgcn_ballot_w64(!ok) == 0ull) break;
+        if (++it > PSPIN_G || aborted(ctl)) {
+            give_up(ctl, a.status, lane);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(4);
+        wave_lds_sync();      // every lane has read the buffer before it is loaded again
+        act_dma<CPOL_SC1>(G, nb, lane, buf);
+        WM_WAIT_VMCNT(0);
+    }
+    if (on) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = __builtin_bit_cast(float, (uint32_t)w[j]);
+        lds32_t* rec = (lds32_t*)(lds + a.o_reg) + ((int64_t)slot * nseg + seg) * XOP_DW;
+        if (slot == K) xop_part<SDT>(v, part, rec);
+        else xop_part<DT>(v, part, rec);
+    }
+    lds_set(&ctl->act_done[slot][at], 1u, lane);
+}
 
 // ------------------------------------------------------------------ streaming waves
 // Streaming wave w of nstream takes the list entries s = w, w + nstream, ...
@@ -291,9 +349,21 @@ struct TileDesc {
     int64_t off;
 };
 template <int GUT, int DT, int SGUT, int SDT>
-WM_DEV TileDesc tile_desc(const PersistArgs& a, const Part& P, const TileList& L, int j, int lg_gu, int lg_dn) {
+WM_DEV TileDesc tile_desc(const PersistArgs& a, const Part& P, const TRef& r, int lg_gu, int lg_dn) {
     const int K = a.K, H = a.H, I = a.I;
-    const TRef r = L.at(j < L.n ? j : 0);
+    if (r.kind == K_ACT) {
+        // segments [t*aseg, (t+1)*aseg) of the slot's tagged SwiGLU outputs in
+        // replica w % P_AREP (byte offset from a.tact)
+        TileDesc d;
+        const int seg0 = r.t * a.aseg;
+        d.kind = K_ACT;
+        d.slot = r.slot;
+        d.rows = 0;
+        d.out = r.t;
+        d.off = ((int64_t)(r.slot * P_AREP + P.w % P_AREP) * I + (int64_t)seg0 * SEG) * 8;
+        d.nb = min(a.aseg, I / SEG - seg0) * SEG * 8;
+        return d;
+    }
     const bool gu = r.kind <= K_RU;
     const int rpt_gu = SEG >> lg_gu, rpt_dn = SEG >> lg_dn;
     const int rpt = gu ? rpt_gu : rpt_dn, rows = gu ? I : H, abs_t = (gu ? P.tw0 : P.d0) + r.t;
@@ -328,19 +398,20 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
     const bool active = wave < ns;
     lds8_t* ring = lds + a.o_ring + wave * PRING * a.ring_buf;
 
-    // ---- descriptors, lane t: this wave's tile t (s = wave + ns * t)
+    // ---- descriptors, lane t: this wave's tile t (entry wave + ns * t)
     int ntile = 0, d_kind, d_slot, d_out, d_rows, d_nb;
     int64_t d_off;
     uint64_t d_addr;
     {
         const Part P = partition(a);
         TileList L;
-        L.init(K, sh, P.ngu, P.ndn);
+        L.init(K, sh, P.ngu, P.ndn, a.nact);
         if (active) ntile = (L.n - wave + ns - 1) / ns;
-        const TileDesc d = tile_desc<GUT, DT, SGUT, SDT>(a, P, L, wave + ns * lane, lg_gu, lg_dn);
+        const TRef r = L.at(min(wave + ns * lane, max(L.n - 1, 0)));
+        const TileDesc d = tile_desc<GUT, DT, SGUT, SDT>(a, P, r, lg_gu, lg_dn);
         d_kind = d.kind; d_slot = d.slot; d_out = d.out; d_rows = d.rows; d_nb = d.nb; d_off = d.off;
-        const uint64_t sg = sval(a.sh_gate), su = sval(a.sh_up), sd = sval(a.sh_down);
-        const uint64_t base = d.kind == K_SG ? sg : d.kind == K_SU ? su : sd;
+        const uint64_t sg = sval(a.sh_gate), su = sval(a.sh_up), sd = sval(a.sh_down), ta = sval(a.tact);
+        const uint64_t base = d.kind == K_SG ? sg : d.kind == K_SU ? su : d.kind == K_ACT ? ta : sd;
         d_addr = routed_kind(d.kind) ? 0ull : base + (uint64_t)d.off;
     }
     int picked = 0;                      // picks whose tiles have addresses
@@ -391,6 +462,7 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
             case K_SG: case K_SU: ni = ring_dma<SGUT>(G, nb, lane, buf); break;
             case K_RG: case K_RU: ni = ring_dma<GUT>(G, nb, lane, buf); break;
             case K_SD: ni = ring_dma<SDT>(G, nb, lane, buf); break;
+            case K_ACT: ni = act_dma<0>(G, nb, lane, buf); break;
             default: ni = ring_dma<DT>(G, nb, lane, buf); break;
             }
         }
@@ -425,7 +497,13 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
             sg.load(buf, lane);
             return row_reduce(seg_dot<T>(sg, xo), lpr);
         };
-        if (kind <= K_RU) {
+        if (kind == K_ACT) {
+            const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)d_addr, tl);
+            const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(d_addr >> 32), tl);
+            const int nb = __builtin_amdgcn_readlane(d_nb, tl);
+            act_tile<DT, SDT>(a, ctl, lds, ring + (t % PRING) * a.ring_buf, ((uint64_t)hi << 32) | lo, nb, slot, out,
+                              lane);
+        } else if (kind <= K_RU) {
             const bool shared = kind <= K_SU;
             const int key = 1000 + (shared ? SGUT : GUT);
             if (xkey != key) {
@@ -440,7 +518,7 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
         } else {
             const bool shared = kind == K_SD;
             if (xkey != slot) {
-                lds_wait(ctl, &ctl->act_ready[slot], 1u, a.status, lane);
+                for (int i = 0; i < a.nact; i++) lds_wait(ctl, &ctl->act_done[slot][i], 1u, a.status, lane);
                 xop_read((const lds32_t*)(lds + a.o_reg) + ((int64_t)slot * nseg_dn + sub_dn) * XOP_DW, xo);
                 xkey = slot;
             }
@@ -470,7 +548,7 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
         // the normalised x lives in LDS (the router's x region) until the
         // router helpers are done, which needs this wave's records first
         if (a.norm_w) lds_wait(ctl, &ctl->x_in, 1u, a.status, lane);
-        const lf32_t* xl = (const lf32_t*)(lds + a.o_ring);
+        const lf32_t* xl = (const lf32_t*)(lds + a.o_router);
         for (int sg = wave * 8 + (lane >> 3); sg < nseg; sg += PW * 8) {
             if (a.norm_w) {
                 xop_part_fetch_lds<GUT>(xl, sg, part, v);
@@ -591,13 +669,16 @@ template <int MAXV>
 WM_DEV void route_tagged(const PersistArgs& a, lctl_t* ctl, int rep, uint32_t tag, int lane, int& my_e, float& wk,
                          bool& degenerate, bool& nonfinite) {
     const int E = a.E, K = a.K;
-    const uint64_t* src = a.tlogits + (int64_t)rep * E;
+    // one lane address plus constant offsets (the loads then need no address
+    // registers of their own, so nothing is spilled around them)
+    const uint64_t* src = a.tlogits + (int64_t)rep * E + lane;
+    const uint64_t pad = (uint64_t)tag << 32;     // words past E: taken as present (never picked)
     // the first read takes every logit; later polls re-read only the words
     // that still carry an older tag (a poll of the whole vector by every
     // workgroup would take bandwidth from the weight streams)
     uint64_t tv[MAXV];
 #pragma unroll
-    for (int i = 0; i < MAXV; i++) tv[i] = gld_first64(src + min(lane + 64 * i, E - 1));
+    for (int i = 0; i < MAXV; i++) tv[i] = lane + 64 * i < E ? gld_first64(src + 64 * i) : pad;
     uint32_t it = 0;
     while (true) {
         bool ok = true;
@@ -611,7 +692,7 @@ WM_DEV void route_tagged(const PersistArgs& a, lctl_t* ctl, int rep, uint32_t ta
         __builtin_amdgcn_s_sleep(8);
 #pragma unroll
         for (int i = 0; i < MAXV; i++)
-            if ((uint32_t)(tv[i] >> 32) != tag) tv[i] = gld_agent64(src + min(lane + 64 * i, E - 1));
+            if ((uint32_t)(tv[i] >> 32) != tag) tv[i] = gld_agent64(src + 64 * i);
     }
     if (lane == 0) ctl->t[11] = now();
     float lv[MAXV];
@@ -647,89 +728,6 @@ WM_DEV void route_tagged(const PersistArgs& a, lctl_t* ctl, int rep, uint32_t ta
     nonfinite = __builtin_amdgcn_ballot_w64(mine && !isfinite(wk)) != 0ull;
 }
 
-// Operand records of the slots at positions q0 .. q0+n-1 of the down order
-// (n * passes <= 4, a pass = 8 segments, 8 lanes per segment, 8 values per
-// lane) from replica `rep` of their tagged SwiGLU outputs.  Each pass's 4 KB
-// of tagged words comes into this staging wave's LDS area with LDS-DMA (1 KB
-// per instruction, so every request is a whole run of cache lines; the first
-// read through the L2, re-reads at agent scope) until every word carries
-// `tag`; then each lane takes its 8 values from LDS and builds its part of
-// the records.
-template <int DT, int SDT>
-WM_DEV void stage_batch(const PersistArgs& a, lctl_t* ctl, lds8_t* lds, int q0, int n, uint32_t tag, int rep,
-                        int sidx, int lane) {
-    const int K = a.K, sh = a.has_shared, I = a.I, nseg = I / SEG, passes = (nseg + 7) / 8;
-    const int part = lane & 7;
-    lds8_t* stg = lds + a.o_stage + sidx * 4 * 4096;
-    // the records are on the critical path of every wave's down tiles: this
-    // wave goes ahead of the streaming waves while it stages
-    __builtin_amdgcn_s_setprio(2);
-    uint64_t tv[4][8];
-    int slot[4], seg[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int q = q0 + i / passes;
-        slot[i] = slot_at(q, K, sh);
-        seg[i] = (i % passes) * 8 + (lane >> 3);
-    }
-    uint32_t it = 0;
-    while (true) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            if (i < n * passes) {
-                const int c0 = (i % passes) * 512;                     // first column of the pass
-                const int nch = min(256, ((I - c0) * 8) >> 4);          // granules of the pass inside the row
-                const uint8_t* src = (const uint8_t*)(a.tact + ((int64_t)slot[i] * P_AREP + rep) * I + c0);
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const int g = min(lane + 64 * k, nch - 1);
-                    if (it == 0)
-                        __builtin_amdgcn_global_load_lds((const void*)(src + 16 * g),
-                                                         (__attribute__((address_space(3))) void*)(stg + i * 4096 + 1024 * k),
-                                                         16, 0, 0);
-                    else
-                        __builtin_amdgcn_global_load_lds((const void*)(src + 16 * g),
-                                                         (__attribute__((address_space(3))) void*)(stg + i * 4096 + 1024 * k),
-                                                         16, 0, CPOL_SC1);
-                }
-            }
-        }
-        WM_WAIT_VMCNT(0);
-        bool ok = true;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const bool on = i < n * passes && seg[i] < nseg;
-            const int col = on ? (slot[i] == K ? seg_col(SDT, seg[i], 8 * part) : seg_col(DT, seg[i], 8 * part)) : 0;
-            const lds64_t* w = (const lds64_t*)(stg + i * 4096) + (col - (i % passes) * 512);
-#pragma unroll
-            for (int j = 0; j < 8; j++) tv[i][j] = on ? w[j] : tagged(tag, 0.0f);
-#pragma unroll
-            for (int j = 0; j < 8; j++) ok = ok && (uint32_t)(tv[i][j] >> 32) == tag;
-        }
-        if (__builtin_amdgcn_ballot_w64(!ok) == 0ull) break;
-        if (++it > PSPIN_G || aborted(ctl)) {
-            give_up(ctl, a.status, lane);
-            break;
-        }
-        __builtin_amdgcn_s_sleep(4);
-        wave_lds_sync();      // every lane has read the area before it is loaded again
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        if (i < n * passes && seg[i] < nseg) {
-            float v[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = __builtin_bit_cast(float, (uint32_t)tv[i][j]);
-            lds32_t* rec = (lds32_t*)(lds + a.o_reg) + ((int64_t)slot[i] * nseg + seg[i]) * XOP_DW;
-            if (slot[i] == K) xop_part<SDT>(v, part, rec);
-            else xop_part<DT>(v, part, rec);
-        }
-    }
-    for (int i = 0; i < n; i++) lds_set(&ctl->act_ready[slot_at(q0 + i, K, sh)], 1u, lane);
-    __builtin_amdgcn_s_setprio(0);
-    wave_lds_sync();
-}
-
 // RMSNorm of the residual stream h in LDS, in place (attention.h:29-44):
 // ss = sum of (double)h[i]^2 (each lane a strided part, then the lanes; the
 // reference adds in index order, which can differ in the last bits of ss),
@@ -748,43 +746,16 @@ WM_DEV void rmsnorm_lds(lf32_t* xl, const float* __restrict__ w, int H, float ep
     WM_WAIT_LGKM0();
 }
 
-// Staging wave `sidx` of PSTAGE: the operand records of the slots, in down
-// order, in batches of up to 4 passes of loads; batch b is staged by wave
-// b % PSTAGE, so that the next batches' loads are in flight while one batch
-// waits.  A batch is read once this workgroup has finished its own gate/up
-// tiles of the batch's last slot (the others finish theirs at about the
-// same time).
-template <int DT, int SDT>
-WM_DEV void stage_slots(const PersistArgs& a, lctl_t* ctl, lds8_t* lds, uint32_t tag, int sidx, int lane) {
-    const Part P = partition(a);
-    if (P.ndn > 0) {
-        const int K = a.K, sh = a.has_shared;
-        TileList L;
-        L.init(K, sh, P.ngu, P.ndn);
-        const int nq = K + sh, passes = (a.I / SEG + 7) / 8, nb = max(1, 4 / passes);
-        for (int q = sidx * nb; q < nq; q += PSTAGE * nb) {
-            const int n = min(nb, nq - q);
-            wait_progress(ctl, (uint32_t)L.gu_end(slot_at(q + n - 1, K, sh)), a.status, lane);
-            stage_batch<DT, SDT>(a, ctl, lds, q, n, tag, P.w % P_AREP, sidx, lane);
-        }
-    }
-    if (lane == 0) ctl->t[5] = now();
-}
-
-// The other staging waves: wait for the tag of this launch, then stage.
-template <int DT, int SDT>
-WM_DEV void helper_stage(const PersistArgs& a, uint8_t* smem, int sidx, int lane) {
+// The x loader (the second helper wave): x into the router region, the
+// RMSNorm in place when the layer has one.
+WM_DEV void helper_xload(const PersistArgs& a, uint8_t* smem, int lane) {
     lctl_t* ctl = (lctl_t*)smem;
-    if (sidx == 1) {
-        __builtin_amdgcn_s_setprio(3);
-        lds8_t* xl = (lds8_t*)smem + a.o_ring;
-        if (!a.forced || a.norm_w) router_dma(a.x, nullptr, a.H, 0, -1, -1, xl, a.x_region, lane);
-        if (a.norm_w) rmsnorm_lds((lf32_t*)xl, a.norm_w, a.H, a.norm_eps, lane);
-        lds_set(&ctl->x_in, 1u, lane);
-        __builtin_amdgcn_s_setprio(0);
-    }
-    lds_wait(ctl, &ctl->rows_in, 1u, a.status, lane);
-    stage_slots<DT, SDT>(a, ctl, (lds8_t*)smem, ctl->tag, sidx, lane);
+    __builtin_amdgcn_s_setprio(3);
+    lds8_t* xl = (lds8_t*)smem + a.o_router;
+    if (!a.forced || a.norm_w) router_dma(a.x, nullptr, a.H, 0, -1, -1, xl, a.x_region, lane);
+    if (a.norm_w) rmsnorm_lds((lf32_t*)xl, a.norm_w, a.H, a.norm_eps, lane);
+    lds_set(&ctl->x_in, 1u, lane);
+    __builtin_amdgcn_s_setprio(0);
 }
 
 // ------------------------------------------------------------------ helper 0: router rows, routing, operand records
@@ -809,12 +780,12 @@ WM_DEV void helper_router(const PersistArgs& a, uint8_t* smem, int lane) {
         const int r0 = P.w * a.rr, nr = max(0, min(a.rr, E - r0));
         // rows 0 and 2 here, rows 1 and 3 on the publishing helper, x on the
         // second staging wave: three waves' loads land together
-        if (nr > 0) router_dma(nullptr, a.router, a.H, r0, 0, nr > 2 ? 2 : -1, lds + a.o_ring, a.x_region, lane);
+        if (nr > 0) router_dma(nullptr, a.router, a.H, r0, 0, nr > 2 ? 2 : -1, lds + a.o_router, a.x_region, lane);
         lds_wait(ctl, &ctl->x_in, 1u, a.status, lane);
         lds_set(&ctl->rows_in, 1u, lane);          // (also when this workgroup has no router rows)
         if (lane == 0) ctl->t[1] = now();
         if (nr > 0)   // rows 0 and 2 here, rows 1 and 3 on the other helper
-            router_chains(lds + a.o_ring, a.x_region, a.H, r0, 0, nr > 2 ? 2 : -1, E, tag, a.tlogits, lane);
+            router_chains(lds + a.o_router, a.x_region, a.H, r0, 0, nr > 2 ? 2 : -1, E, tag, a.tlogits, lane);
         lds_set(&ctl->router_done[0], 1u, lane);
         if (lane == 0) ctl->t[2] = now();
         bool degenerate = false, nonfinite = false;
@@ -854,8 +825,6 @@ WM_DEV void helper_router(const PersistArgs& a, uint8_t* smem, int lane) {
     lds_set(&ctl->routed, 1u, lane);
     __builtin_amdgcn_s_setprio(0);
     if (lane == 0) ctl->t[3] = now();
-
-    stage_slots<DT, SDT>(a, ctl, lds, tag, 0, lane);
 }
 
 // ------------------------------------------------------------------ helper 1: router rows, shared gate, SwiGLU publisher, combine
@@ -868,19 +837,19 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
     const int K = a.K, sh = a.has_shared, nq = K + sh;
     if (!a.forced) {
         const int r0 = P.w * a.rr, nr = max(0, min(a.rr, a.E - r0));
-        if (nr > 1) router_dma(nullptr, a.router, a.H, r0, 1, nr > 3 ? 3 : -1, lds + a.o_ring, a.x_region, lane);
+        if (nr > 1) router_dma(nullptr, a.router, a.H, r0, 1, nr > 3 ? 3 : -1, lds + a.o_router, a.x_region, lane);
     }
     lds_wait(ctl, &ctl->rows_in, 1u, a.status, lane);
     const uint32_t tag = ctl->tag;
     if (!a.forced) {
         const int r0 = P.w * a.rr, nr = max(0, min(a.rr, a.E - r0));
-        if (nr > 1) router_chains(lds + a.o_ring, a.x_region, a.H, r0, 1, nr > 3 ? 3 : -1, a.E, tag, a.tlogits, lane);
+        if (nr > 1) router_chains(lds + a.o_router, a.x_region, a.H, r0, 1, nr > 3 ? 3 : -1, a.E, tag, a.tlogits, lane);
     }
     // the shared gate: from the normalised x in LDS before the x region is
     // given up, or from x in memory after
     if (sh && a.sh_gate_inp && a.norm_w) {
         lds_wait(ctl, &ctl->x_in, 1u, a.status, lane);
-        const float g = wave_shgate_lds((const lf32_t*)(lds + a.o_ring), a.sh_gate_inp, a.H, lane);
+        const float g = wave_shgate_lds((const lf32_t*)(lds + a.o_router), a.sh_gate_inp, a.H, lane);
         if (lane == 0) ctl->sgate = g;
     }
     lds_set(&ctl->router_done[1], 1u, lane);
@@ -895,7 +864,7 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
     lf32_t* uarr = garr + (K + 1) * a.gu_cap;
     lf32_t* yarr = (lf32_t*)(lds + a.o_y);
     TileList L;
-    L.init(K, sh, P.ngu, P.ndn);
+    L.init(K, sh, P.ngu, P.ndn, a.nact);
     if (P.ngu > 0) {
         const int rpt = geometry(GUT, a.H).rpt;
         const int row0 = P.tw0 * rpt, nrows = min(a.I, (P.tw0 + P.ngu) * rpt) - row0;
@@ -917,7 +886,7 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
     }
     if (lane == 0) ctl->t[4] = now();
     if (P.ndn > 0) {
-        wait_progress(ctl, (uint32_t)L.n, a.status, lane);
+        wait_progress(ctl, 0xFFFFFFFFu, a.status, lane);     // every streaming wave is done
         lds_wait(ctl, &ctl->routed, 1u, a.status, lane);     // the weights come after the last pick
         if (lane == 0) ctl->t[6] = now();
         const int rpt = geometry(DT, a.I).rpt;
@@ -968,7 +937,7 @@ __global__ __launch_bounds__(PTHREADS) void k_decode_persist(PersistArgs a) {
     // routing is known (their later polling must not)
     else if (wave == PW) { __builtin_amdgcn_s_setprio(3); helper_router<GUT, DT, SGUT, SDT>(a, smem, lane); }
     else if (wave == PW + 1) { __builtin_amdgcn_s_setprio(3); helper_publish<GUT, DT, SGUT, SDT>(a, smem, lane); }
-    else helper_stage<DT, SDT>(a, smem, wave - PW - 1, lane);
+    else if (wave == PW + 2) helper_xload(a, smem, lane);
 }
 
 template <int GUT, int DT, int SGUT, int SDT>
