@@ -578,14 +578,18 @@ def test_gguf_router_f16_and_quantised(wm, orc, tmp_path, rtype):
 
 def kernel_order_scale(h, H, eps=1e-6):
     """The RMSNorm scale as the persistent kernel forms it: lane l of 64 sums
-    (double)h[i]^2 for i = l, l + 64, ... in order, then an xor butterfly over
-    the lanes (32, 16, ..., 1); scale = 1 / sqrtf((float)(ss / H) + eps)."""
+    (double)h[i]^2 for i = 4l + 256k + c (k, then c = 0..3, in order), then an
+    xor butterfly over the lanes (32, 16, ..., 1); scale = 1 / sqrtf((float)
+    (ss / H) + eps)."""
     v = np.asarray(h, np.float32).astype(np.float64)
     lanes = np.zeros(64)
     for l in range(64):
         acc = 0.0
-        for x in v[l::64]:
-            acc += x * x
+        for k in range((H + 255) // 256):
+            for c in range(4):
+                i = 4 * l + 256 * k + c
+                if i < H:
+                    acc += v[i] * v[i]
         lanes[l] = acc
     for m in (32, 16, 8, 4, 2, 1):
         lanes = lanes + lanes[np.arange(64) ^ m]

@@ -535,8 +535,8 @@ static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
     // SwiGLU operand records | x operand records | gate/up row sums | down row sums
     int o = (int)((sizeof(PersistCtl) + 255) / 256 * 256);
     a.x_region = (H * 4 + 1023) / 1024 * 1024;
-    // (with the RMSNorm, x is normalised in LDS also under forced routing)
-    const int router_bytes = forced ? (d->norm_w ? a.x_region : 0) : (1 + rr) * a.x_region;
+    // x (normalised in place when the layer has an RMSNorm), then the router rows
+    const int router_bytes = (1 + (forced ? 0 : rr)) * a.x_region;
     a.n_rwaves = (router_bytes + PRING * a.ring_buf - 1) / (PRING * a.ring_buf);
     const int rec = XOP_DW * 4;
     a.o_reg = o; o += (K + 1) * (I / SEG) * rec;
@@ -572,6 +572,7 @@ static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
     // (and more than half of a CU's LDS, so that each CU holds one workgroup)
     const int lds = std::max((o + a.nstream * PRING * a.ring_buf + 255) / 256 * 256,
                              (max_lds_per_wg() / 2 + 256) / 256 * 256);
+    if (d->norm_w && !al(d->norm_w, 16)) return 1;      // (its weights are read as 16-byte vectors)
     if (int rc = aligned_input(x, H, (float*)(ws + L.xin), s)) return rc;
     a.x = x; a.out = out; a.router = d->router;
     a.norm_w = d->norm_w; a.norm_eps = d->norm_eps; a.add_res = d->norm_w && d->add_residual ? 1 : 0;

@@ -547,16 +547,11 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
         float v[8], v2[8];
         // the normalised x lives in LDS (the router's x region) until the
         // router helpers are done, which needs this wave's records first
-        if (a.norm_w) lds_wait(ctl, &ctl->x_in, 1u, a.status, lane);
+        lds_wait(ctl, &ctl->x_in, 1u, a.status, lane);
         const lf32_t* xl = (const lf32_t*)(lds + a.o_router);
         for (int sg = wave * 8 + (lane >> 3); sg < nseg; sg += PW * 8) {
-            if (a.norm_w) {
-                xop_part_fetch_lds<GUT>(xl, sg, part, v);
-                if (two) xop_part_fetch_lds<SGUT>(xl, sg, part, v2);
-            } else {
-                xop_part_fetch<GUT>(a.x, sg, part, v);
-                if (two) xop_part_fetch<SGUT>(a.x, sg, part, v2);
-            }
+            xop_part_fetch_lds<GUT>(xl, sg, part, v);
+            if (two) xop_part_fetch_lds<SGUT>(xl, sg, part, v2);
             xop_part<GUT>(v, part, (lds32_t*)(lds + a.o_xop) + sg * XOP_DW);
             if (two) xop_part<SGUT>(v2, part, (lds32_t*)(lds + a.o_xop2) + sg * XOP_DW);
         }
@@ -729,33 +724,69 @@ WM_DEV void route_tagged(const PersistArgs& a, lctl_t* ctl, int rep, uint32_t ta
 }
 
 // RMSNorm of the residual stream h in LDS, in place (attention.h:29-44):
-// ss = sum of (double)h[i]^2 (each lane a strided part, then the lanes; the
-// reference adds in index order, which can differ in the last bits of ss),
-// scale = 1 / sqrtf((float)(ss / H) + eps) correctly rounded, x[i] =
-// (h[i] * scale) * w[i].
-WM_DEV void rmsnorm_lds(lf32_t* xl, const float* __restrict__ w, int H, float eps, int lane) {
+// ss = sum of (double)h[i]^2, lane l adding its elements 4l + 256k + c (k,
+// then c, in order; each product is exact in fp64) before an xor tree over
+// the lanes (32, 16, ..., 1) -- the reference adds in index order, which can
+// differ in the last bits of ss --, scale = 1 / sqrtf((float)(ss / H) + eps)
+// correctly rounded, x[i] = (h[i] * scale) * w[i].  wv[k] holds
+// w[4l + 256k .. +3] (loaded before x arrives).
+WM_DEV void rmsnorm_lds(lf32_t* xl, const f32x4 (&wv)[16], int H, float eps, int lane) {
+    typedef __attribute__((address_space(3))) f32x4 lf32x4_t;
+    const int nst = (H + 255) / 256;
     double ss = 0.0;
-    for (int i = lane; i < H; i += 64) {
-        const double v = (double)xl[i];
-        ss = fma(v, v, ss);          // v * v is exact in fp64: the same as a product then a sum
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        if (k < nst && 4 * lane + 256 * k < H) {
+            const f32x4 v = *(const lf32x4_t*)(xl + 4 * lane + 256 * k);
+            ss = fma((double)v.x, (double)v.x, ss);
+            ss = fma((double)v.y, (double)v.y, ss);
+            ss = fma((double)v.z, (double)v.z, ss);
+            ss = fma((double)v.w, (double)v.w, ss);
+        }
     }
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
     const float scale = __fdiv_rn(1.0f, __fsqrt_rn((float)(ss / (double)H) + eps));
-    for (int i = lane; i < H; i += 64) xl[i] = (xl[i] * scale) * w[i];
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        if (k < nst && 4 * lane + 256 * k < H) {
+            lf32x4_t* p = (lf32x4_t*)(xl + 4 * lane + 256 * k);
+            const f32x4 v = *p;
+            f32x4 o;
+            o.x = (v.x * scale) * wv[k].x;
+            o.y = (v.y * scale) * wv[k].y;
+            o.z = (v.z * scale) * wv[k].z;
+            o.w = (v.w * scale) * wv[k].w;
+            *p = o;
+        }
+    }
     WM_WAIT_LGKM0();
 }
 
-// The x loader (the second helper wave): x into the router region, the
-// RMSNorm in place when the layer has one.
+// The x loader (the second helper wave): x into the router region (every
+// wave's x operand records are built from there), the RMSNorm in place when
+// the layer has one (its weights come in first, with 16-byte loads).
 WM_DEV void helper_xload(const PersistArgs& a, uint8_t* smem, int lane) {
     lctl_t* ctl = (lctl_t*)smem;
     __builtin_amdgcn_s_setprio(3);
     lds8_t* xl = (lds8_t*)smem + a.o_router;
-    if (!a.forced || a.norm_w) router_dma(a.x, nullptr, a.H, 0, -1, -1, xl, a.x_region, lane);
-    if (a.norm_w) rmsnorm_lds((lf32_t*)xl, a.norm_w, a.H, a.norm_eps, lane);
+    f32x4 wv[16];
+    if (a.norm_w) {
+        const int nst = (a.H + 255) / 256;
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+            if (k < nst && 4 * lane + 256 * k < a.H) wv[k] = *(const f32x4*)(a.norm_w + 4 * lane + 256 * k);
+    }
+    router_dma(a.x, nullptr, a.H, 0, -1, -1, xl, a.x_region, lane);
+    if (a.norm_w) rmsnorm_lds((lf32_t*)xl, wv, a.H, a.norm_eps, lane);
     lds_set(&ctl->x_in, 1u, lane);
     __builtin_amdgcn_s_setprio(0);
+    // the shared expert's sigmoid gate (fp64 dot with x, winmoe_inference.c:2005-2009)
+    if (a.has_shared && a.sh_gate_inp) {
+        const float g = wave_shgate_lds((const lf32_t*)xl, a.sh_gate_inp, a.H, lane);
+        if (lane == 0) ctl->sgate = g;
+    }
+    lds_set(&ctl->sgate_ready, 1u, lane);
 }
 
 // ------------------------------------------------------------------ helper 0: router rows, routing, operand records
@@ -845,20 +876,11 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
         const int r0 = P.w * a.rr, nr = max(0, min(a.rr, a.E - r0));
         if (nr > 1) router_chains(lds + a.o_router, a.x_region, a.H, r0, 1, nr > 3 ? 3 : -1, a.E, tag, a.tlogits, lane);
     }
-    // the shared gate: from the normalised x in LDS before the x region is
-    // given up, or from x in memory after
-    if (sh && a.sh_gate_inp && a.norm_w) {
-        lds_wait(ctl, &ctl->x_in, 1u, a.status, lane);
-        const float g = wave_shgate_lds((const lf32_t*)(lds + a.o_router), a.sh_gate_inp, a.H, lane);
-        if (lane == 0) ctl->sgate = g;
-    }
+    // the x loader computes the shared gate from x in the router region: that
+    // region is given up (router_done) only after it is done
+    if (sh && a.sh_gate_inp) lds_wait(ctl, &ctl->sgate_ready, 1u, a.status, lane);
     lds_set(&ctl->router_done[1], 1u, lane);
     __builtin_amdgcn_s_setprio(0);
-    if (sh && a.sh_gate_inp && !a.norm_w) {
-        const float g = wave_shgate(a.x, a.sh_gate_inp, a.H, lane);
-        if (lane == 0) ctl->sgate = g;
-    }
-    lds_set(&ctl->sgate_ready, 1u, lane);
 
     lf32_t* garr = (lf32_t*)(lds + a.o_gu);
     lf32_t* uarr = garr + (K + 1) * a.gu_cap;
