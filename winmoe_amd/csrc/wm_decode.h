@@ -81,6 +81,7 @@ constexpr int PSTAGE = 2;                // helper waves besides the publisher: 
 constexpr int PTHREADS = 64 * (PW + 1 + PSTAGE);  // + publisher
 constexpr int PMAXK = 16;
 constexpr int PMAXACT = 16;              // act tiles of one slot (64-value segments of I / segments per act tile)
+constexpr int P_MAXBLK = 3 * (PMAXK + 1);   // blocks of the tile list: gate/up, act and down of every slot (<= 64)
 constexpr int P_TL = 32;                 // timeline words per workgroup
 constexpr int P_MAX_WG = 1024;           // workgroups (CUs) the workspace has start-tag words for
 constexpr int P_REP = 8;                 // replicas of the tagged logits (each read by 1/8 of the workgroups)
@@ -93,13 +94,13 @@ constexpr uint32_t PSPIN_G = 1u << 17;   // device-memory polls (~1 us each) bef
 template <int T> WM_HD constexpr int ring_tile_bytes() { return T == Q8_0 ? 4416 : (T == Q6_K ? 4096 : ((T == Q4_K || T == Q5_K) ? 3072 : 2048)); }
 WM_HD int ring_tile_bytes_rt(int t) { return t == Q8_0 ? 4416 : (t == Q6_K ? 4096 : ((t == Q4_K || t == Q5_K) ? 3072 : 2048)); }
 
-// LDS control block of one workgroup.  The streaming waves never use LDS
-// atomics (the compiler makes every LDS atomic wait for all of the wave's
-// LDS-DMA loads, which would drain its weight stream): each writes its own
-// words, and readers combine them.
+// LDS control block of one workgroup (zeroed at the start of every launch).
+// The streaming waves use LDS atomics only while none of their LDS-DMA loads
+// is in flight (the compiler makes every LDS atomic wait for all of them).
 struct PersistCtl {
-    uint32_t progress[PW];         // streaming wave w: next tile-list entry it will process (all of its
-                                   // entries below are done); a large value when its list is done
+    uint32_t next;                 // next tile-list entry to claim
+    uint32_t n_done;               // tile-list entries processed
+    uint32_t gu_done[PMAXK + 1];   // gate/up tiles of the slot processed
     uint32_t xop_built[PW];        // streaming wave w wrote its part of the x operand records
     uint32_t routed;               // routing of this step is in ids / w / valid
     uint32_t sgate_ready;          // sgate holds the shared-expert gate
@@ -127,6 +128,8 @@ struct PersistArgs {
     int32_t o_router;                  // LDS: x and the router rows (the first rings, or a region of its own)
     int32_t o_reg;                     // LDS: SwiGLU operand records [K+1][I/64]
     int32_t aseg, nact;                // act tiles: segments of the SwiGLU vector per tile, tiles per slot
+    int32_t nblk;                      // blocks of the tile list
+    uint8_t blk[P_MAXBLK];             // block b: 0 gate/up, 1 act, 2 down | slot position << 2
     int32_t o_xop, o_xop2;             // LDS: x operand records of the routed / shared gate-up types
     int32_t o_gu, gu_cap;              // LDS: gate and up row sums [K+1][gu_cap] each
     int32_t o_y, y_cap;                // LDS: down row sums [K+1][y_cap]

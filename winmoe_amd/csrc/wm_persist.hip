@@ -49,6 +49,7 @@
 namespace wm {
 
 static_assert(PRING >= 1 && PRING <= 8, "a streaming wave keeps at most PRING tiles in its ring");
+static_assert(P_MAXBLK <= 64, "a wave holds one tile-list block per lane");
 static_assert(PSTAGE == 2, "two helper waves besides the publisher: the router wave and the x loader");
 
 typedef __attribute__((address_space(3))) PersistCtl lctl_t;
@@ -121,26 +122,6 @@ WM_DEV void lds_wait(lctl_t* ctl, const lds32_t* p, uint32_t target, int32_t* st
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-// Smallest progress word of the streaming waves: every tile-list entry below
-// it has been processed (a wave done with its entries shows 0xFFFFFFFF).
-WM_DEV uint32_t min_progress(lctl_t* ctl) {
-    uint32_t m = lds_ld(&ctl->progress[0]);
-#pragma unroll
-    for (int w = 1; w < PW; w++) m = min(m, lds_ld(&ctl->progress[w]));
-    return m;
-}
-// The wave waits until every entry below `target` has been processed (bounded).
-WM_DEV void wait_progress(lctl_t* ctl, uint32_t target, int32_t* status, int lane) {
-    uint32_t it = 0;
-    while (min_progress(ctl) < target) {
-        if (++it > PSPIN || aborted(ctl)) {
-            give_up(ctl, status, lane);
-            break;
-        }
-        backoff(it);
-    }
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
 // The wave waits until all n words at p are nonzero (bounded).
 WM_DEV void wait_all(lctl_t* ctl, const lds32_t* p, int n, int32_t* status, int lane) {
     for (int i = 0; i < n; i++) lds_wait(ctl, p + i, 1u, status, lane);
@@ -201,11 +182,6 @@ struct TRef {
     int kind, slot, t;    // t: tile within the workgroup's range
 };
 
-// floor(j / d) for 0 <= j, d < 2^16 with m = floor((2^32 - 1) / d) + 1
-// (exact in that range; d == 1 is passed through).
-WM_DEV int fdiv(int j, int d, uint32_t m) { return d == 1 ? j : (int)__umulhi((uint32_t)j, m); }
-WM_HD uint32_t fdiv_magic(int d) { return d > 1 ? 0xFFFFFFFFu / (uint32_t)d + 1u : 0u; }
-
 struct Part {
     int w, tw0, ngu, d0, ndn;
 };
@@ -222,56 +198,46 @@ WM_DEV Part partition(const PersistArgs& a) {
 // Slot at position q of the order shared, 0 .. K-1 (shared first when present).
 WM_DEV int slot_at(int q, int K, int sh) { return sh ? (q == 0 ? K : q - 1) : q; }
 
-// The workgroup's tile list.  With the slots in the order shared, 0 .. K-1,
-// G(q) = the gate/up tiles of slot q (gate and up of a row adjacent) and
-// D(q) = its act tiles (the slot's SwiGLU outputs from every workgroup, into
-// operand records) then its down tiles, the list is
-//   G(0) .. G(PLAG), D(0), G(PLAG+1), D(1), G(PLAG+2), ..., D(nq-1-PLAG) .. D(nq-1):
-// the down tiles of a slot come PLAG slots of gate/up later.  Every D(q)
-// comes after G(q).  Streaming wave w takes entries w, w + nstream, ...
-constexpr int PLAG = 16;
+// The workgroup's tile list: blocks of entries in the order a.blk gives,
+// G(q) = the gate/up tiles of the slot at position q of the order shared,
+// 0 .. K-1 (gate and up of a row adjacent), A(q) = its act tiles (the slot's
+// SwiGLU outputs from every workgroup, into operand records) and D(q) = its
+// down tiles.  Every A(q) comes after G(q) and before D(q).  Lane b of the
+// wave holds block b's code (kind | position << 2) and first entry, so an
+// entry's block is the count of blocks that start at or before it, minus
+// one.  init and at are called with all 64 lanes active.
 struct TileList {
-    int K, sh, nq, g, d, na, npre, npair, n;
-    uint32_t mg, mgd, md;
-    WM_DEV void init(int K_, int sh_, int ngu_, int ndn_, int nact_) {
-        K = K_; sh = sh_; nq = K + sh;
-        na = ndn_ > 0 ? nact_ : 0;       // (a workgroup without down rows needs no records)
-        g = 2 * ngu_; d = na + ndn_;
-        npre = min(nq, PLAG + 1);
-        npair = max(0, nq - (PLAG + 1));
-        n = nq * (g + d);
-        mg = fdiv_magic(g); mgd = fdiv_magic(g + d); md = fdiv_magic(d);
-    }
-    // list position after the gate/up tiles of `slot`
-    WM_DEV int gu_end(int slot) const {
-        const int q = slot == K ? 0 : slot + sh;
-        return q <= PLAG ? (q + 1) * g : npre * g + (q - PLAG - 1) * (g + d) + d + g;
+    int K, sh, g, na, dn, n;
+    int v_blk, v_start;
+    WM_DEV void init(const PersistArgs& a, int ngu, int ndn, int lane) {
+        K = a.K; sh = a.has_shared;
+        g = 2 * ngu; dn = ndn;
+        na = ndn > 0 ? a.nact : 0;       // (a workgroup without down rows needs no records)
+        const bool on = lane < a.nblk;
+        v_blk = on ? (int)a.blk[lane] : 0;
+        const int c = v_blk & 3, size = on ? (c == 0 ? g : (c == 1 ? na : dn)) : 0;
+        int incl = size;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int u = __shfl_up(incl, o);
+            if (lane >= o) incl += u;
+        }
+        n = __shfl(incl, 63);
+        v_start = on ? incl - size : 0x7FFFFFFF;
     }
     WM_DEV TRef at(int j) const {
-        TRef r;
-        int q, t;
-        bool down;
-        if (j < npre * g) {
-            q = fdiv(j, g, mg); t = j - q * g; down = false;
-        } else {
-            j -= npre * g;
-            if (j < npair * (g + d)) {
-                const int pi = fdiv(j, g + d, mgd), rr = j - pi * (g + d);
-                down = rr < d;
-                q = down ? pi : PLAG + 1 + pi;
-                t = down ? rr : rr - d;
-            } else {
-                j -= npair * (g + d);
-                const int i = fdiv(j, d, md);
-                q = npair + i; t = j - i * d; down = true;
-            }
-        }
+        const int b = __builtin_popcountll(__builtin_amdgcn_ballot_w64(v_start <= j)) - 1;
+        const int code = __builtin_amdgcn_readlane(v_blk, b), t = j - __builtin_amdgcn_readlane(v_start, b);
+        const int q = code >> 2, c = code & 3;
         const bool shared = sh && q == 0;
+        TRef r;
         r.slot = slot_at(q, K, sh);
-        if (down) {
-            r.kind = t < na ? K_ACT : (shared ? K_SD : K_RD); r.t = t < na ? t : t - na;
+        if (c == 0) {
+            r.kind = (t & 1) ? (shared ? K_SU : K_RU) : (shared ? K_SG : K_RG);
+            r.t = t >> 1;
         } else {
-            r.kind = (t & 1) ? (shared ? K_SU : K_RU) : (shared ? K_SG : K_RG); r.t = t >> 1;
+            r.kind = c == 1 ? K_ACT : (shared ? K_SD : K_RD);
+            r.t = t;
         }
         return r;
     }
@@ -324,15 +290,19 @@ WM_DEV void act_tile(const PersistArgs& a, lctl_t* ctl, lds8_t* lds, lds8_t* buf
 }
 
 // ------------------------------------------------------------------ streaming waves
-// Streaming wave w of nstream takes the list entries s = w, w + nstream, ...
-// and both loads them (LDS-DMA into its own ring of PRING buffers) and
-// processes them.  The LDS-DMA bandwidth of a CU grows with the number of
-// waves that issue it (each wave's loads complete in order), not with the
-// loads one wave keeps in flight, so every streaming wave issues its own.
-// The first n_rwaves rings hold x and the router rows at the start; those
-// waves send nothing before the router helpers are done with them.
-
-constexpr int PMAXT = 64;    // tiles per streaming wave (one per lane)
+// The streaming waves claim the list entries in order from one LDS counter
+// (ctl->next): a wave that is free takes the next entry, loads it into its
+// own LDS buffer with LDS-DMA and processes it.  Entries therefore start in
+// list order whatever each wave waited for before (a pick, a hand-off), so
+// the act tiles of a slot are always taken before the slot's down tiles.
+// The LDS-DMA bandwidth of a CU grows with the number of waves that issue it
+// (each wave's loads complete in order), so every streaming wave issues its
+// own.  The first n_rwaves buffers hold x and the router rows at the start;
+// those waves send nothing before the router helpers are done with them.
+//
+// A wave claims and counts only while none of its LDS-DMA loads is in flight
+// (one buffer per wave): the compiler makes an LDS atomic wait for all of
+// them.
 
 // A pointer / 64-bit argument as an opaque scalar value.
 WM_DEV uint64_t sval64(int64_t v) {
@@ -388,87 +358,68 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
     lctl_t* ctl = (lctl_t*)smem;
     lds8_t* lds = (lds8_t*)smem;
     const int wave = __builtin_amdgcn_readfirstlane(wave_v);
-    const int K = a.K, sh = a.has_shared, H = a.H, I = a.I, ns = a.nstream;
+    const int K = a.K, sh = a.has_shared, H = a.H, I = a.I;
     const int nseg_dn = I / SEG;
     // geometry (lanes per row: powers of two; a tile is 64 segments, so every
     // lane holds one)
     const int lg_gu = lg_tile_lanes(H), lg_dn = lg_tile_lanes(I);
     const int sub_gu = lane & ((1 << lg_gu) - 1), rig_gu = lane >> lg_gu;
     const int sub_dn = lane & ((1 << lg_dn) - 1), rig_dn = lane >> lg_dn;
-    const bool active = wave < ns;
-    lds8_t* ring = lds + a.o_ring + wave * PRING * a.ring_buf;
+    const bool active = wave < a.nstream;
+    lds8_t* const buf = lds + a.o_ring + wave * a.ring_buf;
+    const Part P = partition(a);
+    TileList L;
+    L.init(a, P.ngu, P.ndn, lane);
+    const int n = active ? L.n : 0;
+    bool rfree = wave >= a.n_rwaves;     // this wave's buffer is free of the router rows
 
-    // ---- descriptors, lane t: this wave's tile t (entry wave + ns * t)
-    int ntile = 0, d_kind, d_slot, d_out, d_rows, d_nb;
-    int64_t d_off;
-    uint64_t d_addr;
-    {
-        const Part P = partition(a);
-        TileList L;
-        L.init(K, sh, P.ngu, P.ndn, a.nact);
-        if (active) ntile = (L.n - wave + ns - 1) / ns;
-        const TRef r = L.at(min(wave + ns * lane, max(L.n - 1, 0)));
-        const TileDesc d = tile_desc<GUT, DT, SGUT, SDT>(a, P, r, lg_gu, lg_dn);
-        d_kind = d.kind; d_slot = d.slot; d_out = d.out; d_rows = d.rows; d_nb = d.nb; d_off = d.off;
-        const uint64_t sg = sval(a.sh_gate), su = sval(a.sh_up), sd = sval(a.sh_down), ta = sval(a.tact);
-        const uint64_t base = d.kind == K_SG ? sg : d.kind == K_SU ? su : d.kind == K_ACT ? ta : sd;
-        d_addr = routed_kind(d.kind) ? 0ull : base + (uint64_t)d.off;
-    }
-    int picked = 0;                      // picks whose tiles have addresses
-    bool rfree = wave >= a.n_rwaves;     // this wave's ring is free of the router rows
-
-    // the tiles in flight are th .. ti-1; lane t % 64 of v_ni / v_meta: tile
-    // t's instruction count and meta word (0x100 | first byte's offset in the
-    // buffer, 0: no weights)
-    int v_ni = 0, v_meta = 0, th = 0, ti = 0, outstanding = 0;
-
-    // Send tile t (= ti); false (nothing sent) when it needs a pick that is not
-    // known yet and !block.
-    auto try_issue = [&](int t, bool block) -> bool {
-        const int tl = t & 63;
-        const int kind = __builtin_amdgcn_readlane(d_kind, tl);
-        if (routed_kind(kind)) {
-            const int slot = __builtin_amdgcn_readlane(d_slot, tl);
-            if (slot >= picked) {
-                if ((int)lds_ld(&ctl->npicked) <= slot) {
-                    if (!block) return false;
-                    lds_wait(ctl, &ctl->npicked, (uint32_t)(slot + 1), a.status, lane);
-                }
-                picked = (int)lds_ld(&ctl->npicked);
-                // the addresses of the routed tiles whose expert is now known
-                const uint64_t g = sval(a.gate), u = sval(a.up), dn = sval(a.down);
-                const uint64_t gs = sval64(a.gstride), us = sval64(a.ustride), ds = sval64(a.dstride);
-                const bool now_known = routed_kind(d_kind) && d_slot < picked;
-                const int sl = now_known ? d_slot : 0;
-                const int64_t e = (int)lds_ld((const lds32_t*)&ctl->ids[sl]);
-                const bool ok = lds_ld((const lds32_t*)&ctl->valid[sl]) != 0u;
-                const uint64_t base = d_kind == K_RG ? g : d_kind == K_RU ? u : dn;
-                const uint64_t stride = d_kind == K_RG ? gs : d_kind == K_RU ? us : ds;
-                if (now_known) d_addr = ok ? base + (uint64_t)e * stride + (uint64_t)d_off : 0ull;
+    // the claimed entry j: its tile, source address (0: no weights) and the
+    // count of load instructions sent for it
+    int j = n;
+    TileDesc d = {};
+    uint64_t G = 0ull;
+    bool sent = false;
+    auto claim = [&]() {
+        uint32_t v = 0u;
+        if (lane == 0) v = __hip_atomic_fetch_add(&ctl->next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        j = min(__builtin_amdgcn_readfirstlane((int)v), n);
+        if (j < n) d = tile_desc<GUT, DT, SGUT, SDT>(a, P, L.at(j), lg_gu, lg_dn);
+        sent = false;
+    };
+    // Send the claimed tile's loads; false (nothing sent) when it needs a pick
+    // or its buffer that is not available yet and !block.
+    auto send = [&](bool block) -> bool {
+        uint64_t base;
+        if (routed_kind(d.kind)) {
+            if ((int)lds_ld(&ctl->npicked) <= d.slot) {
+                if (!block) return false;
+                lds_wait(ctl, &ctl->npicked, (uint32_t)(d.slot + 1), a.status, lane);
             }
+            const int64_t e = (int)lds_ld((const lds32_t*)&ctl->ids[d.slot]);
+            const bool ok = lds_ld((const lds32_t*)&ctl->valid[d.slot]) != 0u;
+            const uint64_t mb = d.kind == K_RG ? sval(a.gate) : d.kind == K_RU ? sval(a.up) : sval(a.down);
+            const uint64_t st = d.kind == K_RG ? sval64(a.gstride) : d.kind == K_RU ? sval64(a.ustride) : sval64(a.dstride);
+            base = ok ? mb + (uint64_t)e * st : 0ull;
+        } else {
+            base = d.kind == K_SG ? sval(a.sh_gate) : d.kind == K_SU ? sval(a.sh_up)
+                 : d.kind == K_ACT ? sval(a.tact) : sval(a.sh_down);
         }
         if (!rfree) {
+            if (!block) return false;
             wait_all(ctl, ctl->router_done, 2, a.status, lane);
             rfree = true;
         }
-        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)d_addr, tl);
-        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(d_addr >> 32), tl);
-        const uint64_t G = ((uint64_t)hi << 32) | lo;
-        lds8_t* buf = ring + (t % PRING) * a.ring_buf;
-        int ni = 0;
+        G = base ? base + (uint64_t)d.off : 0ull;
         if (G) {
-            const int nb = __builtin_amdgcn_readlane(d_nb, tl);
-            switch (kind) {
-            case K_SG: case K_SU: ni = ring_dma<SGUT>(G, nb, lane, buf); break;
-            case K_RG: case K_RU: ni = ring_dma<GUT>(G, nb, lane, buf); break;
-            case K_SD: ni = ring_dma<SDT>(G, nb, lane, buf); break;
-            case K_ACT: ni = act_dma<0>(G, nb, lane, buf); break;
-            default: ni = ring_dma<DT>(G, nb, lane, buf); break;
+            switch (d.kind) {
+            case K_SG: case K_SU: ring_dma<SGUT>(G, d.nb, lane, buf); break;
+            case K_RG: case K_RU: ring_dma<GUT>(G, d.nb, lane, buf); break;
+            case K_SD: ring_dma<SDT>(G, d.nb, lane, buf); break;
+            case K_ACT: act_dma<0>(G, d.nb, lane, buf); break;
+            default: ring_dma<DT>(G, d.nb, lane, buf); break;
             }
         }
-        v_ni = lane == tl ? ni : v_ni;
-        v_meta = lane == tl ? (G ? (int)(0x100u | (lo & 15u)) : 0) : v_meta;
-        outstanding += ni;
+        sent = true;
         return true;
     };
 
@@ -480,29 +431,20 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
     lf32_t* sums = (lf32_t*)(lds + a.o_gu);
     lf32_t* yarr = (lf32_t*)(lds + a.o_y);
 
-    // Row sums of tile t.
-    auto process = [&](int t) {
-        const int tl = t & 63;
-        const int kind = __builtin_amdgcn_readlane(d_kind, tl);
-        const int slot = __builtin_amdgcn_readlane(d_slot, tl);
-        const int out = __builtin_amdgcn_readlane(d_out, tl);
-        const int nrow = __builtin_amdgcn_readlane(d_rows, tl);
-        const uint32_t meta = (uint32_t)__builtin_amdgcn_readlane(v_meta, tl);
-        const bool has_w = meta != 0u;
-        const lds8_t* buf = ring + (t % PRING) * a.ring_buf + (meta & 15u);
+    // Row sums of the claimed tile (landed in buf).
+    auto process = [&]() {
+        const int kind = d.kind, slot = d.slot, out = d.out, nrow = d.rows;
+        const bool has_w = G != 0ull;
+        const lds8_t* tb = buf + (uint32_t)(G & 15u);
         auto rowsum = [&](auto tag_t, int lpr) -> float {
             constexpr int T = decltype(tag_t)::value;
             if (!has_w) return 0.0f;
             Seg<T> sg;
-            sg.load(buf, lane);
+            sg.load(tb, lane);
             return row_reduce(seg_dot<T>(sg, xo), lpr);
         };
         if (kind == K_ACT) {
-            const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)d_addr, tl);
-            const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(d_addr >> 32), tl);
-            const int nb = __builtin_amdgcn_readlane(d_nb, tl);
-            act_tile<DT, SDT>(a, ctl, lds, ring + (t % PRING) * a.ring_buf, ((uint64_t)hi << 32) | lo, nb, slot, out,
-                              lane);
+            act_tile<DT, SDT>(a, ctl, lds, buf, G, d.nb, slot, out, lane);
         } else if (kind <= K_RU) {
             const bool shared = kind <= K_SU;
             const int key = 1000 + (shared ? SGUT : GUT);
@@ -537,10 +479,13 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
         }
     };
 
-    if (!active) lds_set(&ctl->progress[wave], 0xFFFFFFFFu, lane);
-    // ---- the first tiles (waves whose rings are free), then the x operand
-    // records (8 lanes per segment, 8 segments per wave) while they fly
-    if (rfree) while (ti < ntile && ti < PRING && try_issue(ti, false)) ti++;
+    // ---- the first entry (sent when its buffer is free and it needs no
+    // pick), then the x operand records (8 lanes per segment, 8 segments per
+    // wave) while it flies
+    if (active) {
+        claim();
+        if (j < n && rfree) send(false);
+    }
     {
         const int nseg = H / SEG, part = lane & 7;
         const bool two = sh && SGUT != GUT;
@@ -560,19 +505,19 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
     wait_all(ctl, ctl->xop_built, PW, a.status, lane);
     if (wave == 0 && lane == 0) ctl->t[8] = now();
 
-    while (th < ntile) {
-        while (ti < ntile && ti - th < PRING && try_issue(ti, ti == th)) ti++;
-        // the head's bytes have landed once at most the later tiles'
-        // instructions are outstanding
-        wait_vm(outstanding - __builtin_amdgcn_readlane(v_ni, th & 63));
-        process(th);
-        // progress after the row sums (LDS executes one wave's writes in order)
-        if (lane == 0) *(volatile lds32_t*)&ctl->progress[wave] = (uint32_t)(wave + ns * (th + 1));
+    while (j < n) {
+        if (!sent) send(true);
+        WM_WAIT_VMCNT(0);         // (the claimed tile's loads are the only ones in flight)
+        process();
+        // counted after the row sums (LDS executes one wave's operations in order)
+        if (lane == 0) {
+            if (d.kind <= K_RU)
+                __hip_atomic_fetch_add(&ctl->gu_done[d.slot], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_fetch_add(&ctl->n_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
         wave_lds_sync();          // every lane's reads of the buffer are done before it is refilled
-        outstanding -= __builtin_amdgcn_readlane(v_ni, th & 63);
-        th++;
+        claim();
     }
-    lds_set(&ctl->progress[wave], 0xFFFFFFFFu, lane);
     if (wave == 0 && lane == 0) ctl->t[9] = now();
 }
 
@@ -787,6 +732,26 @@ WM_DEV void helper_xload(const PersistArgs& a, uint8_t* smem, int lane) {
         if (lane == 0) ctl->sgate = g;
     }
     lds_set(&ctl->sgate_ready, 1u, lane);
+    // workgroup 0 advances the epoch once every workgroup has posted this
+    // launch's tag (each has read the old epoch by then); the next launch
+    // starts only after this one ends, so the new value is read only then
+    if (blockIdx.x == 0) {
+        lds_wait(ctl, &ctl->rows_in, 1u, a.status, lane);       // (the tag is set before rows_in)
+        const uint32_t tag = ctl->tag;
+        for (int i = lane; i < a.nwg; i += 64) {
+            uint32_t it = 0;
+            while (gld_agent(a.hello + i) != tag) {
+                if (++it > PSPIN_G || aborted(ctl)) {
+                    atomicOr(a.status, WM_STATUS_SPIN_TIMEOUT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(8);
+            }
+        }
+        WM_WAIT_VMCNT(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        if (lane == 0) gst_agent(a.epoch, tag);
+    }
 }
 
 // ------------------------------------------------------------------ helper 0: router rows, routing, operand records
@@ -886,13 +851,13 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
     lf32_t* uarr = garr + (K + 1) * a.gu_cap;
     lf32_t* yarr = (lf32_t*)(lds + a.o_y);
     TileList L;
-    L.init(K, sh, P.ngu, P.ndn, a.nact);
+    L.init(a, P.ngu, P.ndn, lane);
     if (P.ngu > 0) {
         const int rpt = geometry(GUT, a.H).rpt;
         const int row0 = P.tw0 * rpt, nrows = min(a.I, (P.tw0 + P.ngu) * rpt) - row0;
         for (int q = 0; q < nq; q++) {
             const int slot = slot_at(q, K, sh);
-            wait_progress(ctl, (uint32_t)L.gu_end(slot), a.status, lane);
+            lds_wait(ctl, &ctl->gu_done[slot], (uint32_t)L.g, a.status, lane);
             __builtin_amdgcn_s_setprio(2);
             if (lane == 0 && q < 12) ctl->t[16 + q] = now();
             const bool valid = slot == K || ctl->valid[slot] != 0;
@@ -908,36 +873,36 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
     }
     if (lane == 0) ctl->t[4] = now();
     if (P.ndn > 0) {
-        wait_progress(ctl, 0xFFFFFFFFu, a.status, lane);     // every streaming wave is done
-        lds_wait(ctl, &ctl->routed, 1u, a.status, lane);     // the weights come after the last pick
-        if (lane == 0) ctl->t[6] = now();
         const int rpt = geometry(DT, a.I).rpt;
         const int h0 = P.d0 * rpt, nrows = min(a.H, (P.d0 + P.ndn) * rpt) - h0;
+        // the routing weights into registers while the down tiles finish
+        lds_wait(ctl, &ctl->routed, 1u, a.status, lane);     // the weights come after the last pick
+        bool vk[PMAXK];
+        float wk[PMAXK];
+#pragma unroll
+        for (int k = 0; k < PMAXK; k++) {
+            vk[k] = k < K && ctl->valid[k] != 0;
+            wk[k] = k < K ? ctl->w[k] : 0.0f;
+        }
+        lds_wait(ctl, &ctl->n_done, (uint32_t)L.n, a.status, lane);     // every entry is processed
+        if (lane == 0) ctl->t[6] = now();
         for (int r = lane; r < nrows; r += 64) {
             // out[h] = sum_k w_k y_k[h] (k order, invalid ids skipped) + gate * y_shared[h]
+            float y[PMAXK];
+#pragma unroll
+            for (int k = 0; k < PMAXK; k++) y[k] = vk[k] ? yarr[k * a.y_cap + r] : 0.0f;
+            const float ys = sh ? yarr[K * a.y_cap + r] : 0.0f;
+            const float xr = a.add_res ? a.x[h0 + r] : 0.0f;
             float acc = 0.0f;
-            for (int k = 0; k < K; k++)
-                if (ctl->valid[k]) acc = fmaf(ctl->w[k], yarr[k * a.y_cap + r], acc);
-            if (sh) acc = acc + yarr[K * a.y_cap + r];
-            if (a.add_res) acc = a.x[h0 + r] + acc;          // residual + moe_out
+#pragma unroll
+            for (int k = 0; k < PMAXK; k++)
+                if (vk[k]) acc = fmaf(wk[k], y[k], acc);
+            if (sh) acc = acc + ys;
+            if (a.add_res) acc = xr + acc;          // residual + moe_out
             a.out[h0 + r] = acc;
         }
     }
 
-    if (P.w == 0) {
-        // every workgroup has read the old epoch once all have posted this tag
-        for (int i = lane; i < a.nwg; i += 64) {
-            uint32_t it = 0;
-            while (gld_agent(a.hello + i) != tag) {
-                if (++it > PSPIN_G || aborted(ctl)) {
-                    atomicOr(a.status, WM_STATUS_SPIN_TIMEOUT);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(2);
-            }
-        }
-        if (lane == 0) gst_agent(a.epoch, tag);
-    }
     if (lane == 0) ctl->t[7] = now();
     if (a.timeline && lane < P_TL) a.timeline[(int64_t)P.w * P_TL + lane] = ctl->t[lane];
 }
@@ -948,7 +913,7 @@ template <int GUT, int DT, int SGUT, int SDT>
 __global__ __launch_bounds__(PTHREADS) void k_decode_persist(PersistArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     for (int i = threadIdx.x; i < (int)(sizeof(PersistCtl) / 4); i += PTHREADS)
-        ((lds32_t*)(lds8_t*)smem)[i] = i < PW ? (uint32_t)i : 0u;     // progress[w] = w: wave w's first entry
+        ((lds32_t*)(lds8_t*)smem)[i] = 0u;
     // the timeout test hook: every wait gives up at its first unsuccessful poll
     if (threadIdx.x == 0 && a.probe) ((PersistCtl*)smem)->abort = 1u;
     __syncthreads();
