@@ -577,20 +577,20 @@ def test_gguf_router_f16_and_quantised(wm, orc, tmp_path, rtype):
 # ------------------------------------------------------------------ RMSNorm in, residual out
 
 def kernel_order_scale(h, H, eps=1e-6):
-    """The RMSNorm scale as the persistent kernel forms it: lane l of 64 sums
-    (double)h[i]^2 for i = 4l + 256k + c (k, then c = 0..3, in order), then an
-    xor butterfly over the lanes (32, 16, ..., 1); scale = 1 / sqrtf((float)
-    (ss / H) + eps)."""
+    """The RMSNorm scale as the persistent kernel forms it: lane l of 64 keeps
+    four sums s_c of (double)h[i]^2 over i = 4l + 256k + c (k in order),
+    ss_l = (s_0 + s_1) + (s_2 + s_3), then an xor butterfly over the lanes
+    (32, 16, ..., 1); scale = 1 / sqrtf((float)(ss / H) + eps)."""
     v = np.asarray(h, np.float32).astype(np.float64)
     lanes = np.zeros(64)
     for l in range(64):
-        acc = 0.0
-        for k in range((H + 255) // 256):
-            for c in range(4):
-                i = 4 * l + 256 * k + c
-                if i < H:
-                    acc += v[i] * v[i]
-        lanes[l] = acc
+        s = [0.0, 0.0, 0.0, 0.0]
+        if 4 * l < H:
+            for k in range((H + 255) // 256):
+                for c in range(4):
+                    i = 4 * l + 256 * k + c
+                    s[c] += v[i] * v[i]
+        lanes[l] = (s[0] + s[1]) + (s[2] + s[3])
     for m in (32, 16, 8, 4, 2, 1):
         lanes = lanes + lanes[np.arange(64) ^ m]
     return np.float32(1.0) / np.sqrt(np.float32(lanes[0] / H) + np.float32(eps), dtype=np.float32)

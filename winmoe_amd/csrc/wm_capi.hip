@@ -566,6 +566,10 @@ static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
     a.o_xop = o; o += (H / SEG) * rec;
     a.o_xop2 = a.o_xop;
     if (sh && sgut != gut) { a.o_xop2 = o; o += (H / SEG) * rec; }
+    // the RMSNorm weights share the operand records' space: they are read
+    // before x is in, and every record is written after that
+    a.o_norm = a.o_reg;
+    if (d->norm_w) o = std::max(o, a.o_norm + a.x_region);
     a.o_gu = o; o += 2 * (K + 1) * a.gu_cap * 4;
     a.o_y = o; o += (K + 1) * a.y_cap * 4;
     o = (o + 255) / 256 * 256;

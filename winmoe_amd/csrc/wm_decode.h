@@ -127,6 +127,7 @@ struct PersistArgs {
     int32_t x_region;                  // bytes of x / of one router row in the router region
     int32_t o_router;                  // LDS: x and the router rows (the first rings, or a region of its own)
     int32_t o_reg;                     // LDS: SwiGLU operand records [K+1][I/64]
+    int32_t o_norm;                    // LDS: the RMSNorm weights (x_region bytes, over the records until x is in)
     int32_t aseg, nact;                // act tiles: segments of the SwiGLU vector per tile, tiles per slot
     int32_t nblk;                      // blocks of the tile list
     uint8_t blk[P_MAXBLK];             // block b: 0 gate/up, 1 act, 2 down | slot position << 2

@@ -9,11 +9,12 @@
 //     (the same row range in every slot);
 //   * down rows of its own output range [d0, d1) for every slot, which it
 //     then combines itself: out[h] = sum_k w_k y_k[h] + shared, in k order.
-// The workgroup's tiles form one list (TileList): gate/up of every slot, then
-// per slot its act tiles (the slot's SwiGLU outputs, read back from the other
-// workgroups into operand records) and its down tiles.  Streaming wave c
-// takes entries c, c + PW, ..., loads each into its LDS ring with LDS-DMA and
-// processes it.
+// The workgroup's tiles form one list (TileList) of blocks in a host-given
+// order: gate/up of every slot, the act tiles of each slot (the slot's SwiGLU
+// outputs, read back from the other workgroups into operand records) a few
+// gate/up blocks later, and the down tiles.  The streaming waves claim the
+// entries in list order from an LDS counter; each loads its entry into its
+// own LDS buffer with LDS-DMA and processes it.
 //
 // Hand-offs between workgroups carry the launch tag in every 64-bit word
 // (tag << 32 | value), so a reader needs one read of the data itself and no
@@ -22,13 +23,13 @@
 // slot (every workgroup writes its rows into P_AREP replicas; every workgroup
 // reads one replica back in act tiles).  A stale word carries an older tag,
 // so a reader never takes it.  The tag is epoch + 1; workgroup 0 stores the
-// new epoch at its end, after it has seen every workgroup's start tag (so no
-// workgroup can still read the old one).  Nothing is reset between launches;
-// wm_workspace_reset zeroes the words.
+// new epoch once it has seen every workgroup's start tag (so no workgroup can
+// still read the old one; the next launch begins after this one ends).
+// Nothing is reset between launches; wm_workspace_reset zeroes the words.
 //
-// Helper 0: router DMA and rows 0/2, routing.  Helper 1: rows 1/3,
-// shared-expert gate, SwiGLU publishing, combine.  Helper 2: x into LDS (and
-// the RMSNorm when the layer has one).
+// Helper 0: router DMA and rows 0/2, routing.  Helper 1: rows 1/3, SwiGLU
+// publishing, combine.  Helper 2: x into LDS (and the RMSNorm when the layer
+// has one), the shared-expert gate, and in workgroup 0 the epoch.
 //
 // Progress: every workgroup must be resident at once (the routing needs every
 // workgroup's router rows).  The host launches one workgroup per CU with more
@@ -214,6 +215,8 @@ struct TileList {
         g = 2 * ngu; dn = ndn;
         na = ndn > 0 ? a.nact : 0;       // (a workgroup without down rows needs no records)
         const bool on = lane < a.nblk;
+        // (a per-lane read of the kernel arguments: read as uniform words,
+        // they would be loaded, and waited for, before the first barrier)
         v_blk = on ? (int)a.blk[lane] : 0;
         const int c = v_blk & 3, size = on ? (c == 0 ? g : (c == 1 ? na : dn)) : 0;
         int incl = size;
@@ -668,62 +671,101 @@ WM_DEV void route_tagged(const PersistArgs& a, lctl_t* ctl, int rep, uint32_t ta
     nonfinite = __builtin_amdgcn_ballot_w64(mine && !isfinite(wk)) != 0ull;
 }
 
-// RMSNorm of the residual stream h in LDS, in place (attention.h:29-44):
-// ss = sum of (double)h[i]^2, lane l adding its elements 4l + 256k + c (k,
-// then c, in order; each product is exact in fp64) before an xor tree over
-// the lanes (32, 16, ..., 1) -- the reference adds in index order, which can
-// differ in the last bits of ss --, scale = 1 / sqrtf((float)(ss / H) + eps)
-// correctly rounded, x[i] = (h[i] * scale) * w[i].  wv[k] holds
-// w[4l + 256k .. +3] (loaded before x arrives).
-WM_DEV void rmsnorm_lds(lf32_t* xl, const f32x4 (&wv)[16], int H, float eps, int lane) {
+// RMSNorm of the residual stream h in LDS, in place (attention.h:29-44), for
+// H <= 256 * NST: ss = sum of (double)h[i]^2 (each product exact in fp64),
+// lane l keeping four sums s_c over its elements 4l + 256k + c (k in order),
+// ss_l = (s_0 + s_1) + (s_2 + s_3), then an xor tree over the lanes (32, 16,
+// ..., 1) -- the reference adds in index order, which can differ in the last
+// bits of ss --, scale = 1 / sqrtf((float)(ss / H) + eps) correctly rounded,
+// x[i] = (h[i] * scale) * w[i], w in LDS at wl.  Straight-line code: the
+// reads of a batch are in flight together.  Each region holds at least 256
+// floats, so every read is inside it.
+template <int NST>
+WM_DEV void rmsnorm_lds(lf32_t* xl, const lf32_t* wl, int H, float eps, int lane) {
     typedef __attribute__((address_space(3))) f32x4 lf32x4_t;
-    const int nst = (H + 255) / 256;
-    double ss = 0.0;
+    lf32x4_t* p = (lf32x4_t*)(xl + 4 * lane);
+    const lf32x4_t* q = (const lf32x4_t*)(wl + 4 * lane);
+    const bool in = 4 * lane < H;        // (NST > 1: H >= 512, every lane is in)
+    constexpr int B = NST < 4 ? NST : 4;     // strides per batch of reads
+    double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
-        if (k < nst && 4 * lane + 256 * k < H) {
-            const f32x4 v = *(const lf32x4_t*)(xl + 4 * lane + 256 * k);
-            ss = fma((double)v.x, (double)v.x, ss);
-            ss = fma((double)v.y, (double)v.y, ss);
-            ss = fma((double)v.z, (double)v.z, ss);
-            ss = fma((double)v.w, (double)v.w, ss);
+    for (int k0 = 0; k0 < NST; k0 += B) {
+        f32x4 v[B];
+#pragma unroll
+        for (int k = 0; k < B; k++) v[k] = p[64 * (k0 + k)];
+#pragma unroll
+        for (int k = 0; k < B; k++) {
+            s0 = fma((double)v[k].x, (double)v[k].x, s0);
+            s1 = fma((double)v[k].y, (double)v[k].y, s1);
+            s2 = fma((double)v[k].z, (double)v[k].z, s2);
+            s3 = fma((double)v[k].w, (double)v[k].w, s3);
         }
     }
+    double ss = in ? (s0 + s1) + (s2 + s3) : 0.0;
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
     const float scale = __fdiv_rn(1.0f, __fsqrt_rn((float)(ss / (double)H) + eps));
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
-        if (k < nst && 4 * lane + 256 * k < H) {
-            lf32x4_t* p = (lf32x4_t*)(xl + 4 * lane + 256 * k);
-            const f32x4 v = *p;
+    for (int k0 = 0; k0 < NST; k0 += B) {
+        f32x4 v[B], wv[B];
+#pragma unroll
+        for (int k = 0; k < B; k++) {
+            v[k] = p[64 * (k0 + k)];
+            wv[k] = q[64 * (k0 + k)];
+        }
+#pragma unroll
+        for (int k = 0; k < B; k++) {
             f32x4 o;
-            o.x = (v.x * scale) * wv[k].x;
-            o.y = (v.y * scale) * wv[k].y;
-            o.z = (v.z * scale) * wv[k].z;
-            o.w = (v.w * scale) * wv[k].w;
-            *p = o;
+            o.x = (v[k].x * scale) * wv[k].x;
+            o.y = (v[k].y * scale) * wv[k].y;
+            o.z = (v[k].z * scale) * wv[k].z;
+            o.w = (v[k].w * scale) * wv[k].w;
+            if (in) p[64 * (k0 + k)] = o;
         }
     }
     WM_WAIT_LGKM0();
 }
 
+// H floats (16-byte aligned) into LDS at dst with LDS-DMA, 1 KB per
+// instruction (lanes past the end reload the last granule); no wait.
+WM_DEV void vec_dma(const float* src, int H, lds8_t* dst, int lane) {
+    const int units = (H * 4 + 1023) >> 10, nch = (H * 4 + 15) >> 4;
+    for (int k = 0; k < units; k++) {
+        const int i = min(lane + 64 * k, nch - 1);
+        __builtin_amdgcn_global_load_lds((const void*)((const uint8_t*)src + 16 * i),
+                                         (__attribute__((address_space(3))) void*)(dst + 1024 * k), 16, 0, 0);
+    }
+}
+
+// x into the region at xl and the RMSNorm in place, for H <= 256 * NST; the
+// norm weights land at o_norm (over the operand records, which are built
+// only after x is in) with x.
+template <int NST> WM_DEV void x_norm_in(const PersistArgs& a, uint8_t* smem, lds8_t* xl, int lane) {
+    lds8_t* wl = (lds8_t*)smem + a.o_norm;
+    vec_dma(a.x, a.H, xl, lane);
+    vec_dma(a.norm_w, a.H, wl, lane);
+    WM_WAIT_VMCNT(0);
+    rmsnorm_lds<NST>((lf32_t*)xl, (const lf32_t*)wl, a.H, a.norm_eps, lane);
+}
+
 // The x loader (the second helper wave): x into the router region (every
 // wave's x operand records are built from there), the RMSNorm in place when
-// the layer has one (its weights come in first, with 16-byte loads).
+// the layer has one (its weights come in with x).
 WM_DEV void helper_xload(const PersistArgs& a, uint8_t* smem, int lane) {
     lctl_t* ctl = (lctl_t*)smem;
     __builtin_amdgcn_s_setprio(3);
     lds8_t* xl = (lds8_t*)smem + a.o_router;
-    f32x4 wv[16];
     if (a.norm_w) {
-        const int nst = (a.H + 255) / 256;
-#pragma unroll
-        for (int k = 0; k < 16; k++)
-            if (k < nst && 4 * lane + 256 * k < a.H) wv[k] = *(const f32x4*)(a.norm_w + 4 * lane + 256 * k);
+        switch ((a.H + 255) / 256) {
+        case 1: x_norm_in<1>(a, smem, xl, lane); break;
+        case 2: x_norm_in<2>(a, smem, xl, lane); break;
+        case 4: x_norm_in<4>(a, smem, xl, lane); break;
+        case 8: x_norm_in<8>(a, smem, xl, lane); break;
+        default: x_norm_in<16>(a, smem, xl, lane); break;
+        }
+    } else {
+        router_dma(a.x, nullptr, a.H, 0, -1, -1, xl, a.x_region, lane);
     }
-    router_dma(a.x, nullptr, a.H, 0, -1, -1, xl, a.x_region, lane);
-    if (a.norm_w) rmsnorm_lds((lf32_t*)xl, wv, a.H, a.norm_eps, lane);
     lds_set(&ctl->x_in, 1u, lane);
     __builtin_amdgcn_s_setprio(0);
     // the shared expert's sigmoid gate (fp64 dot with x, winmoe_inference.c:2005-2009)
