@@ -380,6 +380,75 @@ EXTRA = ["c1", "c3", "c4", "c5"]
 CPU_SAMPLE = {"c1": 1, "c2": 16, "c3": 16, "c4": 4, "c5": 8}
 
 
+# marks of the persistent step's per-workgroup timeline (include/winmoe_hip.h, wm_workspace_timeline)
+TL_MARKS = [(1, "x and router rows in LDS"), (8, "x operand records built"), (2, "own logits stored"),
+            (11, "every logit polled"), (3, "routing known")] + \
+           [(16 + q, f"SwiGLU of slot position {q} published") for q in range(12)] + \
+           [(4, "last SwiGLU published"), (9, "first streaming wave done"), (6, "combine start"), (7, "end")]
+
+
+def timeline_report(name, steps):
+    """The device-clock timeline of the last of `steps` decode steps of the
+    workload's first layer (graph replay), per mark the earliest, median and
+    latest workgroup, in us from the earliest workgroup start."""
+    import numpy as np
+    import torch
+    from winmoe_amd.moe import MoELayer
+    wl = Workload(name)
+    if wl.prefill:
+        print("--timeline covers the decode workloads (c1-c4)", file=sys.stderr)
+        sys.exit(2)
+    sl, cfg = wl.layers[0], wl.cfg
+    c = sl.cfg
+    layer = MoELayer(c.H, c.I, sl.layer.E, c.K, sl.router, sl.gate, sl.up, sl.down, c.types, shared=sl.shared,
+                     max_tokens=cfg.tokens, timeline=True, norm_w=wl.norms[0] if wl.chained else None,
+                     add_residual=wl.chained)
+    out = torch.empty(cfg.tokens, cfg.H, device="cuda")
+
+    def step(i):
+        t = i % cfg.tokens
+        if wl.routes is None:
+            layer.decode(wl.X[t], out=out[t], step=i)
+        else:
+            layer.decode_forced(wl.X[t], wl.routes[0][2][t], wl.routes[0][3][t], out=out[t], step=i)
+    for i in range(16):
+        step(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            step(i)
+    g.replay()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    layer.check()
+    us = a.elapsed_time(b) * 1000.0 / steps
+    nwg = torch.cuda.get_device_properties(0).multi_processor_count
+    tl = layer.timeline().cpu().numpy().reshape(-1)[: nwg * 32].reshape(nwg, 32).astype(np.int64)
+    tick_us = 1000.0 / wm_clock_khz()
+    t0 = tl[:, 0][tl[:, 0] > 0].min()
+    print(f"persistent decode step timeline, workload {cfg.name} (layer 0), last of {steps} steps replayed in a HIP "
+          f"graph, {nwg} workgroups; us from the earliest workgroup start")
+    print(f"{'mark':36s} {'min':>8s} {'median':>8s} {'max':>8s}")
+    for k, label in sorted(TL_MARKS, key=lambda m: np.median(tl[:, m[0]][tl[:, m[0]] > 0]) if (tl[:, m[0]] > 0).any()
+                           else 1e30):
+        v = tl[:, k]
+        v = v[v > 0]
+        if v.size == 0:
+            continue
+        r = (v - t0) * tick_us
+        print(f"{label:36s} {r.min():8.2f} {np.median(r):8.2f} {r.max():8.2f}")
+    print(f"step time over the replay (HIP events): {us:.2f} us")
+
+
+def wm_clock_khz():
+    import winmoe_amd as wm
+    return float(wm.load().wm_device_clock_khz())
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -390,6 +459,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--multi-kernel", action="store_true",
                     help="run each decode step as per-phase kernel launches instead of the single fused launch")
+    ap.add_argument("--timeline", action="store_true",
+                    help="print the device-clock timeline of the persistent decode step of --config (its first "
+                         "layer) instead of the JSON line")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run 4 plain device copies and 4 read-only reductions of this many MiB (kernels of "
                          "known traffic for the rocprofv3 FETCH_SIZE / WRITE_SIZE calibration)")
@@ -447,6 +519,10 @@ def main():
         del wl
         torch.cuda.empty_cache()
         return e
+
+    if args.timeline:
+        timeline_report(args.config, min(args.steps, 256))
+        return
 
     head = run(args.config, args.steps, args.warmup, True)
     configs = None

@@ -172,7 +172,14 @@ int wm_workspace_reset(const wm_layer_desc* d, int max_tokens, void* ws, int64_t
  * finished (0 otherwise), and the time its weight rows had landed in LDS
  * (router items only); kind 0 = shared gate / forced
  * routing, 1 = router, 2 = shared gate/up, 3 = routed gate/up, 4 = down (+8
- * when it also combined). */
+ * when it also combined).
+ * The persistent step (the default decode path) writes instead 32 words per
+ * workgroup, [workgroup][32], device clock ticks (0: not reached): 0 start,
+ * 1 x and the router rows in LDS, 2 its logits stored, 3 routing known,
+ * 4 its last SwiGLU outputs published, 6 combine start, 7 end, 8 x operand
+ * records built, 9 first streaming wave done, 11 every logit polled,
+ * 16 + q its SwiGLU outputs of slot position q published (q < 12; position 0
+ * is the shared expert when the layer has one). */
 int wm_workspace_timeline(const wm_layer_desc* d, int max_tokens, int64_t* offset, int64_t* capacity);
 int64_t wm_device_clock_khz(void);
 

@@ -503,29 +503,6 @@ template <typename F> static int persistent_ordered(hipStream_t s, F&& launch) {
     return WM_OK;
 }
 
-// Block order of the persistent step's tile list for nq slots (positions q
-// in the order shared, 0 .. K-1): G(q) = gate/up tiles, A(q) = act tiles,
-// D(q) = down tiles, coded kind | q << 2 (kind 0, 1, 2).  A slot's SwiGLU
-// outputs are complete once every workgroup has processed its G(q), so A(q)
-// waits P_ALAG gate/up blocks after G(q) (the other workgroups' share of it
-// lands meanwhile); the down blocks follow every gate/up block, and each act
-// block not placed by then comes P_ALEAD down blocks before its D(q).
-constexpr int P_ALAG = 3, P_ALEAD = 1;
-static int persist_blocks(int nq, uint8_t* blk) {
-    int nb = 0;
-    auto emit = [&](int kind, int q) { blk[nb++] = (uint8_t)(kind | (q << 2)); };
-    for (int q = 0; q < nq; q++) {
-        emit(0, q);
-        if (q >= P_ALAG) emit(1, q - P_ALAG);
-    }
-    int next_a = std::max(0, nq - P_ALAG);
-    for (int q = 0; q < nq; q++) {
-        while (next_a < nq && next_a <= q + P_ALEAD) emit(1, next_a++);
-        emit(2, q);
-    }
-    return nb;
-}
-
 // One launch of the persistent step kernel (wm_persist.hip); returns 1 when
 // the layer does not fit it (the caller then uses the work-item-list kernel).
 static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, const float* x, float* out,
@@ -591,7 +568,6 @@ static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
     a.aseg = a.ring_buf >= 8 * SEG * 8 ? 8 : 4;
     a.nact = (I / SEG + a.aseg - 1) / a.aseg;
     if (a.nact > PMAXACT || a.aseg * SEG * 8 > a.ring_buf) return 1;
-    a.nblk = persist_blocks(K + (sh ? 1 : 0), a.blk);
     // (and more than half of a CU's LDS, so that each CU holds one workgroup)
     const int lds = std::max((o + a.nstream * PRING * a.ring_buf + 255) / 256 * 256,
                              (max_lds_per_wg() / 2 + 256) / 256 * 256);

@@ -81,7 +81,6 @@ constexpr int PSTAGE = 2;                // helper waves besides the publisher: 
 constexpr int PTHREADS = 64 * (PW + 1 + PSTAGE);  // + publisher
 constexpr int PMAXK = 16;
 constexpr int PMAXACT = 16;              // act tiles of one slot (64-value segments of I / segments per act tile)
-constexpr int P_MAXBLK = 3 * (PMAXK + 1);   // blocks of the tile list: gate/up, act and down of every slot (<= 64)
 constexpr int P_TL = 32;                 // timeline words per workgroup
 constexpr int P_MAX_WG = 1024;           // workgroups (CUs) the workspace has start-tag words for
 constexpr int P_REP = 8;                 // replicas of the tagged logits (each read by 1/8 of the workgroups)
@@ -129,8 +128,6 @@ struct PersistArgs {
     int32_t o_reg;                     // LDS: SwiGLU operand records [K+1][I/64]
     int32_t o_norm;                    // LDS: the RMSNorm weights (x_region bytes, over the records until x is in)
     int32_t aseg, nact;                // act tiles: segments of the SwiGLU vector per tile, tiles per slot
-    int32_t nblk;                      // blocks of the tile list
-    uint8_t blk[P_MAXBLK];             // block b: 0 gate/up, 1 act, 2 down | slot position << 2
     int32_t o_xop, o_xop2;             // LDS: x operand records of the routed / shared gate-up types
     int32_t o_gu, gu_cap;              // LDS: gate and up row sums [K+1][gu_cap] each
     int32_t o_y, y_cap;                // LDS: down row sums [K+1][y_cap]

@@ -9,10 +9,10 @@
 //     (the same row range in every slot);
 //   * down rows of its own output range [d0, d1) for every slot, which it
 //     then combines itself: out[h] = sum_k w_k y_k[h] + shared, in k order.
-// The workgroup's tiles form one list (TileList) of blocks in a host-given
-// order: gate/up of every slot, the act tiles of each slot (the slot's SwiGLU
-// outputs, read back from the other workgroups into operand records) a few
-// gate/up blocks later, and the down tiles.  The streaming waves claim the
+// The workgroup's tiles form one list (TileList) of blocks: gate/up of every
+// slot, the act tiles of each slot (the slot's SwiGLU outputs, read back from
+// the other workgroups into operand records) a few gate/up blocks later, and
+// the down tiles.  The streaming waves claim the
 // entries in list order from an LDS counter; each loads its entry into its
 // own LDS buffer with LDS-DMA and processes it.
 //
@@ -50,7 +50,7 @@
 namespace wm {
 
 static_assert(PRING >= 1 && PRING <= 8, "a streaming wave keeps at most PRING tiles in its ring");
-static_assert(P_MAXBLK <= 64, "a wave holds one tile-list block per lane");
+static_assert(3 * (PMAXK + 1) <= 64, "a wave holds one tile-list block per lane");
 static_assert(PSTAGE == 2, "two helper waves besides the publisher: the router wave and the x loader");
 
 typedef __attribute__((address_space(3))) PersistCtl lctl_t;
@@ -199,14 +199,20 @@ WM_DEV Part partition(const PersistArgs& a) {
 // Slot at position q of the order shared, 0 .. K-1 (shared first when present).
 WM_DEV int slot_at(int q, int K, int sh) { return sh ? (q == 0 ? K : q - 1) : q; }
 
-// The workgroup's tile list: blocks of entries in the order a.blk gives,
-// G(q) = the gate/up tiles of the slot at position q of the order shared,
-// 0 .. K-1 (gate and up of a row adjacent), A(q) = its act tiles (the slot's
-// SwiGLU outputs from every workgroup, into operand records) and D(q) = its
-// down tiles.  Every A(q) comes after G(q) and before D(q).  Lane b of the
-// wave holds block b's code (kind | position << 2) and first entry, so an
-// entry's block is the count of blocks that start at or before it, minus
-// one.  init and at are called with all 64 lanes active.
+// The workgroup's tile list: blocks of entries, G(q) = the gate/up tiles of
+// the slot at position q of the order shared, 0 .. K-1 (gate and up of a row
+// adjacent), A(q) = its act tiles (the slot's SwiGLU outputs from every
+// workgroup, into operand records) and D(q) = its down tiles.  A slot's
+// SwiGLU outputs are complete once every workgroup has processed its G(q), so
+// A(q) comes P_ALAG gate/up blocks after G(q) (the other workgroups' share
+// lands meanwhile); the down blocks follow every gate/up block, and each act
+// block not placed by then comes P_ALEAD down blocks before its D(q).  Every
+// A(q) is after G(q) and before D(q).  Lane b of the wave holds block b's
+// code (kind | position << 2) and first entry, so an entry's block is the
+// count of blocks that start at or before it, minus one.  The order is built
+// in registers (uniform control flow), with no memory read.  init and at are
+// called with all 64 lanes active.
+constexpr int P_ALAG = 3, P_ALEAD = 1;
 struct TileList {
     int K, sh, g, na, dn, n;
     int v_blk, v_start;
@@ -214,11 +220,25 @@ struct TileList {
         K = a.K; sh = a.has_shared;
         g = 2 * ngu; dn = ndn;
         na = ndn > 0 ? a.nact : 0;       // (a workgroup without down rows needs no records)
-        const bool on = lane < a.nblk;
-        // (a per-lane read of the kernel arguments: read as uniform words,
-        // they would be loaded, and waited for, before the first barrier)
-        v_blk = on ? (int)a.blk[lane] : 0;
-        const int c = v_blk & 3, size = on ? (c == 0 ? g : (c == 1 ? na : dn)) : 0;
+        const int nq = K + sh;
+        int code = 0, size = 0, b = 0;
+        auto emit = [&](int kind, int q, int sz) {
+            if (lane == b) {
+                code = kind | (q << 2);
+                size = sz;
+            }
+            b++;
+        };
+        for (int q = 0; q < nq; q++) {
+            emit(0, q, g);
+            if (q >= P_ALAG) emit(1, q - P_ALAG, na);
+        }
+        int next_a = max(0, nq - P_ALAG);
+        for (int q = 0; q < nq; q++) {
+            for (; next_a < nq && next_a <= q + P_ALEAD; next_a++) emit(1, next_a, na);
+            emit(2, q, dn);
+        }
+        v_blk = code;
         int incl = size;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
@@ -226,7 +246,7 @@ struct TileList {
             if (lane >= o) incl += u;
         }
         n = __shfl(incl, 63);
-        v_start = on ? incl - size : 0x7FFFFFFF;
+        v_start = lane < b ? incl - size : 0x7FFFFFFF;
     }
     WM_DEV TRef at(int j) const {
         const int b = __builtin_popcountll(__builtin_amdgcn_ballot_w64(v_start <= j)) - 1;
@@ -959,14 +979,22 @@ __global__ __launch_bounds__(PTHREADS) void k_decode_persist(PersistArgs a) {
     // the timeout test hook: every wait gives up at its first unsuccessful poll
     if (threadIdx.x == 0 && a.probe) ((PersistCtl*)smem)->abort = 1u;
     __syncthreads();
+    // the arguments through a pointer the compiler cannot see through: each
+    // role loads the words it needs after the barrier (loaded before it, they
+    // came in several waited rounds, each one cold-cache latency, before any
+    // wave could start)
+    typedef const __attribute__((address_space(4))) PersistArgs kargs_t;
+    kargs_t* ka = (kargs_t*)__builtin_amdgcn_kernarg_segment_ptr();      // (the only kernel argument)
+    asm volatile("" : "+s"(ka));
+    const PersistArgs* ap = (const PersistArgs*)ka;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (wave < PW) stream_wave<GUT, DT, SGUT, SDT>(a, smem, wave, lane);
+    if (wave < PW) stream_wave<GUT, DT, SGUT, SDT>(*ap, smem, wave, lane);
     // the router rows and the routing are the critical path: the helper
     // waves win the issue arbitration against the streaming waves until the
     // routing is known (their later polling must not)
-    else if (wave == PW) { __builtin_amdgcn_s_setprio(3); helper_router<GUT, DT, SGUT, SDT>(a, smem, lane); }
-    else if (wave == PW + 1) { __builtin_amdgcn_s_setprio(3); helper_publish<GUT, DT, SGUT, SDT>(a, smem, lane); }
-    else if (wave == PW + 2) helper_xload(a, smem, lane);
+    else if (wave == PW) { __builtin_amdgcn_s_setprio(3); helper_router<GUT, DT, SGUT, SDT>(*ap, smem, lane); }
+    else if (wave == PW + 1) { __builtin_amdgcn_s_setprio(3); helper_publish<GUT, DT, SGUT, SDT>(*ap, smem, lane); }
+    else if (wave == PW + 2) helper_xload(*ap, smem, lane);
 }
 
 template <int GUT, int DT, int SGUT, int SDT>
