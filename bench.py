@@ -444,6 +444,68 @@ def timeline_report(name, steps):
     print(f"step time over the replay (HIP events): {us:.2f} us")
 
 
+def stream_report(name, n_slots, steps, warmup):
+    """Decode steps of the workload's layer shape with the experts in pinned
+    host memory, made resident on demand in a pool of n_slots HBM slots
+    (wm_pool_*), Zipf routing with consecutive-token overlap (the forced
+    routing of the C4 workload, at this layer's E and K).  One JSON line:
+    tokens/s, misses per token, achieved host -> device GB/s."""
+    import numpy as np
+    import torch
+    import winmoe_amd as wm
+    from winmoe_amd import synth
+    cfg = synth.CONFIGS[name]
+    if cfg.x_dtype == "bf16" and cfg.tokens > 1:
+        print("--stream-slots covers the decode workloads (c1-c4)", file=sys.stderr)
+        sys.exit(2)
+    sl = synth.build_layer(cfg, layer_index=0, max_tokens=1)
+    c = sl.cfg
+    E = sl.layer.E
+    parts = [wm.matrix_bytes(c.types[0], c.I, c.H), wm.matrix_bytes(c.types[1], c.I, c.H),
+             wm.matrix_bytes(c.types[2], c.H, c.I)]
+    log(f"copying {E} experts ({E * sum(parts) / 1e9:.2f} GB) to pinned host memory")
+    src = []
+    for t in (sl.gate, sl.up, sl.down):
+        h = torch.empty(t.numel(), dtype=torch.uint8, pin_memory=True)
+        h.copy_(t)
+        src.append(h.view(E, -1))
+    pool = wm.ExpertPool(n_slots, *parts)
+    layer = pool.layer(c.H, c.I, c.K, c.types, shared=sl.shared, max_tokens=steps + warmup)
+    rng = np.random.default_rng(11)
+    T = steps + warmup
+    ids = synth.zipf_routing(T, E, c.K, rng, overlap=synth.OVERLAP)
+    w = torch.from_numpy(synth.softmax_weights(T, c.K, rng)).cuda()
+    X = synth.make_hidden(cfg, tokens=min(T, 256))
+    out = torch.empty(c.H, device="cuda")
+    slots = torch.empty(T, c.K, dtype=torch.int32, device="cuda")
+
+    def step(t):
+        pool.acquire(0, ids[t], *src, out=slots[t])
+        layer.decode_forced(X[t % X.shape[0]], slots[t], w[t], out=out, step=t)
+        pool.release()
+    for t in range(warmup):
+        step(t)
+    torch.cuda.synchronize()
+    h0, m0, b0 = pool.stats()
+    t0 = time.perf_counter()
+    for t in range(warmup, T):
+        step(t)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    layer.check()
+    h1, m1, b1 = pool.stats()
+    rec = {"report": "host -> HBM expert streaming", "workload": cfg.name, "experts": E, "top_k": c.K,
+           "expert_bytes": sum(parts), "pool_slots": n_slots, "pool_bytes": n_slots * pool.slot_bytes,
+           "routing": f"zipf s={synth.ZIPF_S} overlap={synth.OVERLAP}", "steps": steps, "warmup": warmup,
+           "tokens_per_s": round(steps / dt, 1), "ms_per_step": round(dt * 1e3 / steps, 4),
+           "hit_rate": round((h1 - h0) / max(1, (h1 - h0) + (m1 - m0)), 4),
+           "misses_per_token": round((m1 - m0) / steps, 3),
+           "h2d_GBps": round((b1 - b0) / dt / 1e9, 2), "timing": "host wall clock over the timed steps, "
+           "synchronised on both sides; copies on the pool's stream overlap the steps"}
+    print(json.dumps(rec))
+    pool.close()
+
+
 def wm_clock_khz():
     import winmoe_amd as wm
     return float(wm.load().wm_device_clock_khz())
@@ -462,6 +524,10 @@ def main():
     ap.add_argument("--timeline", action="store_true",
                     help="print the device-clock timeline of the persistent decode step of --config (its first "
                          "layer) instead of the JSON line")
+    ap.add_argument("--stream-slots", type=int, default=0,
+                    help="host -> HBM expert streaming: run --config's layer shape with its experts in pinned host "
+                         "memory through a pool of this many HBM slots (Zipf routing) and print one report line "
+                         "instead of the JSON line")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run 4 plain device copies and 4 read-only reductions of this many MiB (kernels of "
                          "known traffic for the rocprofv3 FETCH_SIZE / WRITE_SIZE calibration)")
@@ -522,6 +588,9 @@ def main():
 
     if args.timeline:
         timeline_report(args.config, min(args.steps, 256))
+        return
+    if args.stream_slots > 0:
+        stream_report(args.config, args.stream_slots, min(args.steps, 256), min(args.warmup, 64))
         return
 
     head = run(args.config, args.steps, args.warmup, True)

@@ -260,6 +260,48 @@ int wm_moe_decode_noalloc(const wm_layer_desc* d, const float* x, float* out, in
  * the current device. */
 int wm_noalloc_status(int32_t* status_out);
 
+/* ------------------------------------------- host -> HBM expert streaming */
+/* For models whose experts do not all fit in HBM: a pool of n_slots expert
+ * slots in HBM, each holding one expert's [gate | up | down] bytes (each part
+ * 256-byte aligned), filled from host memory on demand.  Replaces the
+ * reference's miss path -- asynchronous reads of every missing pick issued
+ * before the first is computed, into [gate | up | down] slots
+ * (winmoe_inference.c:1736-1789) -- and the per-slot upload of the GPU expert
+ * cache (gpu_offload.cu:590-659).  A missing expert is copied with
+ * asynchronous host-to-device copies on the pool's own stream; the step's
+ * stream waits for those copies on the device, and a slot is rewritten only
+ * after the steps that read it are over, so the host never waits for the
+ * device (except when all 64 entries of the pool's slot-index ring are still
+ * in flight).  Host memory should be pinned (hipHostMalloc) for the copies to
+ * overlap compute.  One host thread drives a pool; its slot memory is the
+ * caller's (n_slots * wm_pool_slot_bytes, 256-byte aligned, device memory). */
+typedef struct wm_expert_pool wm_expert_pool;
+int64_t wm_pool_slot_bytes(int64_t gate_bytes, int64_t up_bytes, int64_t down_bytes);
+int wm_pool_create(void* slots, int64_t slots_bytes, int n_slots, int64_t gate_bytes, int64_t up_bytes,
+                   int64_t down_bytes, wm_expert_pool** pool);
+int wm_pool_destroy(wm_expert_pool* pool);
+/* The pool as a layer's expert tensors: sets gate_exps / up_exps / down_exps
+ * and their strides to the slots and n_experts to n_slots; a step on it takes
+ * slot indices as expert ids (wm_moe_decode_forced). */
+int wm_pool_layer(const wm_expert_pool* pool, wm_layer_desc* d);
+/* Makes experts ids[0..n) of `layer` (n <= n_slots) resident for the next
+ * steps on `stream`: a resident expert is a hit; a missing one goes to a free
+ * slot, else to the least recently used slot that no unreleased acquire
+ * holds, copied from gate_src + id * gate_stride (up, down alike).  Writes,
+ * in stream order, the slot of each id to slots_dev (device int32 [n]): the
+ * ids to pass to wm_moe_decode_forced on the pool's layer.  Returns the
+ * number of misses; WM_EINVAL for a bad argument or when every slot is held
+ * by unreleased acquires. */
+int wm_pool_acquire(wm_expert_pool* pool, int layer, const int32_t* ids, int n, const void* gate_src,
+                    const void* up_src, const void* down_src, int64_t gate_stride, int64_t up_stride,
+                    int64_t down_stride, int32_t* slots_dev, void* stream);
+/* To be called once the steps that read the slots of the acquires since the
+ * last release are enqueued on `stream`: those slots may then be recycled,
+ * after those steps (the pool's stream waits for them on the device). */
+int wm_pool_release(wm_expert_pool* pool, void* stream);
+/* Hits, misses and bytes copied since the pool was created. */
+int wm_pool_stats(const wm_expert_pool* pool, int64_t* hits, int64_t* misses, int64_t* bytes_copied);
+
 /* ------------------------------------------------------------ profiling */
 /* Per-phase device timers of wm_moe_decode / wm_moe_decode_forced /
  * wm_moe_prefill, the counterpart of the reference's per-phase

@@ -74,6 +74,14 @@ SIGNATURES = {
     "wm_noalloc_scratch_bytes": (_i64, []),
     "wm_moe_decode_noalloc": (C.c_int, [C.POINTER(LayerDesc), _vp, _vp, _vp, _vp, _vp]),
     "wm_noalloc_status": (C.c_int, [C.POINTER(C.c_int32)]),
+    "wm_pool_slot_bytes": (_i64, [_i64, _i64, _i64]),
+    "wm_pool_create": (C.c_int, [C.c_void_p, _i64, C.c_int, _i64, _i64, _i64, C.POINTER(C.c_void_p)]),
+    "wm_pool_destroy": (C.c_int, [C.c_void_p]),
+    "wm_pool_layer": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "wm_pool_acquire": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_int32), C.c_int, C.c_void_p, C.c_void_p,
+                                  C.c_void_p, _i64, _i64, _i64, C.c_void_p, C.c_void_p]),
+    "wm_pool_release": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "wm_pool_stats": (C.c_int, [C.c_void_p, C.POINTER(_i64), C.POINTER(_i64), C.POINTER(_i64)]),
     "wm_prefill_workspace_size": (_i64, [C.POINTER(LayerDesc), C.c_int]),
     "wm_moe_prefill": (C.c_int, [C.POINTER(LayerDesc), _vp, C.c_int, _vp, _vp, _i64, C.c_int, _vp]),
     "wm_moe_prefill_forced": (C.c_int, [C.POINTER(LayerDesc), _vp, C.c_int, _vp, _vp, _vp, _vp, _i64, C.c_int,

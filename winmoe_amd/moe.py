@@ -19,6 +19,7 @@ import ctypes as C
 from dataclasses import dataclass
 from typing import Optional, Sequence
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -380,3 +381,79 @@ class MoELayer:
         v = C.c_int32()
         check(load().wm_workspace_status(_p(self.ws), self.ws.numel(), C.byref(v)), "wm_workspace_status")
         return v.value
+
+
+class ExpertPool:
+    """Host -> HBM expert streaming (include/winmoe_hip.h, wm_pool_*): ``n_slots``
+    expert slots in HBM filled on demand from host memory, for models whose
+    experts do not all fit there (the reference's miss path,
+    winmoe_inference.c:1736-1789, and GPU cache upload,
+    gpu_offload.cu:590-659).  ``layer(...)`` builds a MoELayer whose expert
+    tensors are the slots; a step on it runs ``decode_forced`` with the slot
+    indices ``acquire`` returns.  Host tensors should be pinned
+    (``pin_memory=True``) for the copies to overlap compute."""
+
+    def __init__(self, n_slots: int, gate_bytes: int, up_bytes: int, down_bytes: int, device="cuda"):
+        L = load()
+        sb = L.wm_pool_slot_bytes(gate_bytes, up_bytes, down_bytes)
+        if sb < 0:
+            raise ValueError("expert part sizes must be positive")
+        self.n_slots, self.slot_bytes = n_slots, sb
+        self.parts = (gate_bytes, up_bytes, down_bytes)
+        g256 = (gate_bytes + 255) // 256 * 256
+        self.offsets = (0, g256, g256 + (up_bytes + 255) // 256 * 256)
+        self.mem = _ws(n_slots * sb, device)
+        h = C.c_void_p()
+        check(L.wm_pool_create(_p(self.mem), self.mem.numel(), n_slots, gate_bytes, up_bytes, down_bytes,
+                               C.byref(h)), "wm_pool_create")
+        self._h = h
+        self.slots = torch.zeros(n_slots, dtype=torch.int32, device=device)
+
+    def layer(self, H: int, I: int, K: int, types: Sequence[int], shared: Optional[SharedExpert] = None,
+              max_tokens: int = 256, **kw) -> "MoELayer":
+        """A layer whose routed experts are the pool's slots (no router: its
+        steps take slot indices through ``decode_forced``)."""
+        views = [self.mem[o:] for o in self.offsets]
+        return MoELayer(H, I, self.n_slots, K, None, views[0], views[1], views[2], types, shared=shared,
+                        max_tokens=max_tokens, strides=(self.slot_bytes,) * 3, **kw)
+
+    def acquire(self, layer: int, ids, gate_src: torch.Tensor, up_src: torch.Tensor, down_src: torch.Tensor,
+                out: Optional[torch.Tensor] = None, stream=None):
+        """Makes experts ``ids`` of ``layer`` resident (copies the missing ones
+        from the host tensors ``*_src`` [E][bytes]); returns (slots, misses):
+        the device int32 slot indices, written in stream order, and the miss
+        count."""
+        ids = np.ascontiguousarray(np.asarray(ids, dtype=np.int32).reshape(-1))
+        for t, n in ((gate_src, "gate_src"), (up_src, "up_src"), (down_src, "down_src")):
+            if t.device.type != "cpu" or t.dtype != torch.uint8 or t.dim() != 2 or not t.is_contiguous():
+                raise ValueError(f"{n} must be a contiguous uint8 host tensor [E][bytes]")
+        if out is None:
+            out = torch.empty(ids.size, dtype=torch.int32, device=self.mem.device)
+        rc = load().wm_pool_acquire(self._h, layer, ids.ctypes.data_as(C.POINTER(C.c_int32)), ids.size,
+                                    gate_src.data_ptr(), up_src.data_ptr(), down_src.data_ptr(),
+                                    gate_src.stride(0), up_src.stride(0), down_src.stride(0), _p(out),
+                                    _stream(stream))
+        if rc < 0:
+            check(rc, "wm_pool_acquire")
+        return out, rc
+
+    def release(self, stream=None) -> None:
+        """After the steps that read the acquired slots are enqueued on ``stream``."""
+        check(load().wm_pool_release(self._h, _stream(stream)), "wm_pool_release")
+
+    def stats(self):
+        """(hits, misses, bytes copied) since creation."""
+        h, m, b = C.c_int64(), C.c_int64(), C.c_int64()
+        check(load().wm_pool_stats(self._h, C.byref(h), C.byref(m), C.byref(b)), "wm_pool_stats")
+        return h.value, m.value, b.value
+
+    def close(self) -> None:
+        if self._h:
+            load().wm_pool_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
