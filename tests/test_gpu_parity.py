@@ -418,6 +418,21 @@ def test_prefill_rejects_unsupported_widths(wm):
     assert ei.value.rc == wm._lib.WM_EINVAL
 
 
+@pytest.mark.parametrize("types", [(Q6_K, Q6_K, Q8_0), (Q4_K, Q5_K, Q6_K)])
+def test_prefill_rejects_unsupported_formats(wm, types):
+    """Prefill refuses Q6_K gate/up matrices and gate and up of different
+    formats (WM_EINVAL, nothing launched); decode takes both."""
+    from winmoe_amd import synth
+    cfg = synth.LayerConfig("pf_fmt", E=8, K=2, H=512, I=256, types=types, tokens=1, x_dtype="bf16", seed=5)
+    sl = synth.build_layer(cfg, max_tokens=4)
+    X = synth.make_hidden(cfg, tokens=4)
+    case(f"prefill refuses types={types}")
+    with pytest.raises(wm.WinMoEError) as ei:
+        sl.layer.prefill(X)
+    assert ei.value.rc == wm._lib.WM_EINVAL
+    assert np.isfinite(host(sl.layer.decode(X[0].float()))).all()
+
+
 def test_prefill_forced_multi_pass_and_bad_ids(wm, orc):
     """Caller routing: one expert used by every token (three 32-pair passes),
     one invalid id (skipped, reported)."""
@@ -464,6 +479,86 @@ def test_prefill_c5_full(wm, orc):
         od = host(sl.layer.decode_forced(X[t].float(), dev(ids[t]), dev(w[t])))
         worst = max(worst, rel_l2(out[t], od))
     assert worst <= 1e-4, worst
+    assert sl.layer.prefill_status() == 0
+
+
+# K-quant experts in prefill: (gate = up, down) routed, shared or None, H.
+# Routed and shared experts of different formats run as separate GEMM
+# launches; H = 256 takes the two-block down items, 1024 the four-block ones.
+KQ_PREFILL = [
+    ((Q4_K, Q6_K), (Q8_0, Q8_0), 1024),
+    ((Q2_K, Q3_K), None, 256),
+    ((Q5_K, Q5_K), (Q5_K, Q6_K), 1024),
+    ((Q3_K, Q2_K), (Q4_K, Q4_K), 256),
+    ((Q8_0, Q6_K), (Q2_K, Q8_0), 1024),
+    ((Q4_K, Q4_K), (Q3_K, Q5_K), 256),
+]
+
+
+def _kq_routes(T, E, K, rng):
+    """Every token uses expert 0 (passes of 32 + 32 + rest rows: both row
+    tiles); the other slots are distinct random experts."""
+    ids = np.zeros((T, K), np.int32)
+    for t in range(T):
+        ids[t, 1:] = rng.choice(np.arange(1, E), K - 1, replace=False)
+    w = rng.random((T, K)).astype(np.float32)
+    return ids, w
+
+
+@pytest.mark.parametrize("gu,dn,sh,H", [(g, d, s, h) for (g, d), s, h in KQ_PREFILL],
+                         ids=[f"{g}-{d}-{s}-h{h}" for (g, d), s, h in KQ_PREFILL])
+def test_prefill_kquant_matches_oracle(wm, orc, gu, dn, sh, H):
+    """Prefill with K-quant expert matrices (and a shared expert of another
+    format) == the oracle token by token, with a 70-token batch whose
+    expert 0 takes three passes."""
+    from winmoe_amd import synth
+    E, K, I, T = 24, 3, 512, 70
+    cfg = synth.LayerConfig(f"pf_kq_{gu}_{dn}", E=E, K=K, H=H, I=I, types=(gu, gu, dn),
+                            shared_types=(sh[0], sh[0], sh[1]) if sh else None, shared_inter=256 if sh else 0,
+                            shared_gate_inp=sh is not None, tokens=1, routing="zipf", x_dtype="bf16", seed=13 + gu)
+    sl = synth.build_layer(cfg, max_tokens=T)
+    X = synth.make_hidden(cfg, tokens=T)
+    ids, w = _kq_routes(T, E, K, np.random.default_rng(gu * 31 + dn))
+    case(f"prefill kq gate/up={gu} down={dn} shared={sh} H={H} T={T}")
+    out = host(sl.layer.prefill_forced(X, dev(ids), dev(w)))
+    worst = 0.0
+    for t in range(T):
+        _, _, ref = oracle_token(orc, sl, host(X[t].float()), ids=ids[t], w=w[t])
+        worst = max(worst, rel_l2(out[t], ref))
+    print(f"worst rel-L2 vs oracle {worst:.3e}", flush=True)
+    assert worst <= LAYER_TOL, worst
+    assert sl.layer.prefill_status() == 0
+
+
+@pytest.mark.parametrize("name", ["c3", "c4"])
+def test_prefill_kquant_full_layer(wm, orc, name):
+    """A 512-token prefill through the full 512-expert layer of the Q4_K /
+    Q6_K (shared Q8_0) and the Q2_K / Q3_K workloads with Zipf routing: a
+    sample of tokens against the oracle, every token against the decode path
+    with the same routing, and a second call bit-identical to the first."""
+    import dataclasses
+    from winmoe_amd import synth
+    cfg = dataclasses.replace(synth.CONFIGS[name], tokens=512, routing="zipf", n_layers=1, x_dtype="bf16")
+    T = cfg.tokens
+    sl = synth.build_layer(cfg, max_tokens=T)
+    X = synth.make_hidden(cfg)
+    ids, w = synth.forced_routes(cfg)
+    case(f"prefill {name} full")
+    out = host(sl.layer.prefill_forced(X, dev(ids), dev(w)))
+    again = host(sl.layer.prefill_forced(X, dev(ids), dev(w)))
+    assert np.isfinite(out).all()
+    assert np.array_equal(out.view(np.uint32), again.view(np.uint32))
+    for t in (0, 1, 255, T - 1):
+        case(f"prefill {name} oracle token={t}")
+        _, _, ref = oracle_token(orc, sl, host(X[t].float()), ids=ids[t], w=w[t])
+        assert rel_l2(out[t], ref) <= LAYER_TOL, (t, rel_l2(out[t], ref))
+    case(f"prefill {name} vs decode, all tokens")
+    worst = 0.0
+    for t in range(T):
+        od = host(sl.layer.decode_forced(X[t].float(), dev(ids[t]), dev(w[t])))
+        worst = max(worst, rel_l2(out[t], od))
+    print(f"worst rel-L2 vs decode {worst:.3e}", flush=True)
+    assert worst <= 2e-4, worst
     assert sl.layer.prefill_status() == 0
 
 

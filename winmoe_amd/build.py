@@ -16,7 +16,7 @@ CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libwinmoe_hip.so")
 OBJ_DIR = os.path.join(PKG, "_build")
 SOURCES = ["wm_kernels.hip", "wm_decode.hip", "wm_persist.hip", "wm_capi.hip", "wm_shims.hip", "wm_static.hip", "wm_prefill.hip",
-           "wm_stream.hip"]
+           "wm_prefill_kq.hip", "wm_stream.hip"]
 ARCH = os.environ.get("WINMOE_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [

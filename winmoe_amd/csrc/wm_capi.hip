@@ -850,11 +850,14 @@ static int run_prefill(const wm_layer_desc* d, const uint16_t* x, int T, const i
     PfLayout L = pf_layout(d, max_tokens);
     WM_CHECK_ARG(ws_bytes >= L.total);
     const bool sh = has_shared(d);
-    const bool q8 = d->gate_type == Q8_0 && d->up_type == Q8_0 && d->down_type == Q8_0 &&
-                    (!sh || (d->sh_gate_type == Q8_0 && d->sh_up_type == Q8_0 && d->sh_down_type == Q8_0));
+    const bool types = d->gate_type == d->up_type && prefill_gateup_type(d->gate_type) &&
+                       prefill_down_type(d->down_type) &&
+                       (!sh || (d->sh_gate_type == d->sh_up_type && prefill_gateup_type(d->sh_gate_type) &&
+                                prefill_down_type(d->sh_down_type)));
     const bool shapes = d->hidden % 256 == 0 && d->inter % 256 == 0 && (!sh || Ishared(d) % 256 == 0);
-    if (!q8 || !shapes) {
-        fprintf(stderr, "winmoe_hip: prefill needs Q8_0 expert matrices and H, I multiples of 256\n");
+    if (!types || !shapes) {
+        fprintf(stderr, "winmoe_hip: prefill needs gate and up of one format among Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, "
+                        "down among those or Q6_K, and H, I multiples of 256\n");
         return WM_EINVAL;
     }
     if (wm_init()) return WM_ERR;
@@ -863,6 +866,8 @@ static int run_prefill(const wm_layer_desc* d, const uint16_t* x, int T, const i
     PrefillArgs a = {};
     a.H = d->hidden; a.I = d->inter; a.Is = Ishared(d); a.E = d->n_experts; a.K = d->top_k; a.T = T;
     a.has_shared = sh ? 1 : 0;
+    a.gt = d->gate_type; a.dt = d->down_type;
+    a.sgt = sh ? d->sh_gate_type : a.gt; a.sdt = sh ? d->sh_down_type : a.dt;
     a.x = x; a.router = d->router;
     a.gate = (const uint8_t*)d->gate_exps; a.up = (const uint8_t*)d->up_exps; a.down = (const uint8_t*)d->down_exps;
     a.gstride = d->gate_stride ? d->gate_stride : matrix_bytes(d->gate_type, d->inter, d->hidden);

@@ -20,7 +20,7 @@ namespace wm {
 
 enum QType : int { F32 = 0, F16 = 1, Q8_0 = 8, Q2_K = 10, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14 };
 
-WM_HD int block_bytes(int t) {
+WM_HD constexpr int block_bytes(int t) {
     switch (t) {
     case Q8_0: return 34;
     case Q2_K: return 84;
@@ -32,7 +32,7 @@ WM_HD int block_bytes(int t) {
     }
 }
 
-WM_HD int block_elems(int t) {
+WM_HD constexpr int block_elems(int t) {
     switch (t) {
     case Q8_0: return 32;
     case Q2_K: case Q3_K: case Q4_K: case Q5_K: case Q6_K: return 256;

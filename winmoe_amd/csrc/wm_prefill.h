@@ -4,12 +4,15 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "wm_format.h"
+
 namespace wm {
 
 // A (token, slot) pair p = t * K + k is one routed use of an expert; pair
 // T * K + t is token t's use of the shared expert.
 struct PrefillArgs {
     int32_t H, I, Is, E, K, T, has_shared;
+    int32_t gt, dt, sgt, sdt;   // weight formats: routed gate = up, down; shared gate = up, down
     const uint16_t* x;          // bf16 [T][H]
     const float* router;        // fp32 [E][H]
     const uint8_t* gate;
@@ -44,8 +47,13 @@ struct PrefillArgs {
 // Pass records a prefill of T tokens may need.
 inline int64_t prefill_max_passes(int64_t T, int64_t K, int64_t E) { return (T * K + 31) / 32 + E + (T + 31) / 32 + 1; }
 
-// The phases of a prefill, stream-ordered (the caller checks types: Q8_0
-// expert matrices, H, I, Is multiples of 256, expert strides multiples of 16):
+// Weight formats the expert GEMMs read: gate and up (one format for both) and down.
+inline bool prefill_gateup_type(int t) { return t == Q8_0 || t == Q2_K || t == Q3_K || t == Q4_K || t == Q5_K; }
+inline bool prefill_down_type(int t) { return prefill_gateup_type(t) || t == Q6_K; }
+
+// The phases of a prefill, stream-ordered (the caller checks types: gate and
+// up of one format, formats the GEMMs read, H, I, Is multiples of 256, expert
+// strides multiples of 16):
 //   routing: router + top-K, or the caller's ids / weights; grouping; shared
 //   gate; fp16 copy of x
 //   gate/up + SwiGLU, down projection, combine.

@@ -1,0 +1,35 @@
+// wm_prefill_kq.hip -- the K-quant instances of the prefill expert GEMMs
+// (wm_pf_gemm.h), in a translation unit of their own so that they build in
+// parallel with the rest.
+#include <hip/hip_runtime.h>
+
+#include "wm_pf_gemm.h"
+
+namespace wm {
+
+template <int WT> static int launch_down(int nsub, const PfGemm& g, int n_wg, hipStream_t s) {
+    return nsub == 4 ? launch_pf_gemm<1, 2, 4, WT>(g, n_wg, s) : launch_pf_gemm<1, 2, 2, WT>(g, n_wg, s);
+}
+
+int launch_pf_gemm_kq(int nmat, int nsub, int wt, const PfGemm& g, int n_wg, hipStream_t s) {
+    if (nmat == 2) {
+        switch (wt) {
+        case Q2_K: return launch_pf_gemm<2, 1, 1, Q2_K>(g, n_wg, s);
+        case Q3_K: return launch_pf_gemm<2, 1, 1, Q3_K>(g, n_wg, s);
+        case Q4_K: return launch_pf_gemm<2, 1, 1, Q4_K>(g, n_wg, s);
+        case Q5_K: return launch_pf_gemm<2, 1, 1, Q5_K>(g, n_wg, s);
+        default: return (int)hipErrorInvalidValue;
+        }
+    }
+    if (nmat != 1 || (nsub != 2 && nsub != 4)) return (int)hipErrorInvalidValue;
+    switch (wt) {
+    case Q2_K: return launch_down<Q2_K>(nsub, g, n_wg, s);
+    case Q3_K: return launch_down<Q3_K>(nsub, g, n_wg, s);
+    case Q4_K: return launch_down<Q4_K>(nsub, g, n_wg, s);
+    case Q5_K: return launch_down<Q5_K>(nsub, g, n_wg, s);
+    case Q6_K: return launch_down<Q6_K>(nsub, g, n_wg, s);
+    default: return (int)hipErrorInvalidValue;
+    }
+}
+
+}  // namespace wm
