@@ -18,6 +18,8 @@ own roofline and CPU baseline:
       overlap, 512 decode tokens (a step = one token through all 8 layers)
   c5  prefill of 512 bf16 tokens through the 512-expert top-10 Q8_0 layer,
       Zipf routing (a step = the whole batch)
+  c3p prefill of 512 bf16 tokens through the c3 layer (Q4_K gate/up, Q6_K
+      down, Q8_0 shared expert), Zipf routing
 
 ``--only`` measures the chosen --config alone (used under the profiler).
 """
@@ -93,14 +95,31 @@ def prefill_bytes(cfg, ids) -> int:
 
 
 def prefill_gateup_bytes(cfg, ids) -> int:
-    """The prefill gate/up launch: gate and up of every expert touched, x rows
-    read once, SwiGLU rows written."""
+    """The prefill gate/up phase: gate and up of every expert touched and of
+    the shared expert, x rows read once, SwiGLU rows written (fp16 hi + lo)."""
     from winmoe_amd.moe import matrix_bytes
     gt, ut, _ = cfg.types
     uniq = len(np.unique(ids[(ids >= 0) & (ids < cfg.E)]))
     b = uniq * (matrix_bytes(gt, cfg.I, cfg.H) + matrix_bytes(ut, cfg.I, cfg.H))
     b += cfg.tokens * cfg.H * 2 + ids.size * cfg.I * 4
+    if cfg.shared_types:
+        sgt, sut, _ = cfg.shared_types
+        Is = cfg.shared_inter or cfg.I
+        b += matrix_bytes(sgt, Is, cfg.H) + matrix_bytes(sut, Is, cfg.H) + cfg.tokens * Is * 4
     return b
+
+
+def prefill_gateup_kernel(cfg) -> str:
+    """What the prefill gate/up phase launches for the workload's formats."""
+    from winmoe_amd import TYPE_NAMES
+    gt = TYPE_NAMES[cfg.types[0]]
+    sgt = TYPE_NAMES[cfg.shared_types[0]] if cfg.shared_types else gt
+    what = ("fp16 MFMA over Q8_0 blocks" if gt == "Q8_0" else
+            f"fp16 MFMA over {gt} super-blocks, mins from activation sums")
+    if sgt == gt:
+        return f"k_pf_gemm<2,1,1,{gt}> (prefill gate+up+SwiGLU: {what}, LDS-DMA ring)"
+    return (f"k_pf_gemm<2,1,1,{gt}> + k_pf_gemm<2,1,1,{sgt}> (prefill gate+up+SwiGLU phase: routed {gt} "
+            f"launch and shared-expert {sgt} launch; {what})")
 
 
 def committed_traffic(kernel, workload):
@@ -260,8 +279,8 @@ def entry(wl, L, steps, warmup, multi_kernel=False):
     rl = None
     if wl.prefill and "gate_up_swiglu" in phases:
         gu = phases["gate_up_swiglu"]
-        rl = roofline("k_pf_gemm<2,1,1> (prefill gate+up+SwiGLU: fp16 MFMA over Q8_0 blocks, LDS-DMA ring)",
-                      "k_pf_gemm", cfg.name, prefill_gateup_bytes(cfg, wl.routes[0][0]), gu["avg_us"])
+        rl = roofline(prefill_gateup_kernel(cfg), "k_pf_gemm", cfg.name, prefill_gateup_bytes(cfg, wl.routes[0][0]),
+                      gu["avg_us"])
     elif not wl.prefill and not multi_kernel:
         # one fused launch per layer per token moves the step's bytes; its
         # average duration is the timed region's event time over the launches
@@ -376,8 +395,8 @@ def cpu_baseline(wl, n_sample):
 
 # ------------------------------------------------------------------ main
 
-EXTRA = ["c1", "c3", "c4", "c5"]
-CPU_SAMPLE = {"c1": 1, "c2": 16, "c3": 16, "c4": 4, "c5": 8}
+EXTRA = ["c1", "c3", "c4", "c5", "c3p"]
+CPU_SAMPLE = {"c1": 1, "c2": 16, "c3": 16, "c4": 4, "c5": 8, "c3p": 16}
 
 
 # marks of the persistent step's per-workgroup timeline (include/winmoe_hip.h, wm_workspace_timeline)
@@ -516,7 +535,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2048)
     ap.add_argument("--warmup", type=int, default=64)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c3p"])
     ap.add_argument("--only", action="store_true", help="measure --config alone (no `configs` object)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--multi-kernel", action="store_true",
@@ -579,7 +598,7 @@ def main():
                        "batch": cfg.tokens if wl.prefill else 1, "distinct_tokens": cfg.tokens,
                        "path": "prefill" if wl.prefill else ("multi-kernel" if args.multi_kernel and headline
                                                              else "fused")}
-        e["dtype"] = ("fp16 MFMA (int8 weights exact in fp16, x fp16 per-token scaled, SwiGLU output fp16 hi+lo) "
+        e["dtype"] = ("fp16 MFMA (quantised weights exact in fp16, x fp16 per-token scaled, SwiGLU output fp16 hi+lo) "
                       "-> fp32" if wl.prefill else
                       "int8 dot (quantised weights x int8 activation digits) -> int32, fp32 scales/accumulation")
         del wl

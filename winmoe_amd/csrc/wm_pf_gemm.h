@@ -79,6 +79,10 @@ constexpr int GM_CW = 8;              // compute waves
 constexpr int GM_THREADS = 64 * (GM_CW + 1);
 constexpr int GM_DESC = 8;            // pass records held in LDS
 
+// Columns per stage of format WT (the launcher's column-step count is
+// the matrix width over this).
+constexpr int gm_kc(int wt) { return wt == Q8_0 ? 128 : 256; }
+
 // Granules of 16 B that hold a row's stage chunk of format WT wherever it starts.
 constexpr int gm_granules(int wt) {
     return wt == Q8_0 ? 9 : wt == Q4_K ? 9 : wt == Q5_K ? 11 : wt == Q2_K ? 7 : wt == Q3_K ? 9 : 15;
@@ -86,14 +90,13 @@ constexpr int gm_granules(int wt) {
 
 template <int NMAT, int AHL, int NSUB, int WT> struct GmGeo {
     static constexpr bool KQ = WT != Q8_0;
-    static constexpr int KC = KQ ? 256 : 128;                          // columns per stage
+    static constexpr int KC = gm_kc(WT);                                // columns per stage
     static constexpr int CHUNK = KQ ? block_bytes(WT) : 136;             // bytes of a row's stage chunk
     static constexpr int GR = gm_granules(WT);
     static constexpr int RSLOT = 16 * GR;                               // LDS bytes of a row's chunk
     static constexpr int GPR = KC / 8 + 1;                              // activation granules per row (+ pad)
     static constexpr int ALD = 16 * GPR;
     static constexpr int NAU = (GM_M * GPR + 63) / 64;                  // DMA units per activation array
-    static constexpr int A16 = (16 * GPR + 63) / 64;                    // units holding rows 0-15
     static constexpr int APART = NAU * 1024;
     static constexpr int S = KQ ? 2 : (NMAT == 2 ? 3 : 5);              // weight ring stages
     static constexpr int W_BYTES = NMAT * GM_ROWS * RSLOT;
@@ -239,68 +242,104 @@ template <int AL> WM_DEV uint32_t ld_u32(const uint8_t* slot, int o) {
     return alignbyte(p[1], p[0], (uint32_t)o & 3u);
 }
 
-// A K-quant super-block of one weight row in LDS (slot + o: its first byte).
-// head() reads the scales once per stage; unit(b) gives the 8 values of
-// columns 32b + 8g .. 32b + 8g + 7 as fp16 (minus the format's bias) and the
-// multipliers am[h] and mins mm[h] of the unit's sub-block(s): h = 0 for
-// columns 32b + [0,16) (or the whole unit when HALVES = 1), h = 1 for
-// 32b + [16,32).  Dequantised weight = am * v - mm.
+// {s, s} as fp16 for the unsigned byte of w that perm selector sel picks
+// (sel: the byte index in bytes 0 and 2, 4 in bytes 1 and 3), minus BIAS.
+template <int BIAS> WM_DEV f16x2 byte_f16x2(uint32_t w, uint32_t sel) {
+    const f16x2 bias = {(_Float16)(1024.0f + BIAS), (_Float16)(1024.0f + BIAS)};
+    return __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w, sel)) - bias;
+}
+WM_HD constexpr uint32_t byte_sel(uint32_t p) { return p | (p << 16) | 0x04000400u; }
+
+// fma(x, s, c) on four fp16 pairs (one rounding each)
+WM_DEV f16x8 f16x8_fma(f16x8 x, f16x2 s, f16x2 c) {
+    const f16x8 s8 = {s[0], s[1], s[0], s[1], s[0], s[1], s[0], s[1]};
+    const f16x8 c8 = {c[0], c[1], c[0], c[1], c[0], c[1], c[0], c[1]};
+    return __builtin_elementwise_fma(x, s8, c8);
+}
+WM_DEV f16x8 f16x8_rep(f16x2 v) { return (f16x8){v[0], v[1], v[0], v[1], v[0], v[1], v[0], v[1]}; }
+
+// 8 unsigned integers below 256, one per byte of (d0, d1), as 1024 + value in fp16.
+WM_DEV f16x8 u8_h1024(uint32_t d0, uint32_t d1) {
+    const uint32_t K = 0x64646464u;
+    return __builtin_bit_cast(f16x8, (u32x4){__builtin_amdgcn_perm(K, d0, 0x04010400u), __builtin_amdgcn_perm(K, d0, 0x04030402u),
+                                             __builtin_amdgcn_perm(K, d1, 0x04010400u), __builtin_amdgcn_perm(K, d1, 0x04030402u)});
+}
+
+// A K-quant super-block of one weight row in LDS (slot + o: its first byte);
+// unit b = columns 32b .. 32b + 31, of which this lane holds 32b + 8g .. + 7
+// (one sub-block: the 32-weight sub-block b, or the 16-weight sub-block
+// 2b + g / 2).  head() reads the block's scales once per stage.
+//
+// FOLD formats (q times its sub-block scale is an integer fp16 holds
+// exactly: Q4_K <= 15*63, Q5_K <= 31*63, Q3_K <= 4*32, Q2_K <= 3*15):
+// unit(b) gives Bq = q * sc and Bm = the sub-block min m, and the weight is
+// d * Bq - dmin * Bm with the block's d, dmin.
+// Q6_K (|q * sc| up to 32*128) unit(b) gives the values q and the
+// multipliers am[h] = d * sc of the unit's two 16-weight sub-blocks (h = 0:
+// columns 32b + [0,16)), applied after the MFMA.
 template <int WT> struct KqRow;
 
-template <> struct KqRow<Q4_K> {                 // q4k_dequant.h:28-33, 112-168
-    static constexpr int HALVES = 1, AL = 16;
-    static constexpr bool MINS = true;
+template <> struct KqRow<Q4_K> {                 // q4k_dequant.h:28-33, 43-60, 112-168
+    static constexpr int AL = 16;
+    static constexpr bool FOLD = true, MINS = true;
     float d, dmin;
-    uint32_t s0, s1, s2;
+    uint32_t sc[2], mn[2];                       // 6-bit scales and mins of sub-blocks 0-3, 4-7 (a byte each)
     WM_DEV void head(const uint8_t* slot, int o) {
         const uint4 h = *(const uint4*)(slot + o);
         d = h2f(h.x);
         dmin = h2f(h.x >> 16);
-        s0 = h.y; s1 = h.z; s2 = h.w;
+        sc[0] = h.y & 0x3F3F3F3Fu;
+        mn[0] = h.z & 0x3F3F3F3Fu;
+        sc[1] = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+        mn[1] = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
     }
     // sub-block b: qs bytes 32 (b / 2) + l, low nibble for even b, high for odd
-    WM_DEV f16x8 unit(const uint8_t* slot, int o, int b, int g, float* am, float* mm) const {
+    WM_DEV void unit(const uint8_t* slot, int o, int b, int g, f16x8& Bq, f16x8& Bm) const {
         uint32_t w0, w1;
         ld_u32x2<AL>(slot, o + 16 + 32 * (b >> 1) + 8 * g, w0, w1);
         const int sh = 4 * (b & 1);
-        int sc, m;
-        k45_scale_min(s0, s1, s2, b, sc, m);
-        am[0] = d * (float)sc;
-        mm[0] = dmin * (float)m;
-        return u8_f16x8<0>((w0 >> sh) & 0x0F0F0F0Fu, (w1 >> sh) & 0x0F0F0F0Fu);
+        const uint32_t scw = b >= 4 ? sc[1] : sc[0], mnw = b >= 4 ? mn[1] : mn[0];
+        const f16x2 s2 = byte_f16x2<0>(scw, byte_sel(b & 3));
+        const f16x2 c2 = s2 * (f16x2){(_Float16)-1024.0f, (_Float16)-1024.0f};
+        // (1024 + q) * sc - 1024 * sc, one rounding of the exact integer q * sc
+        Bq = f16x8_fma(u8_h1024((w0 >> sh) & 0x0F0F0F0Fu, (w1 >> sh) & 0x0F0F0F0Fu), s2, c2);
+        Bm = f16x8_rep(byte_f16x2<0>(mnw, byte_sel(b & 3)));
     }
 };
 
 template <> struct KqRow<Q5_K> {                 // q5k_dequant.h:19-25, 98-131
-    static constexpr int HALVES = 1, AL = 16;
-    static constexpr bool MINS = true;
+    static constexpr int AL = 16;
+    static constexpr bool FOLD = true, MINS = true;
     float d, dmin;
-    uint32_t s0, s1, s2;
+    uint32_t sc[2], mn[2];
     WM_DEV void head(const uint8_t* slot, int o) {
         const uint4 h = *(const uint4*)(slot + o);
         d = h2f(h.x);
         dmin = h2f(h.x >> 16);
-        s0 = h.y; s1 = h.z; s2 = h.w;
+        sc[0] = h.y & 0x3F3F3F3Fu;
+        mn[0] = h.z & 0x3F3F3F3Fu;
+        sc[1] = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+        mn[1] = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
     }
     // sub-block b: nibble as Q4_K (qs at 48), fifth bit = bit b of qh[l] (qh at 16)
-    WM_DEV f16x8 unit(const uint8_t* slot, int o, int b, int g, float* am, float* mm) const {
+    WM_DEV void unit(const uint8_t* slot, int o, int b, int g, f16x8& Bq, f16x8& Bm) const {
         uint32_t w0, w1, e0, e1;
         ld_u32x2<AL>(slot, o + 48 + 32 * (b >> 1) + 8 * g, w0, w1);
         ld_u32x2<AL>(slot, o + 16 + 8 * g, e0, e1);
         const int sh = 4 * (b & 1);
-        int sc, m;
-        k45_scale_min(s0, s1, s2, b, sc, m);
-        am[0] = d * (float)sc;
-        mm[0] = dmin * (float)m;
-        return u8_f16x8<0>(((w0 >> sh) & 0x0F0F0F0Fu) | (((e0 >> b) & 0x01010101u) << 4),
-                           ((w1 >> sh) & 0x0F0F0F0Fu) | (((e1 >> b) & 0x01010101u) << 4));
+        const f16x2 s2 = byte_f16x2<0>(sc[b >> 2], byte_sel(b & 3));
+        const f16x8 q = u8_f16x8<0>(((w0 >> sh) & 0x0F0F0F0Fu) | (((e0 >> b) & 0x01010101u) << 4),
+                                    ((w1 >> sh) & 0x0F0F0F0Fu) | (((e1 >> b) & 0x01010101u) << 4));
+        Bq = q * f16x8_rep(s2);                  // exact: q * sc <= 1953
+        Bm = f16x8_rep(byte_f16x2<0>(mn[b >> 2], byte_sel(b & 3)));
     }
 };
 
-// Column 128 h + 32 j + l of the 16-weight sub-block formats: unit b = 4 h + j.
+// Column 128 h + 32 j + l of the 16-weight sub-block formats: unit b = 4 h + j,
+// sub-block 8 h + 2 j + l / 16 (l / 16 = g / 2 for this lane).
 template <> struct KqRow<Q6_K> {                 // q6k_dequant.h:20-25, 112-141
-    static constexpr int HALVES = 2, AL = 2;
-    static constexpr bool MINS = false;
+    static constexpr int AL = 2;
+    static constexpr bool FOLD = false, MINS = false;
     float d;
     uint32_t sc[4];                              // int8 scales[16]
     WM_DEV void head(const uint8_t* slot, int o) {
@@ -308,82 +347,95 @@ template <> struct KqRow<Q6_K> {                 // q6k_dequant.h:20-25, 112-141
         ld_u32x2<AL>(slot, o + 200, sc[2], sc[3]);
         d = h2f(*(const uint16_t*)(slot + o + 208));
     }
-    // ql[64 h + 32 (j & 1) + l] (low nibble for j < 2), qh[32 h + l] bits 2j,
-    // 2j+1; value q - 32; scale 8 h + 2 j + l / 16
-    WM_DEV f16x8 unit(const uint8_t* slot, int o, int b, int g, float* am, float* mm) const {
-        const int h = b >> 2, j = b & 3;
-        uint32_t w0, w1, e0, e1;
-        ld_u32x2<AL>(slot, o + 64 * h + 32 * (j & 1) + 8 * g, w0, w1);
-        ld_u32x2<AL>(slot, o + 128 + 32 * h + 8 * g, e0, e1);
+    // The bytes of half h this lane's units read: ql[64 h + 8g ..] (units
+    // j = 0, 2: low, high nibble), ql[64 h + 32 + 8g ..] (j = 1, 3), qh[32 h + 8g ..]
+    // (bits 2j, 2j+1 for unit j).
+    uint32_t ql[2][2], qh[2];
+    WM_DEV void half(const uint8_t* slot, int o, int h, int g) {
+        ld_u32x2<AL>(slot, o + 64 * h + 8 * g, ql[0][0], ql[0][1]);
+        ld_u32x2<AL>(slot, o + 64 * h + 32 + 8 * g, ql[1][0], ql[1][1]);
+        ld_u32x2<AL>(slot, o + 128 + 32 * h + 8 * g, qh[0], qh[1]);
+    }
+    // unit 4 h + j of the loaded half: values q - 32, multipliers of
+    // sub-blocks 8 h + 2 j and 8 h + 2 j + 1
+    WM_DEV f16x8 unit(int h, int j, float* am) const {
         const int sh = 4 * (j >> 1);
         const int k = 8 * h + 2 * j;
         am[0] = d * (float)(int8_t)byte_of(sc[k >> 2], k & 3);
         am[1] = d * (float)(int8_t)byte_of(sc[(k + 1) >> 2], (k + 1) & 3);
-        mm[0] = mm[1] = 0.0f;
-        return u8_f16x8<32>(((w0 >> sh) & 0x0F0F0F0Fu) | (((e0 >> (2 * j)) & 0x03030303u) << 4),
-                            ((w1 >> sh) & 0x0F0F0F0Fu) | (((e1 >> (2 * j)) & 0x03030303u) << 4));
+        const uint32_t* w = ql[j & 1];
+        return u8_f16x8<32>(((w[0] >> sh) & 0x0F0F0F0Fu) | (((qh[0] >> (2 * j)) & 0x03030303u) << 4),
+                            ((w[1] >> sh) & 0x0F0F0F0Fu) | (((qh[1] >> (2 * j)) & 0x03030303u) << 4));
     }
 };
 
 template <> struct KqRow<Q3_K> {                 // hmask[32] qs[64] scales[12] d
-    static constexpr int HALVES = 2, AL = 2;
-    static constexpr bool MINS = false;
-    float d;
-    uint32_t s0, s1, s2;
+    static constexpr int AL = 2;
+    static constexpr bool FOLD = true, MINS = false;
+    float d, dmin;
+    uint32_t sc[4];                              // sub-blocks 4i .. 4i+3: the 6-bit scale + 32 (a byte each)
     WM_DEV void head(const uint8_t* slot, int o) {
+        uint32_t s0, s1, s2;
         ld_u32x2<AL>(slot, o + 96, s0, s1);
         s2 = ld_u32<AL>(slot, o + 104);
         d = h2f(*(const uint16_t*)(slot + o + 108));
+        dmin = 0.0f;
+        // low 4 bits: bytes 0-7 of the scales (sub-blocks 0-7), their high
+        // nibbles (8-15); high 2 bits: bits 2(k / 4) of byte 8 + k % 4
+        sc[0] = (s0 & 0x0F0F0F0Fu) | ((s2 << 4) & 0x30303030u);
+        sc[1] = (s1 & 0x0F0F0F0Fu) | ((s2 << 2) & 0x30303030u);
+        sc[2] = ((s0 >> 4) & 0x0F0F0F0Fu) | (s2 & 0x30303030u);
+        sc[3] = ((s1 >> 4) & 0x0F0F0F0Fu) | ((s2 >> 2) & 0x30303030u);
     }
     // low bits (qs[32 h + l] >> 2j) & 3, high bit (hmask[l] >> (4h + j)) & 1
-    // (clear: minus 4), i.e. value u - 4; scale 8 h + 2 j + l / 16
-    WM_DEV f16x8 unit(const uint8_t* slot, int o, int b, int g, float* am, float* mm) const {
-        const int h = b >> 2, j = b & 3;
+    // (clear: minus 4), i.e. value u - 4
+    WM_DEV void unit(const uint8_t* slot, int o, int b, int g, f16x8& Bq, f16x8& Bm) const {
+        const int h = b >> 2, j = b & 3, hb = 4 * h + j;
         uint32_t w0, w1, e0, e1;
         ld_u32x2<AL>(slot, o + 32 + 32 * h + 8 * g, w0, w1);
         ld_u32x2<AL>(slot, o + 8 * g, e0, e1);
-        const int k = 8 * h + 2 * j, hb = 4 * h + j;
-        am[0] = d * (float)q3k_scale(s0, s1, s2, k);
-        am[1] = d * (float)q3k_scale(s0, s1, s2, k + 1);
-        mm[0] = mm[1] = 0.0f;
-        return u8_f16x8<4>(((w0 >> (2 * j)) & 0x03030303u) | (((e0 >> hb) & 0x01010101u) << 2),
-                           ((w1 >> (2 * j)) & 0x03030303u) | (((e1 >> hb) & 0x01010101u) << 2));
+        const int k = 8 * h + 2 * j;             // + g / 2
+        const f16x2 s2 = byte_f16x2<32>(sc[k >> 2], byte_sel((uint32_t)((k & 3) + (g >> 1))));
+        const f16x8 q = u8_f16x8<4>(((w0 >> (2 * j)) & 0x03030303u) | (((e0 >> hb) & 0x01010101u) << 2),
+                                    ((w1 >> (2 * j)) & 0x03030303u) | (((e1 >> hb) & 0x01010101u) << 2));
+        Bq = q * f16x8_rep(s2);                  // exact: |q * sc| <= 128
+        Bm = Bq;
     }
 };
 
 template <> struct KqRow<Q2_K> {                 // scales[16] qs[64] d dmin
-    static constexpr int HALVES = 2, AL = 4;
-    static constexpr bool MINS = true;
+    static constexpr int AL = 4;
+    static constexpr bool FOLD = true, MINS = true;
     float d, dmin;
-    uint32_t sc[4];
+    uint32_t sb[4];                              // sub-blocks 4i .. 4i+3: scale (low nibble), min (high)
     WM_DEV void head(const uint8_t* slot, int o) {
-        ld_u32x2<AL>(slot, o, sc[0], sc[1]);
-        ld_u32x2<AL>(slot, o + 8, sc[2], sc[3]);
+        ld_u32x2<AL>(slot, o, sb[0], sb[1]);
+        ld_u32x2<AL>(slot, o + 8, sb[2], sb[3]);
         const uint32_t dd = ld_u32<AL>(slot, o + 80);
         d = h2f(dd);
         dmin = h2f(dd >> 16);
     }
-    // (qs[32 h + l] >> 2j) & 3; scale byte 8 h + 2 j + l / 16: d * (s & 15), min dmin * (s >> 4)
-    WM_DEV f16x8 unit(const uint8_t* slot, int o, int b, int g, float* am, float* mm) const {
+    // (qs[32 h + l] >> 2j) & 3
+    WM_DEV void unit(const uint8_t* slot, int o, int b, int g, f16x8& Bq, f16x8& Bm) const {
         const int h = b >> 2, j = b & 3;
         uint32_t w0, w1;
         ld_u32x2<AL>(slot, o + 16 + 32 * h + 8 * g, w0, w1);
-        const int k = 8 * h + 2 * j;
-        const uint32_t sa = byte_of(sc[k >> 2], k & 3), sb = byte_of(sc[(k + 1) >> 2], (k + 1) & 3);
-        am[0] = d * (float)(sa & 15u);
-        am[1] = d * (float)(sb & 15u);
-        mm[0] = dmin * (float)(sa >> 4);
-        mm[1] = dmin * (float)(sb >> 4);
-        return u8_f16x8<0>((w0 >> (2 * j)) & 0x03030303u, (w1 >> (2 * j)) & 0x03030303u);
+        const int k = 8 * h + 2 * j;             // + g / 2
+        const uint32_t sel = byte_sel((uint32_t)((k & 3) + (g >> 1)));
+        const f16x2 s2 = byte_f16x2<0>(sb[k >> 2] & 0x0F0F0F0Fu, sel);
+        const f16x2 c2 = s2 * (f16x2){(_Float16)-1024.0f, (_Float16)-1024.0f};
+        Bq = f16x8_fma(u8_h1024((w0 >> (2 * j)) & 0x03030303u, (w1 >> (2 * j)) & 0x03030303u), s2, c2);
+        Bm = f16x8_rep(byte_f16x2<0>((sb[k >> 2] >> 4) & 0x0F0F0F0Fu, sel));
     }
 };
 
 // Q8_0 needs no K-quant row decoder; a placeholder keeps the kernel generic.
 template <> struct KqRow<Q8_0> {
-    static constexpr int HALVES = 1, AL = 16;
-    static constexpr bool MINS = false;
+    static constexpr int AL = 16;
+    static constexpr bool FOLD = false, MINS = false;
     WM_DEV void head(const uint8_t*, int) {}
-    WM_DEV f16x8 unit(const uint8_t*, int, int, int, float*, float*) const { return (f16x8){}; }
+    WM_DEV void half(const uint8_t*, int, int, int) {}
+    WM_DEV f16x8 unit(int, int, float*) const { return (f16x8){}; }
 };
 
 // ------------------------------------------------------------------ the kernel
@@ -435,20 +487,11 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
     // Down (NMAT = 1) activations carry a scale per (row, column step);
     // gate/up activations (x) one per token, applied in the epilogue.
     constexpr bool SCALED = NMAT == 1;
-    // DMA instructions of this wave per weight stage, and per activation
-    // column step (activations + scales; a pass of at most 16 pairs loads only
-    // the first A16 units of each activation array: rows 0-15)
-    int n_wt = 0, n_a = SCALED && wave == GM_CW - 1 ? 1 : 0;
+    // DMA instructions of this wave per weight stage
+    int n_wt = 0;
 #pragma unroll
     for (int t = 0; t < G::NWT; t++)
         if (wave + GM_CW * t < G::NW) n_wt++;
-    int n_a16 = n_a;
-#pragma unroll
-    for (int t = 0; t < G::NAT; t++) {
-        const int u = wave + GM_CW * t;
-        if (u < G::NA) n_a++;
-        if (u < G::NA && u % G::NAU < G::A16) n_a16++;
-    }
     const int m_s = lane & 31;        // this lane's pass row of the scale load
 
     // issue pointer: item ii, stage ist = NSUB * column step + row block; the
@@ -465,10 +508,20 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
     __amdgpu_buffer_rsrc_t rW0 = rA0, rW1 = rA0;
     uint32_t iwo[G::NWT], iao[G::NAT];
     uint32_t iso = 0, irowb = 0;
-    bool itwo = true;                 // the issue item's pass uses rows 16-31
+    // The issue item's pass: DMA units of each activation array holding its
+    // rows (the first ceil(pairs * GPR / 64); rows past the pair count feed
+    // only output rows that are never stored) and this wave's activation DMA
+    // instructions per column step (with the scales)
+    int iau = G::NAU, n_a = 0;
     auto setup_issue = [&]() __attribute__((always_inline)) {
         const int32_t* rec = desc + (ii % GM_DESC) * GM_REC;
-        itwo = __builtin_amdgcn_readfirstlane(rec[1]) > 16;
+        iau = min((__builtin_amdgcn_readfirstlane(rec[1]) * G::GPR + 63) >> 6, G::NAU);
+        n_a = SCALED && wave == GM_CW - 1 ? 1 : 0;
+#pragma unroll
+        for (int t = 0; t < G::NAT; t++) {
+            const int u = wave + GM_CW * t;
+            if (u < G::NA && u % G::NAU < iau) n_a++;
+        }
         const int ge = __builtin_amdgcn_readfirstlane(rec[0]);
         const bool shared = ip >= n_rp;
         const int mb = shared ? a.mb_s : a.mb_r;
@@ -493,7 +546,7 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
         }
         // scale dword of lane l: pass row l % 32, the stage's 128-column half l / 32
         if constexpr (SCALED)
-            iso = ((uint32_t)rec[4 + m_s] * (uint32_t)a.sc_ld + (KQ ? (uint32_t)(lane >> 5) : 0u)) * 4u;
+            iso = ((uint32_t)rec[4 + m_s] * (uint32_t)a.sc_ld + (G::KC > 128 ? (uint32_t)(lane >> 5) : 0u)) * 4u;
     };
     int issued = 0, a_issued = 0;
     // Per-wave DMA instruction counts of the issued stages not yet consumed,
@@ -510,7 +563,7 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
         constexpr bool SW = decltype(sw_tag)::value;
         const int kc = ist / NSUB, sub = ist - kc * NSUB;
         if constexpr (!SW) {
-            const int n = n_wt + (sub == 0 ? (itwo ? n_a : n_a16) : 0);
+            const int n = n_wt + (sub == 0 ? n_a : 0);
             qpack |= (uint32_t)n << (4 * qn);
             ++qn;
             qsum += n;
@@ -528,7 +581,7 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
 #pragma unroll
                 for (int t = 0; t < G::NAT; t++) {
                     const int u = wave + GM_CW * t;
-                    if (u < G::NA && (itwo || u % G::NAU < G::A16))
+                    if (u < G::NA && u % G::NAU < iau)
                         __builtin_amdgcn_raw_ptr_buffer_load_lds(u >= G::NAU ? rA1 : rA0,
                                                                  (lds_void*)(adst + G::APART * (u / G::NAU) + 1024 * (u % G::NAU)),
                                                                  16, iao[t], (uint32_t)(2 * G::KC) * (uint32_t)kc, 0, 0);
@@ -555,19 +608,13 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
 
     f32x4 acc[NSUB][1][NMAT][2];
     const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    // 16-weight sub-blocks: the lanes of one half of an MFMA operand's k
-    // range (lanes 0-31: k 0-15, lanes 32-63: k 16-31) and fp16 ones over a
-    // unit (or one half of it) for the activation sums of the mins
+    // Q6_K's 16-weight sub-blocks: the lanes of one half of an MFMA
+    // operand's k range (lanes 0-31: k 0-15, lanes 32-63: k 16-31)
     const bool lo32 = lane < 32;
     auto half_of = [&](f16x8 v, int hv) __attribute__((always_inline)) -> f16x8 {
         const u32x4 u = __builtin_bit_cast(u32x4, v);
         const bool keep = hv == 0 ? lo32 : !lo32;
         return __builtin_bit_cast(f16x8, (u32x4){keep ? u[0] : 0u, keep ? u[1] : 0u, keep ? u[2] : 0u, keep ? u[3] : 0u});
-    };
-    auto ones = [&](int hv) __attribute__((always_inline)) -> f16x8 {
-        const f16x8 one = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f,
-                           (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
-        return F::HALVES == 1 ? one : half_of(one, hv);
     };
 #pragma unroll
     for (int u = 0; u < NSUB; u++)
@@ -628,7 +675,6 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
         } else {
             // one super-block per row: its first byte is lsh (the row start's
             // offset past a 16-byte boundary) plus the chunk offset's into the slot
-            constexpr int HV = F::HALVES;
             const int o = lsh + ((kc * G::CHUNK) & 15);
             const uint8_t* slot[NMAT];
             F row[NMAT];
@@ -637,56 +683,97 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                 slot[mat] = wb + (mat * GM_ROWS + 16 * wave + c) * G::RSLOT;
                 row[mat].head(slot[mat], o);
             }
+            if constexpr (F::FOLD) {
+                // the stage's sums of q * sc and of the mins, per 128-column
+                // half, in the MFMA accumulators; d and dmin once at the end
+                f32x4 sq[NH][NMAT][2], sm[NH][NMAT][2];
 #pragma unroll
-            for (int b = 0; b < 8; b++) {
-                const int hs = SCALED ? b / 4 : 0;          // the stage's 128-column half
-                f16x8 A[AHL][2];
+                for (int h = 0; h < NH; h++)
 #pragma unroll
-                for (int h = 0; h < AHL; h++)
+                    for (int mat = 0; mat < NMAT; mat++) sq[h][mat][0] = sq[h][mat][1] = sm[h][mat][0] = sm[h][mat][1] = zero;
 #pragma unroll
-                    for (int mt = 0; mt < 2; mt++)
-                        A[h][mt] = *(const f16x8*)(ab + G::APART * h + (16 * mt + c) * G::ALD + 16 * (4 * b + g));
-                // activation sums of the unit (or of its halves) for the mins
-                f32x4 X[HV][2];
-                if constexpr (F::MINS) {
+                for (int b = 0; b < 8; b++) {
+                    const int hs = SCALED ? b / 4 : 0;
+                    f16x8 A[AHL][2];
 #pragma unroll
-                    for (int hv = 0; hv < HV; hv++)
+                    for (int h = 0; h < AHL; h++)
+#pragma unroll
+                        for (int mt = 0; mt < 2; mt++)
+                            A[h][mt] = *(const f16x8*)(ab + G::APART * h + (16 * mt + c) * G::ALD + 16 * (4 * b + g));
+#pragma unroll
+                    for (int mat = 0; mat < NMAT; mat++) {
+                        f16x8 Bq, Bm;
+                        row[mat].unit(slot[mat], o, b, g, Bq, Bm);
 #pragma unroll
                         for (int mt = 0; mt < 2; mt++) {
                             if (mt == 1 && !TWO) continue;
-                            X[hv][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0][mt], ones(hv), zero, 0, 0, 0);
-                            if constexpr (AHL == 2)
-                                X[hv][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1][mt], ones(hv), X[hv][mt], 0, 0, 0);
-                        }
-                }
 #pragma unroll
-                for (int mat = 0; mat < NMAT; mat++) {
-                    float am[2], mm[2];
-                    const f16x8 Bv = row[mat].unit(slot[mat], o, b, g, am, mm);
-                    f16x8 B[HV];
-#pragma unroll
-                    for (int hv = 0; hv < HV; hv++) B[hv] = HV == 1 ? Bv : half_of(Bv, hv);
-#pragma unroll
-                    for (int mt = 0; mt < 2; mt++) {
-                        if (mt == 1 && !TWO) continue;
-                        f32x4 r = tv[hs][mat][mt];
-#pragma unroll
-                        for (int hv = 0; hv < HV; hv++) {
-                            f32x4 P = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0][mt], B[hv], zero, 0, 0, 0);
-                            if constexpr (AHL == 2) P = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1][mt], B[hv], P, 0, 0, 0);
-#pragma unroll
-                            for (int i = 0; i < 4; i++) r[i] = fmaf(am[hv], P[i], r[i]);
+                            for (int h = 0; h < AHL; h++)
+                                sq[hs][mat][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[h][mt], Bq, sq[hs][mat][mt], 0, 0, 0);
                             if constexpr (F::MINS) {
 #pragma unroll
-                                for (int i = 0; i < 4; i++) r[i] = fmaf(-mm[hv], X[hv][mt][i], r[i]);
+                                for (int h = 0; h < AHL; h++)
+                                    sm[hs][mat][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[h][mt], Bm, sm[hs][mat][mt], 0, 0, 0);
                             }
                         }
-                        tv[hs][mat][mt] = r;
                     }
                 }
-                // one unit's operands live at a time (fewer registers than
-                // letting the scheduler hoist the next units' LDS reads)
-                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int h = 0; h < NH; h++)
+#pragma unroll
+                    for (int mat = 0; mat < NMAT; mat++)
+#pragma unroll
+                        for (int mt = 0; mt < 2; mt++) {
+                            if (mt == 1 && !TWO) continue;
+                            f32x4 r = tv[h][mat][mt];
+#pragma unroll
+                            for (int i = 0; i < 4; i++) r[i] = fmaf(row[mat].d, sq[h][mat][mt][i], r[i]);
+                            if constexpr (F::MINS) {
+#pragma unroll
+                                for (int i = 0; i < 4; i++) r[i] = fmaf(-row[mat].dmin, sm[h][mat][mt][i], r[i]);
+                            }
+                            tv[h][mat][mt] = r;
+                        }
+            } else {
+                // Q6_K: two MFMAs per unit, each over one 16-weight sub-block
+                // (the other half of the weight operand zero), times d * sc;
+                // the quantised bytes of a 128-column half are read once
+#pragma unroll
+                for (int b = 0; b < 8; b++) {
+                    const int hs = SCALED ? b / 4 : 0;
+                    if ((b & 3) == 0) {
+#pragma unroll
+                        for (int mat = 0; mat < NMAT; mat++) row[mat].half(slot[mat], o, b >> 2, g);
+                    }
+                    f16x8 A[AHL][2];
+#pragma unroll
+                    for (int h = 0; h < AHL; h++)
+#pragma unroll
+                        for (int mt = 0; mt < 2; mt++)
+                            A[h][mt] = *(const f16x8*)(ab + G::APART * h + (16 * mt + c) * G::ALD + 16 * (4 * b + g));
+#pragma unroll
+                    for (int mat = 0; mat < NMAT; mat++) {
+                        float am[2];
+                        const f16x8 Bv = row[mat].unit(b >> 2, b & 3, am);
+                        const f16x8 B[2] = {half_of(Bv, 0), half_of(Bv, 1)};
+#pragma unroll
+                        for (int mt = 0; mt < 2; mt++) {
+                            if (mt == 1 && !TWO) continue;
+                            f32x4 r = tv[hs][mat][mt];
+#pragma unroll
+                            for (int hv = 0; hv < 2; hv++) {
+                                f32x4 P = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0][mt], B[hv], zero, 0, 0, 0);
+                                if constexpr (AHL == 2) P = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1][mt], B[hv], P, 0, 0, 0);
+#pragma unroll
+                                for (int i = 0; i < 4; i++) r[i] = fmaf(am[hv], P[i], r[i]);
+                            }
+                            tv[hs][mat][mt] = r;
+                        }
+                    }
+                    // one unit's operands live at a time (fewer registers than
+                    // letting the scheduler hoist the next units' LDS reads)
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
         }
     };

@@ -370,9 +370,6 @@ int launch_prefill_route(const PrefillArgs& a, const int32_t* forced_ids, const 
     return (int)hipGetLastError();
 }
 
-// Columns per stage of the expert GEMMs for weight format t.
-static int gm_kc(int t) { return t == Q8_0 ? 128 : 256; }
-
 // One gate/up or down GEMM launch of format wt over the passes sel selects.
 static int launch_fmt(int nmat, int nsub, int wt, const PfGemm& g, int n_wg, hipStream_t s) {
     if (wt != Q8_0) return launch_pf_gemm_kq(nmat, nsub, wt, g, n_wg, s);
