@@ -80,8 +80,10 @@ constexpr int GM_THREADS = 64 * (GM_CW + 1);
 constexpr int GM_DESC = 8;            // pass records held in LDS
 
 // Columns per stage of format WT (the launcher's column-step count is
-// the matrix width over this).
+// the matrix width over this); Q8_0 gate/up stages hold one matrix's rows
+// over 256 columns (272-byte runs per row).
 constexpr int gm_kc(int wt) { return wt == Q8_0 ? 128 : 256; }
+constexpr int gm_kc_gateup(int wt) { return wt == Q8_0 ? 256 : gm_kc(wt); }
 
 // Granules of 16 B that hold a row's stage chunk of format WT wherever it starts.
 constexpr int gm_granules(int wt) {
@@ -90,15 +92,19 @@ constexpr int gm_granules(int wt) {
 
 template <int NMAT, int AHL, int NSUB, int WT> struct GmGeo {
     static constexpr bool KQ = WT != Q8_0;
-    static constexpr int KC = gm_kc(WT);                                // columns per stage
-    static constexpr int CHUNK = KQ ? block_bytes(WT) : 136;             // bytes of a row's stage chunk
-    static constexpr int GR = gm_granules(WT);
+    static constexpr bool GU = AHL == 1;                                // gate/up (else down)
+    static constexpr bool SPLIT = GU && NMAT == 1;                      // gate and up in alternate stages
+    static constexpr int KC = SPLIT ? gm_kc_gateup(WT) : gm_kc(WT);     // columns per stage
+    static constexpr int CHUNK = KQ ? block_bytes(WT) : KC / 32 * 34;   // bytes of a row's stage chunk
+    static constexpr int GR = SPLIT ? CHUNK / 16 : gm_granules(WT);
+    static constexpr int ROWS_ITEM = SPLIT ? GM_ROWS : NSUB * GM_ROWS;  // matrix rows per item
+    static_assert(!SPLIT || (NSUB == 2 && WT == Q8_0 && CHUNK % 16 == 0), "split gate/up stages");
     static constexpr int RSLOT = 16 * GR;                               // LDS bytes of a row's chunk
     static constexpr int GPR = KC / 8 + 1;                              // activation granules per row (+ pad)
     static constexpr int ALD = 16 * GPR;
     static constexpr int NAU = (GM_M * GPR + 63) / 64;                  // DMA units per activation array
     static constexpr int APART = NAU * 1024;
-    static constexpr int S = KQ ? 2 : (NMAT == 2 ? 3 : 5);              // weight ring stages
+    static constexpr int S = KQ ? 2 : (GU ? 3 : 5);                     // weight ring stages
     static constexpr int W_BYTES = NMAT * GM_ROWS * RSLOT;
     static constexpr int A_BYTES = AHL * APART;
     static constexpr int A_SLOT = A_BYTES + 256;                        // + 64 scale dwords
@@ -107,10 +113,10 @@ template <int NMAT, int AHL, int NSUB, int WT> struct GmGeo {
     static constexpr int ABASE = S * W_BYTES;
     static constexpr int DESC = ABASE + NAS * A_SLOT;
     static constexpr int RED = DESC + GM_DESC * GM_REC * 4;             // [32 pairs][8 waves] maxima
-    static constexpr int STG = RED + (NMAT == 2 ? GM_M * GM_CW * 4 : 0);
+    static constexpr int STG = RED + (GU ? GM_M * GM_CW * 4 : 0);
     // staging: gate/up 32 pairs x 128 rows of fp16 hi and lo + 32 scales;
     // down 16 pairs x 128 rows of fp32 (the halves of a pass pass through in turn)
-    static constexpr int LDS = STG + (NMAT == 2 ? GM_M * GM_ROWS * 4 + GM_M * 4 : 16 * GM_ROWS * 4);
+    static constexpr int LDS = STG + (GU ? GM_M * GM_ROWS * 4 + GM_M * 4 : 16 * GM_ROWS * 4);
     static constexpr int NW = NMAT * GM_ROWS * GR / 64;                 // weight DMA instructions per stage
     static constexpr int NWT = (NW + GM_CW - 1) / GM_CW;
     static constexpr int NA = AHL * NAU;                                // activation DMA instructions per column step
@@ -440,11 +446,13 @@ template <> struct KqRow<Q8_0> {
 
 // ------------------------------------------------------------------ the kernel
 
-// NMAT = 2: gate and up of a pass (activations: the tokens' x, AHL = 1),
-// SwiGLU epilogue.  NMAT = 1: down (activations: the pairs' SwiGLU outputs as
-// hi + lo, AHL = 2), fp32 epilogue.  An item covers NSUB blocks of 128 rows:
-// each column step loads the activations once and the NSUB weight blocks in
-// turn (one ring stage each).  WT: the weight format of every matrix the
+// AHL = 1: gate and up of a pass (activations: the tokens' x), SwiGLU
+// epilogue; both matrices in each stage (NMAT = 2, NSUB = 1), or gate and up
+// in alternate stages over one activation column step (NMAT = 1, NSUB = 2,
+// Q8_0: 272-byte runs per row).  AHL = 2: down (activations: the pairs'
+// SwiGLU outputs as hi + lo), fp32 epilogue; an item covers NSUB blocks of
+// 128 rows: each column step loads the activations once and the NSUB weight
+// blocks in turn (one ring stage each).  WT: the weight format of every matrix the
 // launch reads (a.sel picks the routed or the shared passes when the two
 // differ).
 template <int NMAT, int AHL, int NSUB, int WT>
@@ -484,9 +492,9 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                                          (lds_void*)(gsm + G::DESC + (i % GM_DESC) * GM_REC * 4), 4, 0, 0);
     };
 
-    // Down (NMAT = 1) activations carry a scale per (row, column step);
-    // gate/up activations (x) one per token, applied in the epilogue.
-    constexpr bool SCALED = NMAT == 1;
+    // Down activations carry a scale per (row, 128 columns); gate/up
+    // activations (x) one per token, applied in the epilogue.
+    constexpr bool SCALED = !G::GU;
     // DMA instructions of this wave per weight stage
     int n_wt = 0;
 #pragma unroll
@@ -526,12 +534,12 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
         const bool shared = ip >= n_rp;
         const int mb = shared ? a.mb_s : a.mb_r;
         rW0 = gm_rsrc(shared ? a.s0 : a.w0 + (int64_t)ge * a.st0, mb);
-        rW1 = NMAT == 2 ? gm_rsrc(shared ? a.s1 : a.w1 + (int64_t)ge * a.st1, mb) : rW0;
+        rW1 = G::GU ? gm_rsrc(shared ? a.s1 : a.w1 + (int64_t)ge * a.st1, mb) : rW0;
         irowb = (uint32_t)(shared ? a.rb_s : a.rb_r);
 #pragma unroll
         for (int t = 0; t < G::NWT; t++) {
             const int p = 64 * (wave + GM_CW * t) + lane, rem = p % (GM_ROWS * G::GR), r = rem / G::GR;
-            iwo[t] = (((uint32_t)(irg * NSUB * GM_ROWS + r) * irowb) & ~15u) + 16u * (uint32_t)(rem - G::GR * r);
+            iwo[t] = (((uint32_t)(irg * G::ROWS_ITEM + r) * irowb) & ~15u) + 16u * (uint32_t)(rem - G::GR * r);
         }
         // activation instruction u = wave + 8 t: array u / NAU, LDS granules
         // 64 (u % NAU) + lane = GPR m + jj of the array (jj = GPR - 1: pad;
@@ -568,13 +576,14 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
             ++qn;
             qsum += n;
             lds8_t* dst = (lds8_t*)(gsm + (issued % S) * G::W_BYTES);
-            const uint32_t soff = (((uint32_t)kc * (uint32_t)G::CHUNK) & ~15u) + (uint32_t)(sub * GM_ROWS) * irowb;
+            const uint32_t soff = (((uint32_t)kc * (uint32_t)G::CHUNK) & ~15u) +
+                                  (G::SPLIT ? 0u : (uint32_t)(sub * GM_ROWS) * irowb);
 #pragma unroll
             for (int t = 0; t < G::NWT; t++) {
                 const int q = wave + GM_CW * t;
                 if (q < G::NW)
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(q < GM_ROWS * G::GR / 64 ? rW0 : rW1, (lds_void*)(dst + 1024 * q),
-                                                             16, iwo[t], soff, 0, 0);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds((G::SPLIT ? sub != 0 : q >= GM_ROWS * G::GR / 64) ? rW1 : rW0,
+                                                             (lds_void*)(dst + 1024 * q), 16, iwo[t], soff, 0, 0);
             }
             if (sub == 0) {
                 lds8_t* adst = (lds8_t*)(gsm + G::ABASE + (a_issued % G::NAS) * G::A_SLOT);
@@ -644,9 +653,9 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                 for (int mat = 0; mat < NMAT; mat++) tv[h][mat][0] = tv[h][mat][1] = zero;
         }
         if constexpr (!KQ) {
-            const int sh8 = (kc & 1) * 8;
+            const int sh8 = G::KC == 128 ? (kc & 1) * 8 : 0;
 #pragma unroll
-            for (int b = 0; b < 4; b++) {
+            for (int b = 0; b < G::KC / 32; b++) {
                 f16x8 A[AHL][2];
 #pragma unroll
                 for (int h = 0; h < AHL; h++)
@@ -661,7 +670,11 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                     if (b == 0) B = q8_f16x8<0>(rowp, g);
                     else if (b == 1) B = q8_f16x8<1>(rowp, g);
                     else if (b == 2) B = q8_f16x8<2>(rowp, g);
-                    else B = q8_f16x8<3>(rowp, g);
+                    else if (b == 3) B = q8_f16x8<3>(rowp, g);
+                    else if (b == 4) B = q8_f16x8<4>(rowp, g);
+                    else if (b == 5) B = q8_f16x8<5>(rowp, g);
+                    else if (b == 6) B = q8_f16x8<6>(rowp, g);
+                    else B = q8_f16x8<7>(rowp, g);
 #pragma unroll
                     for (int mt = 0; mt < 2; mt++) {
                         if (mt == 1 && !TWO) continue;
@@ -858,7 +871,7 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
         auto row_shift = [&]() __attribute__((always_inline)) -> int {
             if constexpr (F::AL >= 16) return 0;
             const uint32_t rb = (uint32_t)(cp >= n_rp ? a.rb_s : a.rb_r);
-            return (int)(((uint32_t)(crg * NSUB * GM_ROWS + 16 * wave + c) * rb) & 15u);
+            return (int)(((uint32_t)(crg * G::ROWS_ITEM + 16 * wave + c) * rb) & 15u);
         };
         int clsh = row_shift();
         bool two = false, pend = false;
@@ -907,7 +920,7 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                 continue;
             }
             // item done: epilogue into the staging area
-            if constexpr (NMAT == 2) {
+            if constexpr (G::GU) {
                 // this lane's pass rows are 16 mt + 4 g + i: one base per
                 // array plus constant offsets
                 float av[2][4];
@@ -922,7 +935,9 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                         for (int i = 0; i < 4; i++) {
                             const int xe = (int)(int8_t)((mt ? xw1 : xw) >> (8 * i));
                             const float xs = ldexpf(1.0f, xe);
-                            const float v = silu_mul(acc[0][0][0][mt][i] * xs, acc[0][0][1][mt][i] * xs);
+                            const float gv = acc[0][0][0][mt][i], uv = G::SPLIT ? acc[NSUB - 1][0][0][mt][i]
+                                                                                 : acc[0][0][NMAT - 1][mt][i];
+                            const float v = silu_mul(gv * xs, uv * xs);
                             av[mt][i] = v;
                             float mx = fabsf(v);
                             mx = fmaxf(mx, dpp_f32<DPP_ROR8>(mx));

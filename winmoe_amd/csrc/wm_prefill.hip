@@ -12,14 +12,14 @@
 //   k_pf_group     counting sort of the pairs by expert; passes of <= 32
 //                  pairs of one expert
 //   k_pf_xpack     x as fp16 times a power of two per token
-//   k_pf_gemm<2,1> gate and up + SwiGLU on fp16 MFMA, persistent: one
+//   k_pf_gemm      gate and up + SwiGLU on fp16 MFMA, persistent: one
 //                  workgroup per CU streams (pass, 128-row block) items
 //                  through an LDS-DMA ring; the SwiGLU output is stored as
-//                  fp16 hi + lo times a power of two per (pair, 128 rows)
-//   k_pf_gemm<1,2> down projection of the same form (hi and lo: two MFMAs)
-//                  (both in wm_pf_gemm.h, one instance per weight format;
-//                  routed and shared experts of different formats take a
-//                  launch each)
+//                  fp16 hi + lo times a power of two per (pair, 128 rows);
+//                  then the down projection of the same form (hi and lo:
+//                  two MFMAs) (both in wm_pf_gemm.h, one instance per weight
+//                  format; routed and shared experts of different formats
+//                  take a launch each)
 //   k_pf_combine   per token: sum_k w_k y_k in k order + gate * y_shared
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -373,7 +373,7 @@ int launch_prefill_route(const PrefillArgs& a, const int32_t* forced_ids, const 
 // One gate/up or down GEMM launch of format wt over the passes sel selects.
 static int launch_fmt(int nmat, int nsub, int wt, const PfGemm& g, int n_wg, hipStream_t s) {
     if (wt != Q8_0) return launch_pf_gemm_kq(nmat, nsub, wt, g, n_wg, s);
-    if (nmat == 2) return launch_pf_gemm<2, 1, 1, Q8_0>(g, n_wg, s);
+    if (nmat == 2) return launch_pf_gemm<1, 1, 2, Q8_0>(g, n_wg, s);     // gate and up in alternate stages
     return nsub == 4 ? launch_pf_gemm<1, 2, 4, Q8_0>(g, n_wg, s) : launch_pf_gemm<1, 2, 2, Q8_0>(g, n_wg, s);
 }
 
@@ -402,7 +402,7 @@ int launch_prefill_gateup(const PrefillArgs& a, hipStream_t s) {
     g.a_bytes = (int32_t)((int64_t)a.T * a.H * 2); g.sc_bytes = 0;
     g.T = a.T; g.K = a.K; g.E = a.E; g.by_token = 1;
     g.nrb_r = a.I / GM_ROWS; g.nrb_s = a.has_shared ? a.Is / GM_ROWS : 1;
-    g.nkc_r = a.H / gm_kc(a.gt); g.nkc_s = a.H / gm_kc(a.has_shared ? a.sgt : a.gt);
+    g.nkc_r = a.H / gm_kc_gateup(a.gt); g.nkc_s = a.H / gm_kc_gateup(a.has_shared ? a.sgt : a.gt);
     g.recs = a.passes; g.npass = a.pass_count;
     g.o_hi = a.act_hi; g.o_lo = a.act_lo; g.o_sc = a.act_sc; g.o_ld = a.act_stride; g.osc_ld = a.act_stride / 128;
     return launch_split(2, 1, a.gt, a.sgt, a.has_shared, g, a.n_wg, s);
