@@ -6,14 +6,16 @@
 // One workgroup per CU works through a static list of items: item j of a
 // launch is (pass, block of 128 matrix rows), and workgroup b takes items
 // b, b + grid, b + 2 grid, ...  For each item it streams the block's rows (of
-// gate and up, or of down) through an S-stage LDS ring, KC columns per stage
-// (Q8_0: 128 = 4 blocks; K-quants: 256 = one super-block), filled by
+// gate and up, or of down) through an S-stage LDS ring, 256 columns per
+// stage (Q8_0: 8 blocks; K-quants: one super-block), filled by
 // global_load_lds:
 //   * weights: each row's stage chunk as GR granules of 16 B from the
 //     16-byte boundary at or before the row start plus the 16-byte boundary
-//     at or before the chunk's offset in the row (Q8_0 136 B: 9 granules;
-//     Q4_K 144 B and Q5_K 176 B start aligned: 9 and 11; Q2_K 84 B, Q3_K
-//     110 B and Q6_K 210 B start up to 24 or 28 bytes in: 7, 9 and 15);
+//     at or before the chunk's offset in the row (Q8_0 272 B, Q4_K 144 B and
+//     Q5_K 176 B start aligned: 17, 9 and 11 granules; Q2_K 84 B, Q3_K 110 B
+//     and Q6_K 210 B start up to 24 or 28 bytes in: 7, 9 and 15).  Longer
+//     runs per row stream faster: a probe of this one-workgroup-per-CU ring
+//     reads 136-byte row pieces at 4.6 TB/s, 272-byte ones at 5.5;
 //   * activations: the pass's 32 rows x KC fp16, rows one pad granule
 //     longer than their data, so the MFMA operand reads of 16 rows hit 16
 //     different 16-byte slots of a 256-byte bank cycle;
@@ -79,32 +81,31 @@ constexpr int GM_CW = 8;              // compute waves
 constexpr int GM_THREADS = 64 * (GM_CW + 1);
 constexpr int GM_DESC = 8;            // pass records held in LDS
 
-// Columns per stage of format WT (the launcher's column-step count is
-// the matrix width over this); Q8_0 gate/up stages hold one matrix's rows
-// over 256 columns (272-byte runs per row).
-constexpr int gm_kc(int wt) { return wt == Q8_0 ? 128 : 256; }
-constexpr int gm_kc_gateup(int wt) { return wt == Q8_0 ? 256 : gm_kc(wt); }
+// Columns per stage, every format (the launcher's column-step count is the
+// matrix width over this).
+constexpr int GM_KC = 256;
 
 // Granules of 16 B that hold a row's stage chunk of format WT wherever it starts.
 constexpr int gm_granules(int wt) {
-    return wt == Q8_0 ? 9 : wt == Q4_K ? 9 : wt == Q5_K ? 11 : wt == Q2_K ? 7 : wt == Q3_K ? 9 : 15;
+    return wt == Q8_0 ? 17 : wt == Q4_K ? 9 : wt == Q5_K ? 11 : wt == Q2_K ? 7 : wt == Q3_K ? 9 : 15;
 }
 
 template <int NMAT, int AHL, int NSUB, int WT> struct GmGeo {
     static constexpr bool KQ = WT != Q8_0;
     static constexpr bool GU = AHL == 1;                                // gate/up (else down)
     static constexpr bool SPLIT = GU && NMAT == 1;                      // gate and up in alternate stages
-    static constexpr int KC = SPLIT ? gm_kc_gateup(WT) : gm_kc(WT);     // columns per stage
+    static constexpr int KC = GM_KC;                                    // columns per stage
     static constexpr int CHUNK = KQ ? block_bytes(WT) : KC / 32 * 34;   // bytes of a row's stage chunk
-    static constexpr int GR = SPLIT ? CHUNK / 16 : gm_granules(WT);
+    static constexpr int GR = gm_granules(WT);
     static constexpr int ROWS_ITEM = SPLIT ? GM_ROWS : NSUB * GM_ROWS;  // matrix rows per item
-    static_assert(!SPLIT || (NSUB == 2 && WT == Q8_0 && CHUNK % 16 == 0), "split gate/up stages");
+    static_assert(!SPLIT || (NSUB == 2 && WT == Q8_0), "split gate/up stages");
+    static_assert(KQ || GR * 16 == CHUNK, "Q8_0 chunks are whole granules");
     static constexpr int RSLOT = 16 * GR;                               // LDS bytes of a row's chunk
     static constexpr int GPR = KC / 8 + 1;                              // activation granules per row (+ pad)
     static constexpr int ALD = 16 * GPR;
     static constexpr int NAU = (GM_M * GPR + 63) / 64;                  // DMA units per activation array
     static constexpr int APART = NAU * 1024;
-    static constexpr int S = KQ ? 2 : (GU ? 3 : 5);                     // weight ring stages
+    static constexpr int S = SPLIT ? 3 : 2;                             // weight ring stages
     static constexpr int W_BYTES = NMAT * GM_ROWS * RSLOT;
     static constexpr int A_BYTES = AHL * APART;
     static constexpr int A_SLOT = A_BYTES + 256;                        // + 64 scale dwords
@@ -186,7 +187,7 @@ WM_DEV void gm_wait_vm(int n) {
 }
 
 // The 8 int8 weights k = 8g .. 8g+7 of block B of a row chunk as fp16
-// (exact).  rowp: the chunk's first byte in LDS (8-byte aligned).
+// (exact).  rowp: the chunk's first byte in LDS (16-byte aligned).
 template <int B> WM_DEV f16x8 q8_f16x8(const uint8_t* rowp, int g) {
     constexpr int off = 34 * B + 2;
     const uint32_t* p = (const uint32_t*)(rowp + (off & ~3) + 8 * g);
@@ -653,9 +654,9 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                 for (int mat = 0; mat < NMAT; mat++) tv[h][mat][0] = tv[h][mat][1] = zero;
         }
         if constexpr (!KQ) {
-            const int sh8 = G::KC == 128 ? (kc & 1) * 8 : 0;
 #pragma unroll
             for (int b = 0; b < G::KC / 32; b++) {
+                const int hs = SCALED ? b / 4 : 0;          // the stage's 128-column half
                 f16x8 A[AHL][2];
 #pragma unroll
                 for (int h = 0; h < AHL; h++)
@@ -664,7 +665,7 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                         A[h][mt] = *(const f16x8*)(ab + G::APART * h + (16 * mt + c) * G::ALD + 16 * (4 * b + g));
 #pragma unroll
                 for (int mat = 0; mat < NMAT; mat++) {
-                    const uint8_t* rowp = wb + (mat * GM_ROWS + 16 * wave + c) * G::RSLOT + sh8;
+                    const uint8_t* rowp = wb + (mat * GM_ROWS + 16 * wave + c) * G::RSLOT;
                     const float d = (float)*(const _Float16*)(rowp + 34 * b);
                     f16x8 B;
                     if (b == 0) B = q8_f16x8<0>(rowp, g);
@@ -681,7 +682,7 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                         f32x4 P = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0][mt], B, zero, 0, 0, 0);
                         if constexpr (AHL == 2) P = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[AHL - 1][mt], B, P, 0, 0, 0);
 #pragma unroll
-                        for (int i = 0; i < 4; i++) tv[0][mat][mt][i] = fmaf(d, P[i], tv[0][mat][mt][i]);
+                        for (int i = 0; i < 4; i++) tv[hs][mat][mt][i] = fmaf(d, P[i], tv[hs][mat][mt][i]);
                     }
                 }
             }
