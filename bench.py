@@ -116,9 +116,10 @@ def prefill_gateup_kernel(cfg) -> str:
     sgt = TYPE_NAMES[cfg.shared_types[0]] if cfg.shared_types else gt
     what = ("fp16 MFMA over Q8_0 blocks" if gt == "Q8_0" else
             f"fp16 MFMA over {gt} super-blocks, mins from activation sums")
+    inst = {t: ("k_pf_gemm<1,1,2,Q8_0>" if t == "Q8_0" else f"k_pf_gemm<2,1,1,{t}>") for t in (gt, sgt)}
     if sgt == gt:
-        return f"k_pf_gemm<2,1,1,{gt}> (prefill gate+up+SwiGLU: {what}, LDS-DMA ring)"
-    return (f"k_pf_gemm<2,1,1,{gt}> + k_pf_gemm<2,1,1,{sgt}> (prefill gate+up+SwiGLU phase: routed {gt} "
+        return f"{inst[gt]} (prefill gate+up+SwiGLU: {what}, LDS-DMA ring)"
+    return (f"{inst[gt]} + {inst[sgt]} (prefill gate+up+SwiGLU phase: routed {gt} "
             f"launch and shared-expert {sgt} launch; {what})")
 
 
