@@ -215,10 +215,9 @@ int wm_moe_decode_forced(const wm_layer_desc* d, const float* x, const int32_t* 
  * gathers the outputs.  T <= max_tokens; the workspace (one per layer and
  * stream) holds wm_prefill_workspace_size(d, max_tokens) bytes, 256-byte
  * aligned.  x and out are 16-byte aligned.  Expert matrices (routed and
- * shared, each with its own formats): gate and up of one format among Q8_0,
- * Q2_K, Q3_K, Q4_K, Q5_K, down any of those or Q6_K; 16-byte aligned with
- * strides that are multiples of 16; H, I, inter_shared multiples of 256;
- * otherwise WM_EINVAL. */
+ * shared, each with its own formats): Q8_0 or Q2_K .. Q6_K, gate and up of
+ * one format; 16-byte aligned with strides that are multiples of 16; H, I,
+ * inter_shared multiples of 256; otherwise WM_EINVAL. */
 int64_t wm_prefill_workspace_size(const wm_layer_desc* d, int max_tokens);
 int wm_moe_prefill(const wm_layer_desc* d, const uint16_t* x_bf16, int T, float* out, void* ws,
                    int64_t ws_bytes, int max_tokens, void* stream);

@@ -418,10 +418,10 @@ def test_prefill_rejects_unsupported_widths(wm):
     assert ei.value.rc == wm._lib.WM_EINVAL
 
 
-@pytest.mark.parametrize("types", [(Q6_K, Q6_K, Q8_0), (Q4_K, Q5_K, Q6_K)])
+@pytest.mark.parametrize("types", [(Q4_K, Q5_K, Q6_K), (Q8_0, Q6_K, Q8_0)])
 def test_prefill_rejects_unsupported_formats(wm, types):
-    """Prefill refuses Q6_K gate/up matrices and gate and up of different
-    formats (WM_EINVAL, nothing launched); decode takes both."""
+    """Prefill refuses gate and up of different formats (WM_EINVAL, nothing
+    launched); decode takes them."""
     from winmoe_amd import synth
     cfg = synth.LayerConfig("pf_fmt", E=8, K=2, H=512, I=256, types=types, tokens=1, x_dtype="bf16", seed=5)
     sl = synth.build_layer(cfg, max_tokens=4)
@@ -492,6 +492,8 @@ KQ_PREFILL = [
     ((Q3_K, Q2_K), (Q4_K, Q4_K), 256),
     ((Q8_0, Q6_K), (Q2_K, Q8_0), 1024),
     ((Q4_K, Q4_K), (Q3_K, Q5_K), 256),
+    ((Q6_K, Q4_K), None, 256),
+    ((Q6_K, Q6_K), (Q8_0, Q6_K), 1024),
 ]
 
 

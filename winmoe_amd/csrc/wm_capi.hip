@@ -850,14 +850,13 @@ static int run_prefill(const wm_layer_desc* d, const uint16_t* x, int T, const i
     PfLayout L = pf_layout(d, max_tokens);
     WM_CHECK_ARG(ws_bytes >= L.total);
     const bool sh = has_shared(d);
-    const bool types = d->gate_type == d->up_type && prefill_gateup_type(d->gate_type) &&
-                       prefill_down_type(d->down_type) &&
-                       (!sh || (d->sh_gate_type == d->sh_up_type && prefill_gateup_type(d->sh_gate_type) &&
-                                prefill_down_type(d->sh_down_type)));
+    const bool types = d->gate_type == d->up_type && prefill_type(d->gate_type) && prefill_type(d->down_type) &&
+                       (!sh || (d->sh_gate_type == d->sh_up_type && prefill_type(d->sh_gate_type) &&
+                                prefill_type(d->sh_down_type)));
     const bool shapes = d->hidden % 256 == 0 && d->inter % 256 == 0 && (!sh || Ishared(d) % 256 == 0);
     if (!types || !shapes) {
-        fprintf(stderr, "winmoe_hip: prefill needs gate and up of one format among Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, "
-                        "down among those or Q6_K, and H, I multiples of 256\n");
+        fprintf(stderr, "winmoe_hip: prefill needs quantised expert matrices (Q8_0, Q2_K .. Q6_K) with gate and up "
+                        "of one format, and H, I multiples of 256\n");
         return WM_EINVAL;
     }
     if (wm_init()) return WM_ERR;

@@ -98,7 +98,7 @@ template <int NMAT, int AHL, int NSUB, int WT> struct GmGeo {
     static constexpr int CHUNK = KQ ? block_bytes(WT) : KC / 32 * 34;   // bytes of a row's stage chunk
     static constexpr int GR = gm_granules(WT);
     static constexpr int ROWS_ITEM = SPLIT ? GM_ROWS : NSUB * GM_ROWS;  // matrix rows per item
-    static_assert(!SPLIT || (NSUB == 2 && WT == Q8_0), "split gate/up stages");
+    static_assert(!SPLIT || NSUB == 2, "split gate/up stages");
     static_assert(KQ || GR * 16 == CHUNK, "Q8_0 chunks are whole granules");
     static constexpr int RSLOT = 16 * GR;                               // LDS bytes of a row's chunk
     static constexpr int GPR = KC / 8 + 1;                              // activation granules per row (+ pad)
@@ -1030,9 +1030,9 @@ template <int NMAT, int AHL, int NSUB, int WT> int launch_pf_gemm(const PfGemm& 
     return (int)hipGetLastError();
 }
 
-// The K-quant instances (wm_prefill_kq.hip): gate/up (nmat = 2) of formats
-// Q2_K, Q3_K, Q4_K, Q5_K; down (nmat = 1, nsub = 2 or 4) of Q2_K .. Q6_K.
-// Returns hipErrorInvalidValue for another combination.
+// The K-quant instances (wm_prefill_kq.hip): gate/up (nmat = 2) and down
+// (nmat = 1, nsub = 2 or 4) of Q2_K .. Q6_K.  Returns hipErrorInvalidValue
+// for another combination.
 int launch_pf_gemm_kq(int nmat, int nsub, int wt, const PfGemm& g, int n_wg, hipStream_t s);
 
 }  // namespace wm

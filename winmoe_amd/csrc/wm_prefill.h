@@ -48,8 +48,7 @@ struct PrefillArgs {
 inline int64_t prefill_max_passes(int64_t T, int64_t K, int64_t E) { return (T * K + 31) / 32 + E + (T + 31) / 32 + 1; }
 
 // Weight formats the expert GEMMs read: gate and up (one format for both) and down.
-inline bool prefill_gateup_type(int t) { return t == Q8_0 || t == Q2_K || t == Q3_K || t == Q4_K || t == Q5_K; }
-inline bool prefill_down_type(int t) { return prefill_gateup_type(t) || t == Q6_K; }
+inline bool prefill_type(int t) { return t == Q8_0 || t == Q2_K || t == Q3_K || t == Q4_K || t == Q5_K || t == Q6_K; }
 
 // The phases of a prefill, stream-ordered (the caller checks types: gate and
 // up of one format, formats the GEMMs read, H, I, Is multiples of 256, expert

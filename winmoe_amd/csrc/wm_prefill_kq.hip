@@ -13,11 +13,15 @@ template <int WT> static int launch_down(int nsub, const PfGemm& g, int n_wg, hi
 
 int launch_pf_gemm_kq(int nmat, int nsub, int wt, const PfGemm& g, int n_wg, hipStream_t s) {
     if (nmat == 2) {
+        // gate and up in one stage (half the stages of alternating them, at
+        // a 2-deep ring: faster for these formats); Q6_K's row slots only fit
+        // as alternate gate and up stages
         switch (wt) {
         case Q2_K: return launch_pf_gemm<2, 1, 1, Q2_K>(g, n_wg, s);
         case Q3_K: return launch_pf_gemm<2, 1, 1, Q3_K>(g, n_wg, s);
         case Q4_K: return launch_pf_gemm<2, 1, 1, Q4_K>(g, n_wg, s);
         case Q5_K: return launch_pf_gemm<2, 1, 1, Q5_K>(g, n_wg, s);
+        case Q6_K: return launch_pf_gemm<1, 1, 2, Q6_K>(g, n_wg, s);
         default: return (int)hipErrorInvalidValue;
         }
     }
