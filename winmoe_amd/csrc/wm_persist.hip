@@ -590,31 +590,43 @@ WM_DEV void router_chains(const lds8_t* lx, int region, int H, int r0, int ra, i
     if (row < 0) return;                            // (idle lanes take no LDS bandwidth)
     const lf32_t* xr = (const lf32_t*)lx;
     const lf32_t* wr = (const lf32_t*)(lx + (1 + (row >= 0 ? row : 0)) * region);
-    const int H16 = H - (H & 15), nsteps = H16 / 16;
+    const int H16 = H - (H & 15), nsteps = H16 / 16, nblk = nsteps / 16;
     float acc = 0.0f;
-    int s = 0;
-    if (nsteps >= 16) {
+    // block b: steps 16 b .. 16 b + 15, this lane's columns c + 256 b + 16 j:
+    // one base address per block and immediate offsets (the LDS reads pair up
+    // two to an instruction); the next block's reads are issued before the
+    // current block's FMAs, alternating two register sets
+    const lf32_t* wp = wr + c;
+    const lf32_t* xp = xr + c;
+    if (nblk > 0) {
         float wa[16], xa[16], wb[16], xb[16];
-#pragma unroll
-        for (int j = 0; j < 16; j++) { wa[j] = wr[c + 16 * j]; xa[j] = xr[c + 16 * j]; }
-        for (; s + 32 <= nsteps; s += 32) {
-#pragma unroll
-            for (int j = 0; j < 16; j++) { wb[j] = wr[c + 16 * (s + 16 + j)]; xb[j] = xr[c + 16 * (s + 16 + j)]; }
-#pragma unroll
-            for (int j = 0; j < 16; j++) acc = fmaf(wa[j], xa[j], acc);
-            const int sn = min(s + 32, nsteps - 16);        // next block (a repeat at the end is never used)
-#pragma unroll
-            for (int j = 0; j < 16; j++) { wa[j] = wr[c + 16 * (sn + j)]; xa[j] = xr[c + 16 * (sn + j)]; }
-#pragma unroll
-            for (int j = 0; j < 16; j++) acc = fmaf(wb[j], xb[j], acc);
-        }
-        if (s + 16 <= nsteps) {
-#pragma unroll
-            for (int j = 0; j < 16; j++) acc = fmaf(wa[j], xa[j], acc);
-            s += 16;
-        }
+#define WM_RC_LOAD(blk, W, X)                                                  \
+    {                                                                          \
+        const lf32_t* wn_ = wp + 256 * (blk);                                  \
+        const lf32_t* xn_ = xp + 256 * (blk);                                  \
+        _Pragma("unroll") for (int j = 0; j < 16; j++) {                       \
+            W[j] = wn_[16 * j];                                                \
+            X[j] = xn_[16 * j];                                                \
+        }                                                                      \
     }
-    for (; s < nsteps; s++) acc = fmaf(wr[c + 16 * s], xr[c + 16 * s], acc);
+#define WM_RC_FMA(W, X) _Pragma("unroll") for (int j = 0; j < 16; j++) acc = fmaf(W[j], X[j], acc);
+        WM_RC_LOAD(0, wa, xa)
+        int b = 0;
+        // (the compiler barriers keep each block's reads ahead of the FMAs
+        // of the block before it)
+        for (; b + 2 <= nblk; b += 2) {
+            WM_RC_LOAD(b + 1, wb, xb)
+            asm volatile("" ::: "memory");
+            WM_RC_FMA(wa, xa)
+            WM_RC_LOAD(min(b + 2, nblk - 1), wa, xa)       // (a repeat at the end is never used)
+            asm volatile("" ::: "memory");
+            WM_RC_FMA(wb, xb)
+        }
+        if (b < nblk) WM_RC_FMA(wa, xa)                    // an odd block count: the last block
+#undef WM_RC_FMA
+#undef WM_RC_LOAD
+    }
+    for (int s = 16 * nblk; s < nsteps; s++) acc = fmaf(wr[c + 16 * s], xr[c + 16 * s], acc);
     acc += dpp_f32<DPP_ROR8>(acc);
     acc += dpp_f32<DPP_ROR4>(acc);
     acc += dpp_f32<DPP_ROR2>(acc);
