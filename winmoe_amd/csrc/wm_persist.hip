@@ -83,12 +83,15 @@ WM_DEV uint64_t tagged(uint32_t tag, float v) { return ((uint64_t)tag << 32) | (
 WM_DEV uint32_t lds_ld(const lds32_t* p) { return *(const volatile lds32_t*)p; }
 
 // Every LDS write of this wave is complete, then lane 0 stores v to *p (a
-// word with one writer; volatile, not atomic, for the reason above).
+// word with one writer; volatile, not atomic, for the reason above), then
+// s_wakeup ends the s_sleep of every waiting wave of the workgroup, so a
+// waiter polls again at once instead of after its pause.
 WM_DEV void lds_set(lds32_t* p, uint32_t v, int lane) {
     WM_WAIT_LGKM0();
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     if (lane == 0) *(volatile lds32_t*)p = v;
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    asm volatile("s_wakeup" ::: "memory");
 }
 
 // A wait gave up: report it and make every later wait of the workgroup end
@@ -673,7 +676,9 @@ WM_DEV void route_tagged(const PersistArgs& a, lctl_t* ctl, int rep, uint32_t ta
     float lv[MAXV];
 #pragma unroll
     for (int i = 0; i < MAXV; i++) lv[i] = __builtin_bit_cast(float, (uint32_t)tv[i]);
-    SortedPicker<MAXV> pk;
+    // (keys unsorted: pick 0 is one lane maximum and one wave maximum away,
+    // and a later pick recomputes only its winning lane's maximum)
+    Picker<MAXV> pk;
     pk.init_vals(lv, E, lane);
     // lane k keeps pick k's key; ids and values are decoded after the loop
     uint64_t kb = 0ull;
@@ -859,7 +864,8 @@ WM_DEV void helper_router(const PersistArgs& a, uint8_t* smem, int lane) {
         lds_set(&ctl->router_done[0], 1u, lane);
         if (lane == 0) ctl->t[2] = now();
         bool degenerate = false, nonfinite = false;
-        if (E <= 512) route_tagged<8>(a, ctl, P.w % P_REP, tag, lane, my_e, wk, degenerate, nonfinite);
+        if (E <= 64) route_tagged<1>(a, ctl, P.w % P_REP, tag, lane, my_e, wk, degenerate, nonfinite);
+        else if (E <= 512) route_tagged<8>(a, ctl, P.w % P_REP, tag, lane, my_e, wk, degenerate, nonfinite);
         else route_tagged<16>(a, ctl, P.w % P_REP, tag, lane, my_e, wk, degenerate, nonfinite);
         valid = lane < K;
         if (P.w == 0) {

@@ -433,51 +433,6 @@ template <int MAXV> struct Picker {
     }
 };
 
-// As Picker, with each lane's keys sorted (largest first) once, so that a
-// pick costs one 32-bit wave maximum, a ballot and a register shift in the
-// winning lane: the winner is the only lane holding the largest upper half
-// unless values tie, when the lower halves decide as in Picker.  Same picks.
-template <int MAXV> struct SortedPicker {
-    uint64_t key[MAXV];
-    float v0;
-    WM_DEV void init_vals(const float (&lv)[MAXV], int E, int lane) {
-        v0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lv[0]), 0));
-#pragma unroll
-        for (int i = 0; i < MAXV; i++) key[i] = (lane + 64 * i) < E ? topk_key(lv[i], lane + 64 * i) : 0ull;
-        // odd-even transposition sort, descending
-#pragma unroll
-        for (int r = 0; r < MAXV; r++)
-#pragma unroll
-            for (int i = r & 1; i + 1 < MAXV; i += 2) {
-                const uint64_t hi = max_u64(key[i], key[i + 1]), lo = key[i] ^ key[i + 1] ^ hi;
-                key[i] = hi;
-                key[i + 1] = lo;
-            }
-    }
-    WM_DEV uint64_t next() {
-        const uint32_t hh = (uint32_t)(key[0] >> 32);
-        const uint32_t hi = wave_max_u32(hh);
-        const uint64_t m = __builtin_amdgcn_ballot_w64(hh == hi);
-        uint32_t lo;
-        if (hi != 0u && __builtin_popcountll(m) == 1)
-            lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key[0], (int)__builtin_ctzll(m));
-        else
-            lo = wave_max_u32(hh == hi ? (uint32_t)key[0] : 0u);
-        const uint64_t best = ((uint64_t)hi << 32) | lo;
-        if (best != 0ull && key[0] == best) {
-#pragma unroll
-            for (int i = 0; i + 1 < MAXV; i++) key[i] = key[i + 1];
-            key[MAXV - 1] = 0ull;
-        }
-        return best;
-    }
-    WM_DEV float value_of(uint64_t best) const {
-        if (!best) return v0;
-        const uint32_t u = (uint32_t)(best >> 32);
-        return __builtin_bit_cast(float, (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
-    }
-};
-
 // One wave: top-K (K <= 16) of E <= 64 * MAXV logits and the softmax over
 // the picks (transformer.h:142-149).  Lane k keeps pick k, writes ids[k] /
 // w[k] and bumps the pick's hit counter; degenerate / non-finite routing is
