@@ -252,7 +252,7 @@ int64_t wm_expert_workspace_size(int H, int I);
  * on a device shares that device's array: calls that overlap on one device
  * (other streams, other threads) race and give wrong results.  Each call
  * clears the part it uses with a kernel before the step. */
-#define WM_NOALLOC_SCRATCH_BYTES (4 * 1024 * 1024)
+#define WM_NOALLOC_SCRATCH_BYTES (3 * 1024 * 1024)
 int wm_noalloc_init(void);
 int64_t wm_noalloc_scratch_bytes(void);
 int wm_moe_decode_noalloc(const wm_layer_desc* d, const float* x, float* out, int32_t* ids_out, float* w_out,

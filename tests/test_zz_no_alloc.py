@@ -35,7 +35,7 @@ def test_noalloc_matches_workspace_decode():
     assert torch.cuda.is_available()
     L = wm.load()
     assert L.wm_noalloc_init() == 0
-    assert L.wm_noalloc_scratch_bytes() == 4 * 1024 * 1024
+    assert L.wm_noalloc_scratch_bytes() == 3 * 1024 * 1024
     for name, E in (("c2", 512), ("c1", 64)):          # the second call is the smaller layer
         cfg = synth.CONFIGS[name]
         sl = synth.build_layer(cfg, E=E, max_tokens=4)

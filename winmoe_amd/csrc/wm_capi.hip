@@ -277,7 +277,7 @@ static WsLayout layout(const wm_layer_desc* d, int max_tokens) {
     L.tlog = o; o += up256((int64_t)P_REP * E * 8);
     L.hello = o; o += up256((int64_t)P_MAX_WG * 4);
     L.pctr = o; o += (int64_t)CTR_STRIDE * 4;
-    L.tact = o; o += up256((int64_t)L.K1 * P_AREP * L.Imax * 8);
+    L.tact = o; o += up256((int64_t)L.K1 * P_AREP * ((L.Imax + 1) / 2) * 8);
     L.timeline = o;
     if (d->flags & WM_FLAG_TIMELINE) o += up256((int64_t)TIMELINE_CAP * 8 * 8);
     L.total = o;
@@ -527,7 +527,11 @@ static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
     const int rpt_gu = rpt_of(gut, H), rpt_dn = rpt_of(dt, I);
     a.gu_tiles = (I + rpt_gu - 1) / rpt_gu;
     a.dn_tiles = (H + rpt_dn - 1) / rpt_dn;
-    a.gu_cap = (a.gu_tiles + nwg - 1) / nwg * rpt_gu;
+    // a hand-off word carries two SwiGLU outputs, so a workgroup's gate/up
+    // rows come in pairs: one-row tiles are split in units of two
+    a.gu_step = rpt_gu == 1 ? 2 : 1;
+    if (a.gu_tiles % a.gu_step || (rpt_gu * a.gu_step) % 2) return 1;
+    a.gu_cap = (a.gu_tiles / a.gu_step + nwg - 1) / nwg * a.gu_step * rpt_gu;
     a.y_cap = (a.dn_tiles + nwg - 1) / nwg * rpt_dn;
     a.ring_buf = std::max(std::max(ring_tile_bytes_rt(gut), ring_tile_bytes_rt(dt)),
                           std::max(ring_tile_bytes_rt(sgut), ring_tile_bytes_rt(sdt)));
@@ -563,11 +567,15 @@ static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
     }
     if (a.nstream < a.n_rwaves + 1 || a.nstream < 4) return 1;
     // act tiles: the SwiGLU outputs of a slot come into the streaming waves'
-    // rings in tiles of aseg 64-value segments (8 B tagged words each; whole
-    // K-quant super-blocks, so every tile is a contiguous column range)
-    a.aseg = a.ring_buf >= 8 * SEG * 8 ? 8 : 4;
+    // rings in tiles of aseg 64-value segments (4 B per value: two to a
+    // tagged 8-byte word; whole K-quant super-blocks, so every tile is a
+    // contiguous column range).  One wave builds a tile's records, 8
+    // segments at a time: with few slots a slot's down tiles wait for them,
+    // and 8-segment tiles let two waves share a slot; with many, the act
+    // tiles run well ahead and 16-segment tiles halve their number.
+    a.aseg = (K + (sh ? 1 : 0) >= 8 && a.ring_buf >= 16 * SEG * 4) ? 16 : 8;
     a.nact = (I / SEG + a.aseg - 1) / a.aseg;
-    if (a.nact > PMAXACT || a.aseg * SEG * 8 > a.ring_buf) return 1;
+    if (a.nact > PMAXACT || a.aseg * SEG * 4 > a.ring_buf) return 1;
     // (and more than half of a CU's LDS, so that each CU holds one workgroup)
     const int lds = std::max((o + a.nstream * PRING * a.ring_buf + 255) / 256 * 256,
                              (max_lds_per_wg() / 2 + 256) / 256 * 256);

@@ -121,6 +121,7 @@ struct PersistCtl {
 struct PersistArgs {
     int32_t H, I, E, K, has_shared, forced, nwg, rr;
     int32_t gu_tiles, dn_tiles;        // tiles of one gate/up matrix (I rows) and of one down matrix (H rows)
+    int32_t gu_step;                   // gate/up tiles are split among workgroups in units of gu_step (an even row count)
     int32_t n_rwaves;                  // streaming waves whose rings hold x and the router rows at the start
     int32_t o_ring, ring_buf, nstream; // LDS: the rings of the nstream streaming waves (PRING buffers of ring_buf bytes each)
     int32_t x_region;                  // bytes of x / of one router row in the router region
@@ -154,7 +155,7 @@ struct PersistArgs {
     uint64_t* tlogits;                 // [P_REP][E] (tag << 32) | logit bits
     uint32_t* hello;                   // [nwg] tag of the launch each workgroup started in
     uint32_t* epoch;                   // launches completed since the workspace was reset
-    uint64_t* tact;                    // [K+1][P_AREP][I] (tag << 32) | SwiGLU output bits
+    uint64_t* tact;                    // [K+1][P_AREP][I/2] (tag16 << 48) | act24(v[2i+1]) << 24 | act24(v[2i])
     uint64_t* timeline;                // NULL or [nwg][P_TL]
     uint32_t probe;                    // nonzero: every wait of the step gives up at its first unsuccessful poll
 };

@@ -59,12 +59,13 @@ int launch_shgate(const float* x, const float* g, int H, float* out, hipStream_t
 
 // ------------------------------------------------------------------ SwiGLU
 
-// act[slot][i] = silu(g[slot][i]) * u[slot][i] (gate and up of different types).
+// act[slot][i] = silu(g[slot][i]) * u[slot][i] (gate and up of different
+// types), rounded as every decode path hands it to the down projection.
 __global__ __launch_bounds__(256) void k_swiglu(const float* __restrict__ g, const float* __restrict__ u,
                                                 float* __restrict__ act, int n, int64_t stride) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     const int64_t o = (int64_t)blockIdx.y * stride + i;
-    if (i < n) act[o] = silu_mul(g[o], u[o]);
+    if (i < n) act[o] = act_round(silu_mul(g[o], u[o]));
 }
 
 int launch_swiglu(const float* g, const float* u, float* act, int n, int nslots, int64_t stride, hipStream_t s) {

@@ -16,12 +16,13 @@
 // entries in list order from an LDS counter; each loads its entry into its
 // own LDS buffer with LDS-DMA and processes it.
 //
-// Hand-offs between workgroups carry the launch tag in every 64-bit word
-// (tag << 32 | value), so a reader needs one read of the data itself and no
-// counter: the routing (every workgroup reads one replica of the tagged
-// logits and runs the K-pass arg-max itself) and the SwiGLU outputs of each
-// slot (every workgroup writes its rows into P_AREP replicas; every workgroup
-// reads one replica back in act tiles).  A stale word carries an older tag,
+// Hand-offs between workgroups carry the launch tag in every 64-bit word, so
+// a reader needs one read of the data itself and no counter: the routing
+// (logits as tag << 32 | value; every workgroup reads one replica of them
+// and runs the K-pass arg-max itself) and the SwiGLU outputs of each slot
+// (two outputs rounded to 24 bits and the tag's low 16 bits per word; every
+// workgroup writes its row pairs into P_AREP replicas and reads one replica
+// back in act tiles).  A stale word carries an older tag,
 // so a reader never takes it.  The tag is epoch + 1; workgroup 0 stores the
 // new epoch once it has seen every workgroup's start tag (so no workgroup can
 // still read the old one; the next launch begins after this one ends).
@@ -169,13 +170,15 @@ template <int T> WM_DEV int ring_dma(uint64_t G, int nbytes, int lane, lds8_t* d
 }
 
 // The DMA loads of an act tile (nbytes of tagged words, 16-byte aligned, a
-// multiple of 1 KB) into a ring buffer: the first read through the L2 (the
+// multiple of 256) into a ring buffer: the first read through the L2 (the
 // workgroups of an XCD reading one replica share its fetch), a re-read
-// (cpol CPOL_SC1) past it.  Returns the instruction count.
+// (cpol CPOL_SC1) past it.  Lanes past the tile's last 16 bytes read those
+// again (the buffer holds whole kilobytes of the tile).  Returns the
+// instruction count.
 template <int CPOL> WM_DEV int act_dma(uint64_t G, int nbytes, int lane, lds8_t* dst) {
-    const int ni = nbytes >> 10;
+    const int nch = nbytes >> 4, ni = (nch + 63) >> 6;
     for (int k = 0; k < ni; k++)
-        __builtin_amdgcn_global_load_lds((const void*)(uintptr_t)(G + 16u * (uint32_t)(lane + 64 * k)),
+        __builtin_amdgcn_global_load_lds((const void*)(uintptr_t)(G + 16u * (uint32_t)min(lane + 64 * k, nch - 1)),
                                          (__attribute__((address_space(3))) void*)(dst + 1024 * k), 16, 0, CPOL);
     return ni;
 }
@@ -192,8 +195,9 @@ struct Part {
 WM_DEV Part partition(const PersistArgs& a) {
     Part p;
     p.w = (int)blockIdx.x;
-    p.tw0 = (int)((int64_t)p.w * a.gu_tiles / a.nwg);
-    p.ngu = (int)((int64_t)(p.w + 1) * a.gu_tiles / a.nwg) - p.tw0;
+    const int gs = a.gu_step, gu_units = a.gu_tiles / gs;
+    p.tw0 = gs * (int)((int64_t)p.w * gu_units / a.nwg);
+    p.ngu = gs * (int)((int64_t)(p.w + 1) * gu_units / a.nwg) - p.tw0;
     p.d0 = (int)((int64_t)p.w * a.dn_tiles / a.nwg);
     p.ndn = (int)((int64_t)(p.w + 1) * a.dn_tiles / a.nwg) - p.d0;
     return p;
@@ -270,29 +274,40 @@ struct TileList {
 };
 
 // Act tile `at` of `slot`, landed in `buf` (nb bytes loaded from G): segments
-// [at*aseg, (at+1)*aseg) of the slot's tagged SwiGLU outputs, 8 lanes per
-// segment, 8 values per lane.  While a word still carries an older tag (its
-// producer has not published it yet) the tile is loaded again past the L2;
-// then each lane builds its part of the segment's operand record and the
-// tile is marked done for the slot's down tiles.  Act tiles travel in the
-// streaming waves' own lists: a CU's memory pipeline serves its waves in
-// turn, so these 8 KB per slot move at the streaming waves' share instead of
-// one helper wave's.
+// [at*aseg, (at+1)*aseg) of the slot's tagged SwiGLU outputs, in rounds of 8
+// segments, 8 lanes per segment, 8 values (4 words) per lane.  While a word
+// still carries an older tag (its producer has not published it yet) the
+// tile is loaded again past the L2; then each lane builds its part of the
+// segment's operand record and the tile is marked done for the slot's down
+// tiles.  Act tiles travel in the streaming waves' own lists: a CU's memory
+// pipeline serves its waves in turn, so these 4 KB per slot move at the
+// streaming waves' share instead of one helper wave's.
 template <int DT, int SDT>
 WM_DEV void act_tile(const PersistArgs& a, lctl_t* ctl, lds8_t* lds, lds8_t* buf, uint64_t G, int nb, int slot, int at,
                      int lane) {
-    const int K = a.K, nseg = a.I / SEG, part = lane & 7, s_in = lane >> 3, seg = at * a.aseg + s_in;
-    const bool on = s_in < a.aseg && seg < nseg;
+    const int K = a.K, nseg = a.I / SEG, part = lane & 7;
+    const int nround = (a.aseg + 7) >> 3;
     lds_wait(ctl, &ctl->rows_in, 1u, a.status, lane);        // the tag is set before rows_in
-    const uint32_t tag = ctl->tag;
-    const int col = on ? (slot == K ? seg_col(SDT, seg, 8 * part) : seg_col(DT, seg, 8 * part)) : 0;
-    const lds64_t* w = (const lds64_t*)buf + (on ? col - at * a.aseg * SEG : 0);
+    const uint32_t tag16 = ctl->tag & 0xFFFFu;
+    // segment of round rd for this lane (or -1) and its 4 words in the buffer
+    auto seg_of = [&](int rd) -> int {
+        const int s_in = 8 * rd + (lane >> 3), seg = at * a.aseg + s_in;
+        return s_in < a.aseg && seg < nseg ? seg : -1;
+    };
+    auto words = [&](int seg) -> const lds64_t* {
+        const int col = slot == K ? seg_col(SDT, seg, 8 * part) : seg_col(DT, seg, 8 * part);
+        return (const lds64_t*)buf + (col - at * a.aseg * SEG) / 2;
+    };
     uint32_t it = 0;
     while (true) {
         bool ok = true;
-        if (on) {
+        for (int rd = 0; rd < nround; rd++) {
+            const int seg = seg_of(rd);
+            if (seg >= 0) {
+                const lds64_t* w = words(seg);
 #pragma unroll
-            for (int j = 0; j < 8; j++) ok = ok && (uint32_t)(w[j] >> 32) == tag;
+                for (int j = 0; j < 4; j++) ok = ok && (uint32_t)(w[j] >> 48) == tag16;
+            }
         }
         if (__builtin_amdgcn_ballot_w64(!ok) == 0ull) break;
         if (++it > PSPIN_G || aborted(ctl)) {
@@ -304,13 +319,21 @@ WM_DEV void act_tile(const PersistArgs& a, lctl_t* ctl, lds8_t* lds, lds8_t* buf
         act_dma<CPOL_SC1>(G, nb, lane, buf);
         WM_WAIT_VMCNT(0);
     }
-    if (on) {
-        float v[8];
+    for (int rd = 0; rd < nround; rd++) {
+        const int seg = seg_of(rd);
+        if (seg >= 0) {
+            const lds64_t* w = words(seg);
+            float v[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = __builtin_bit_cast(float, (uint32_t)w[j]);
-        lds32_t* rec = (lds32_t*)(lds + a.o_reg) + ((int64_t)slot * nseg + seg) * XOP_DW;
-        if (slot == K) xop_part<SDT>(v, part, rec);
-        else xop_part<DT>(v, part, rec);
+            for (int j = 0; j < 4; j++) {
+                const uint64_t x = w[j];
+                v[2 * j] = act_float((uint32_t)x & 0xFFFFFFu);
+                v[2 * j + 1] = act_float((uint32_t)(x >> 24) & 0xFFFFFFu);
+            }
+            lds32_t* rec = (lds32_t*)(lds + a.o_reg) + ((int64_t)slot * nseg + seg) * XOP_DW;
+            if (slot == K) xop_part<SDT>(v, part, rec);
+            else xop_part<DT>(v, part, rec);
+        }
     }
     lds_set(&ctl->act_done[slot][at], 1u, lane);
 }
@@ -349,15 +372,15 @@ WM_DEV TileDesc tile_desc(const PersistArgs& a, const Part& P, const TRef& r, in
     const int K = a.K, H = a.H, I = a.I;
     if (r.kind == K_ACT) {
         // segments [t*aseg, (t+1)*aseg) of the slot's tagged SwiGLU outputs in
-        // replica w % P_AREP (byte offset from a.tact)
+        // replica w % P_AREP (byte offset from a.tact; a word holds two outputs)
         TileDesc d;
         const int seg0 = r.t * a.aseg;
         d.kind = K_ACT;
         d.slot = r.slot;
         d.rows = 0;
         d.out = r.t;
-        d.off = ((int64_t)(r.slot * P_AREP + P.w % P_AREP) * I + (int64_t)seg0 * SEG) * 8;
-        d.nb = min(a.aseg, I / SEG - seg0) * SEG * 8;
+        d.off = ((int64_t)(r.slot * P_AREP + P.w % P_AREP) * (I / 2) + (int64_t)seg0 * (SEG / 2)) * 8;
+        d.nb = min(a.aseg, I / SEG - seg0) * SEG * 4;
         return d;
     }
     const bool gu = r.kind <= K_RU;
@@ -917,6 +940,11 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
     }
     lds_wait(ctl, &ctl->rows_in, 1u, a.status, lane);
     const uint32_t tag = ctl->tag;
+    // The SwiGLU hand-off words carry the tag's low 16 bits: every launch of
+    // the layer rewrites every word a launch can read (each slot's I
+    // outputs in every replica, an invalid pick's as zeros), so a word is
+    // at most one launch old and never carries the current 16 bits stale.
+    const uint64_t tg16 = (uint64_t)(tag & 0xFFFFu) << 48;
     if (!a.forced) {
         const int r0 = P.w * a.rr, nr = max(0, min(a.rr, a.E - r0));
         if (nr > 1) router_chains(lds + a.o_router, a.x_region, a.H, r0, 1, nr > 3 ? 3 : -1, a.E, tag, a.tlogits, lane);
@@ -941,12 +969,17 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
             __builtin_amdgcn_s_setprio(2);
             if (lane == 0 && q < 12) ctl->t[16 + q] = now();
             const bool valid = slot == K || ctl->valid[slot] != 0;
-            uint64_t* dst = a.tact + (int64_t)slot * P_AREP * a.I + row0;
-            // rows x replicas over the lanes, one tagged word each
-            for (int i = lane; i < nrows * P_AREP; i += 64) {
-                const int r = i / P_AREP, rp = i - r * P_AREP;
-                const float v = valid ? silu_mul(garr[slot * a.gu_cap + r], uarr[slot * a.gu_cap + r]) : 0.0f;
-                gst_agent64(dst + (int64_t)rp * a.I + r, tagged(tag, v));
+            uint64_t* dst = a.tact + (int64_t)slot * P_AREP * (a.I / 2) + row0 / 2;
+            // rows x replicas over the lanes (one output each); the lane of
+            // an even row takes the next row's code from the lane P_AREP up
+            // and stores the pair as one tagged word (row0 and nrows are
+            // even, and 64 lanes hold whole pairs)
+            for (int i0 = 0; i0 < nrows * P_AREP; i0 += 64) {
+                const int i = i0 + lane, r = i / P_AREP, rp = i - r * P_AREP, o = slot * a.gu_cap + r;
+                const bool in = i < nrows * P_AREP;
+                const uint32_t c = act24(in && valid ? silu_mul(garr[o], uarr[o]) : 0.0f);
+                const uint32_t c1 = (uint32_t)__shfl_down((int)c, P_AREP);
+                if (in && !(r & 1)) gst_agent64(dst + (int64_t)rp * (a.I / 2) + r / 2, tg16 | ((uint64_t)c1 << 24) | c);
             }
             __builtin_amdgcn_s_setprio(0);
         }

@@ -75,6 +75,19 @@ WM_DEV float silu_mul(float g, float u) {
     return g * sg * u;
 }
 
+// The SwiGLU output as the decode path's down projection takes it: fp32
+// rounded to a 16-bit significand (the low 8 bits of the pattern, to nearest
+// even: relative error <= 2^-17; an infinity stays, a NaN becomes a quiet
+// NaN of the same sign), so that two of them and a 16-bit tag fit in one
+// 64-bit hand-off word.  act24 is the 24-bit code, act_float its value.
+WM_DEV uint32_t act24(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 8) | 0x400000u;
+    return (u + 0x7Fu + ((u >> 8) & 1u)) >> 8;
+}
+WM_DEV float act_float(uint32_t c) { return __builtin_bit_cast(float, c << 8); }
+WM_DEV float act_round(float v) { return act_float(act24(v)); }
+
 WM_DEV float sigmoid_stable(float v) {
     if (v >= 0.0f) return 1.0f / (1.0f + expf(-v));
     float z = expf(v);
@@ -222,7 +235,8 @@ WM_DEV void wg_gateup_item(const uint8_t* Wg, const uint8_t* Wu, int rows, int i
         wave_stream<T, RING_S, COH>(W, rows, g, t0, t1, x, (lds8_t*)(lds + wave * RING_S * BUF), nullptr,
                                     wave < 2 ? garr : uarr, r0, lane);
     __syncthreads();
-    for (int r = threadIdx.x; r < r1 - r0; r += 256) gst<COH>(act + r0 + r, (Wg && Wu) ? silu_mul(garr[r], uarr[r]) : 0.0f);
+    for (int r = threadIdx.x; r < r1 - r0; r += 256)
+        gst<COH>(act + r0 + r, (Wg && Wu) ? act_round(silu_mul(garr[r], uarr[r])) : 0.0f);
     __syncthreads();
 }
 
