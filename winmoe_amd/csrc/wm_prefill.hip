@@ -158,6 +158,11 @@ WM_DEV int2 block_excl_scan2(int2 v, int* wsum, int2* tot) {
     return make_int2(before.x + inc.x - v.x, before.y + inc.y - v.y);
 }
 
+// Sizes for which k_pf_group keeps its data on chip: the pairs' expert ids
+// in registers (up to PG_REG per thread), the sorted pair list and the
+// tokens' exponents in LDS; larger batches read them from global memory.
+constexpr int PG_REG = 8, PG_SORT = 10240, PG_XEXP = 2048;
+
 // One workgroup: pairs grouped by expert (order inside an expert is free:
 // every pair's output row is computed independently of the others), then
 // cut into pass records: routed passes first, in expert order, then the
@@ -171,13 +176,28 @@ __global__ __launch_bounds__(1024) void k_pf_group(const int32_t* __restrict__ i
     __shared__ int off[1026];
     __shared__ int pbase[1026];
     __shared__ int wsum[32];
+    __shared__ int srt[PG_SORT];
+    __shared__ int xe[PG_XEXP];
     const int tid = threadIdx.x, P = T * K, G = E + 1;      // group E: the shared expert (empty without one)
+    const bool reg = P <= 1024 * PG_REG, lsort = P + (has_shared ? T : 0) <= PG_SORT, lxe = T <= PG_XEXP;
+    // the ids and exponents are read once, together
+    int ev[PG_REG];
+#pragma unroll
+    for (int i = 0; i < PG_REG; i++) ev[i] = reg && tid + 1024 * i < P ? ids[tid + 1024 * i] : -1;
+    if (lxe)
+        for (int t = tid; t < T; t += 1024) xe[t] = xexp[t];
     for (int e = tid; e < E; e += 1024) cnt[e] = 0;
     if (tid == 0) cnt[E] = has_shared ? T : 0;
     __syncthreads();
-    for (int p = tid; p < P; p += 1024) {
-        const int e = ids[p];
-        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    if (reg) {
+#pragma unroll
+        for (int i = 0; i < PG_REG; i++)
+            if (ev[i] >= 0 && ev[i] < E) atomicAdd(&cnt[ev[i]], 1);
+    } else {
+        for (int p = tid; p < P; p += 1024) {
+            const int e = ids[p];
+            if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+        }
     }
     __syncthreads();
     // pair offsets and pass bases of the groups, 1024 groups per round
@@ -205,12 +225,32 @@ __global__ __launch_bounds__(1024) void k_pf_group(const int32_t* __restrict__ i
         pass_count[0] = pbase[E];
         pass_count[1] = pbase[G] - pbase[E];
     }
-    for (int p = tid; p < P; p += 1024) {
-        const int e = ids[p];
-        if (e >= 0 && e < E) sorted[atomicAdd(&cnt[e], 1)] = p;
+    // the sorted list: in LDS when it fits, else in global memory
+    if (reg) {
+#pragma unroll
+        for (int i = 0; i < PG_REG; i++) {
+            const int e = ev[i], p = tid + 1024 * i;
+            if (e >= 0 && e < E) {
+                const int pos = atomicAdd(&cnt[e], 1);
+                if (lsort) srt[pos] = p;
+                else sorted[pos] = p;
+            }
+        }
+    } else {
+        for (int p = tid; p < P; p += 1024) {
+            const int e = ids[p];
+            if (e >= 0 && e < E) {
+                const int pos = atomicAdd(&cnt[e], 1);
+                if (lsort) srt[pos] = p;
+                else sorted[pos] = p;
+            }
+        }
     }
     if (has_shared)
-        for (int t = tid; t < T; t += 1024) sorted[off[E] + t] = P + t;
+        for (int t = tid; t < T; t += 1024) {
+            if (lsort) srt[off[E] + t] = P + t;
+            else sorted[off[E] + t] = P + t;
+        }
     __syncthreads();
     // one thread per pass: its group by binary search over the pass bases
     const int npass = pbase[G];
@@ -230,15 +270,18 @@ __global__ __launch_bounds__(1024) void k_pf_group(const int32_t* __restrict__ i
         rec[3] = 0;
         int prs[GM_M];
 #pragma unroll
-        for (int m = 0; m < GM_M; m++) prs[m] = sorted[first + min(m, mn - 1)];
+        for (int m = 0; m < GM_M; m++) {
+            const int at = first + min(m, mn - 1);
+            prs[m] = lsort ? srt[at] : sorted[at];
+        }
 #pragma unroll
         for (int m4 = 0; m4 < GM_M / 4; m4++) {
             uint32_t ex = 0;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const int pr = prs[4 * m4 + j];
+                const int pr = prs[4 * m4 + j], tok = pair_token(pr, T, K);
                 rec[4 + 4 * m4 + j] = pr;
-                ex |= (uint32_t)(xexp[pair_token(pr, T, K)] & 0xFF) << (8 * j);
+                ex |= (uint32_t)((lxe ? xe[tok] : xexp[tok]) & 0xFF) << (8 * j);
             }
             rec[4 + GM_M + m4] = (int32_t)ex;
         }
