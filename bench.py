@@ -70,7 +70,7 @@ def host_info():
             "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
 
 
-# ------------------------------------------------------------------ algorithmic bytes (rooflines)
+# ------------------------------------------------------------------ algorithmic bytes (the rooflines' numerators)
 
 def decode_layer_bytes(cfg) -> int:
     """One decode token through one layer: every expert weight byte touched (K

@@ -1,7 +1,7 @@
 """ctypes access to the CPU oracle (liboracle.so) and the reference build (_ref/libwmref.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, ``__graft_entry__.smoke()`` and
-bench.py's cpu_baseline leg, as the checker.  The product package never imports
+bench.py's cpu_baseline leg, as the parity reference.  The product package never imports
 this module.
 """
 from __future__ import annotations

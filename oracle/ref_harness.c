@@ -256,8 +256,9 @@ REF_API int ref_moe_layer_cpu(const wmo_layer* L, const float* normed, const int
         }
     }
     if (L->sh_gate && L->sh_up && L->sh_down) {
-        /* The reference sizes the shared expert with the routed I (Appendix B
-         * item 7 of the survey); the configs here have I_shared == I. */
+        /* The reference sizes the shared expert with the routed I
+         * (winmoe_inference.c:1992-1993, 2002); the configs here have
+         * I_shared == I. */
         int Is = L->I_shared > 0 ? L->I_shared : I;
         ref_matvec(gate_buf, L->sh_gate, normed, Is, H, L->sh_gate_type);
         ref_matvec(up_buf, L->sh_up, normed, Is, H, L->sh_up_type);

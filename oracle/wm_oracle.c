@@ -1,8 +1,8 @@
 /*
  * wm_oracle.c -- CPU oracle for the WinMoE MoE expert-layer hot path.
  *
- * TEST INFRASTRUCTURE ONLY (see wm_oracle.h): the checker the HIP path is
- * compared against, never the product.  Built with -ffp-contract=off so the
+ * TEST INFRASTRUCTURE ONLY (see wm_oracle.h): the parity reference the HIP
+ * path is compared against, never the product.  Built with -ffp-contract=off so the
  * fp32 expressions below round exactly as written (the dequant products are
  * exact in fp32 either way; see the per-format notes).
  *

@@ -2,8 +2,8 @@
  * wm_oracle.h -- CPU oracle for the WinMoE MoE expert-layer hot path.
  *
  * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py may load this library, and only as the checker
- * (or, for the baseline, as the timed CPU restatement).  The product path in
+ * cpu_baseline leg of bench.py may load this library, and only as the parity
+ * reference (or, for the baseline, as the timed CPU restatement).  The product path in
  * winmoe_amd/ never calls it.
  *
  * Plain C, scalar, single-threaded unless noted.  Each function cites the

@@ -91,7 +91,7 @@ def test_q4k_known_answer_480(orc):
 
 
 def test_q6k_avx2_vs_scalar_relation(orc):
-    """test/q6k_parity.cpp:78-135 with this build's own generator."""
+    """test/q6k_parity.cpp:78-135, with random blocks from numpy in place of its generator."""
     R = orc.ref()
     if R is None:
         pytest.skip("reference build not available on this host")
