@@ -78,18 +78,17 @@ template <> struct Seg<Q8_0> {
     WM_DEV int run_of(int j) const { return j >> 5; }
 };
 
-// Q4_K / Q5_K 6-bit scale and min of sub-block i (q4k_dequant.h:43-60).
+// Q4_K / Q5_K 6-bit scale and min of sub-block i (q4k_dequant.h:43-60), the
+// 12 scale bytes being s0, s1, s2: i < 4 takes byte i of s0 (scale) and of
+// s1 (min); i >= 4 takes byte j = i - 4 of s2 (low nibbles) and the top two
+// bits of byte j of s0 and of s1.  Shifts and one select, so a lane-varying
+// i indexes no register array.
 WM_DEV void k45_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int i, int& sc, int& m) {
-    uint32_t sb[12] = {byte_of(s0, 0), byte_of(s0, 1), byte_of(s0, 2), byte_of(s0, 3),
-                       byte_of(s1, 0), byte_of(s1, 1), byte_of(s1, 2), byte_of(s1, 3),
-                       byte_of(s2, 0), byte_of(s2, 1), byte_of(s2, 2), byte_of(s2, 3)};
-    if (i < 4) {
-        sc = (int)(sb[i] & 63);
-        m = (int)(sb[i + 4] & 63);
-    } else {
-        sc = (int)((sb[i + 4] & 0xF) | ((sb[i - 4] >> 6) << 4));
-        m = (int)((sb[i + 4] >> 4) | ((sb[i] >> 6) << 4));
-    }
+    const uint32_t sh = 8u * (uint32_t)(i & 3);
+    const uint32_t b0 = (s0 >> sh) & 0xFFu, b1 = (s1 >> sh) & 0xFFu, b2 = (s2 >> sh) & 0xFFu;
+    const bool lo = i < 4;
+    sc = (int)(lo ? (b0 & 63u) : ((b2 & 0xFu) | ((b0 >> 6) << 4)));
+    m = (int)(lo ? (b1 & 63u) : ((b2 >> 4) | ((b1 >> 6) << 4)));
 }
 
 // Q4_K: lane l -> block l/4, chunk c = l%4 (32 qs bytes): low nibbles are
