@@ -347,6 +347,45 @@ def test_fused_step_matches_multi_kernel(wm, name, E, tokens, kernel):
     assert fused.status() == 0 and multi.status() == 0
 
 
+
+@pytest.mark.parametrize("H,I,K,shared", [(256, 64, 2, True), (512, 128, 3, False), (1024, 256, 4, True),
+                                          (4096, 64, 8, True), (2048, 128, 10, False)])
+def test_decode_narrow_intermediate(wm, orc, H, I, K, shared):
+    """Narrow intermediate widths: a slot's SwiGLU hand-off (two outputs per
+    tagged word) is one act tile of 256 or 512 bytes, less than one DMA
+    kilobyte; with 8 slots or more the act tiles hold 16 segments.  Decode
+    against the oracle, the fused step against the per-phase kernels bit for
+    bit, and a decode with a fused RMSNorm (which only the persistent kernel
+    runs) against the plain decode of the normalised input."""
+    import torch
+    from winmoe_amd import synth
+    from winmoe_amd.moe import MoELayer
+    E = 32
+    cfg = synth.LayerConfig(f"narrow_h{H}_i{I}_k{K}", E=E, K=K, H=H, I=I, types=(Q8_0, Q8_0, Q8_0),
+                            shared_types=(Q8_0, Q8_0, Q8_0) if shared else None, shared_inter=I if shared else 0,
+                            shared_gate_inp=shared, tokens=1, seed=11)
+    sl = decode_check(wm, orc, cfg, E=E, tokens=3)
+    fused = synth.twin_layer(sl, multi_kernel=False, flags=_KERNEL_FLAGS["persist"])
+    multi = synth.twin_layer(sl, multi_kernel=True)
+    X = synth.make_hidden(cfg, tokens=3, seed_offset=5)
+    for t in range(3):
+        case(f"narrow H={H} I={I} K={K} fused vs multi token={t}")
+        a = host(fused.decode(X[t]))
+        b = host(multi.decode(X[t]))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), t
+    g = torch.Generator(device="cuda").manual_seed(3)
+    w = (1.0 + 0.1 * torch.randn(H, generator=g, device="cuda")).float()
+    normed = MoELayer(H, I, E, K, sl.router, sl.gate, sl.up, sl.down, cfg.types, shared=sl.shared, max_tokens=4,
+                      norm_w=w, add_residual=False)
+    h = (3.0 * torch.randn(H, generator=g, device="cuda")).contiguous()
+    hh = host(h)
+    assert kernel_order_scale(hh, H).view(np.uint32) == reference_order_scale(hh, H).view(np.uint32)
+    case(f"narrow H={H} I={I} K={K} rmsnorm")
+    got = host(normed.decode(h))
+    want = host(fused.decode(dev(orc.rmsnorm(hh, host(w)))))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert normed.status() == 0 and fused.status() == 0 and multi.status() == 0
+
 # ------------------------------------------------------------------ prefill
 
 def _pf_cfg(E, K, H, I, shared=False, routing="router"):
