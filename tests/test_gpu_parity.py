@@ -386,6 +386,43 @@ def test_decode_narrow_intermediate(wm, orc, H, I, K, shared):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     assert normed.status() == 0 and fused.status() == 0 and multi.status() == 0
 
+
+@pytest.mark.parametrize("E,K", [(64, 4), (512, 10), (1000, 16)])
+def test_decode_routing_ties_and_nan_row(wm, orc, E, K):
+    """The persistent step's routing with planted ties (rows 0 and E-1 copy
+    the token's top row: equal logits go to the smaller index first) and a
+    router row holding a NaN (never picked), at one key per lane (E=64),
+    eight (E=512) and sixteen (E=1000): ids as the oracle's K-pass arg-max,
+    weights within 2 ulp, output bit for bit as the per-phase kernels'."""
+    import torch
+    from winmoe_amd import synth
+    cfg = synth.LayerConfig(f"ties_e{E}_k{K}", E=E, K=K, H=1024, I=256, types=(Q8_0, Q8_0, Q8_0),
+                            shared_types=(Q8_0, Q8_0, Q8_0), shared_inter=256, shared_gate_inp=True, tokens=1,
+                            seed=21)
+    sl = synth.build_layer(cfg, E=E, max_tokens=4)
+    X = synth.make_hidden(cfg, tokens=2, seed_offset=9)
+    xh = host(X[0])
+    W = host(sl.router).copy()
+    top = int(np.argmax(W.astype(np.float64) @ xh.astype(np.float64)))
+    W[0] = W[top]
+    W[E - 1] = W[top]
+    W[E // 3, 7] = np.nan
+    sl.router.copy_(torch.from_numpy(W).to(sl.router.device))
+    multi = synth.twin_layer(sl, multi_kernel=True)
+    for t in range(2):
+        case(f"ties E={E} K={K} token={t}")
+        out = host(sl.layer.decode(X[t]))
+        ids_t, w_t = sl.layer.trace()
+        oid, ow, ref = oracle_token(orc, sl, host(X[t]))
+        assert host(ids_t[t]).tolist() == oid.tolist(), t
+        assert E // 3 not in oid.tolist()
+        assert ulp_diff(host(w_t[t]), ow).max() <= 2
+        assert rel_l2(out, ref) <= LAYER_TOL
+        assert np.array_equal(out.view(np.uint32), host(multi.decode(X[t])).view(np.uint32)), t
+    tied = sorted({0, top, E - 1})
+    assert host(sl.layer.trace()[0][0])[:len(tied)].tolist() == tied
+    assert sl.layer.status() == 0 and multi.status() == 0
+
 # ------------------------------------------------------------------ prefill
 
 def _pf_cfg(E, K, H, I, shared=False, routing="router"):
