@@ -965,14 +965,16 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
     lf32_t* garr = (lf32_t*)(lds + a.o_gu);
     lf32_t* uarr = garr + (K + 1) * a.gu_cap;
     lf32_t* yarr = (lf32_t*)(lds + a.o_y);
-    TileList L;
-    L.init(a, P.ngu, P.ndn, lane);
+    // the counts of this workgroup's list (TileList: per slot, 2 * ngu gate/up
+    // tiles, nact act tiles when it has down rows, ndn down tiles); building
+    // the list itself here took ~2 us of this wave's time
+    const int n_gu = 2 * P.ngu, n_all = nq * (n_gu + (P.ndn > 0 ? a.nact : 0) + P.ndn);
     if (P.ngu > 0) {
         const int rpt = geometry(GUT, a.H).rpt;
         const int row0 = P.tw0 * rpt, nrows = min(a.I, (P.tw0 + P.ngu) * rpt) - row0;
         for (int q = 0; q < nq; q++) {
             const int slot = slot_at(q, K, sh);
-            lds_wait(ctl, &ctl->gu_done[slot], (uint32_t)L.g, a.status, lane);
+            lds_wait(ctl, &ctl->gu_done[slot], (uint32_t)n_gu, a.status, lane);
             __builtin_amdgcn_s_setprio(2);
             if (lane == 0 && q < 12) ctl->t[16 + q] = now();
             const bool valid = slot == K || ctl->valid[slot] != 0;
@@ -1004,7 +1006,7 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
             vk[k] = k < K && ctl->valid[k] != 0;
             wk[k] = k < K ? ctl->w[k] : 0.0f;
         }
-        lds_wait(ctl, &ctl->n_done, (uint32_t)L.n, a.status, lane);     // every entry is processed
+        lds_wait(ctl, &ctl->n_done, (uint32_t)n_all, a.status, lane);   // every entry is processed
         if (lane == 0) ctl->t[6] = now();
         for (int r = lane; r < nrows; r += 64) {
             // out[h] = sum_k w_k y_k[h] (k order, invalid ids skipped) + gate * y_shared[h]
