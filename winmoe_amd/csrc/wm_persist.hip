@@ -609,13 +609,49 @@ WM_DEV void router_dma(const float* x, const float* W, int H, int r0, int qa, in
     WM_WAIT_VMCNT(0);
 }
 
+// NB blocks of 8 reference-order FMA steps (block b: this lane's columns
+// 128 b + 16 j from wp / xp, one base address per block and immediate
+// offsets, the LDS reads paired two to an instruction, 8 per block).  The
+// blocks are unrolled with three register sets in rotation: the reads of
+// blocks b + 1 and b + 2 are in flight while block b's FMAs run, so those
+// FMAs wait only for reads sent two blocks earlier.  (The LDS counter tracks
+// 15 instructions: a loop over 16-step blocks in two sets waited for reads
+// just sent, and a rolled loop's copies of carried registers waited for all.)
+template <int NB> WM_DEV float rc_blocks(const lf32_t* wp, const lf32_t* xp) {
+    float acc = 0.0f;
+    float w[3][8], x[3][8];
+#pragma unroll
+    for (int b = 0; b < NB + 2; b++) {
+        if (b < NB) {
+            // block b's base addresses pass through an empty asm that takes
+            // the running sum after block b - 3: no pass can hoist the reads
+            // above those FMAs (a memory clobber or a scheduling barrier alone
+            // does not hold LDS reads in straight-line code), and the
+            // scheduling barrier below keeps them ahead of block b - 2's FMAs
+            const lf32_t* wq = wp;
+            const lf32_t* xq = xp;
+            if (b >= 3) asm volatile("" : "+v"(wq), "+v"(xq) : "v"(acc));
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                w[b % 3][j] = wq[128 * b + 16 * j];
+                x[b % 3][j] = xq[128 * b + 16 * j];
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (b >= 2) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc = fmaf(w[(b - 2) % 3][j], x[(b - 2) % 3][j], acc);
+        }
+    }
+    return acc;
+}
+
 // Router logits of up to two of the rows in LDS: lanes 16i .. 16i+15 take row
 // rsel i (none when < 0), in the reference order (transformer.h:172-191; as
 // wg_router_rows): lane c of a row keeps the running fp32 FMA over columns
 // c, c+16, ...; xor tree 8, 4, 2, 1 over the 16 lanes; lane 0 of the row adds
-// the scalar tail.  The LDS reads of the next 16 steps are issued before the
-// FMAs of the current ones.  Each logit goes with the tag in its upper 32
-// bits into all P_REP replicas (lane r of the row stores replica r).
+// the scalar tail.  Each logit goes with the tag in its upper 32 bits into
+// all P_REP replicas (lane r of the row stores replica r).
 WM_DEV void router_chains(const lds8_t* lx, int region, int H, int r0, int ra, int rb, int E, uint32_t tag,
                           uint64_t* tlogits, int lane) {
     const int q = lane >> 4, c = lane & 15;
@@ -623,43 +659,21 @@ WM_DEV void router_chains(const lds8_t* lx, int region, int H, int r0, int ra, i
     if (row < 0) return;                            // (idle lanes take no LDS bandwidth)
     const lf32_t* xr = (const lf32_t*)lx;
     const lf32_t* wr = (const lf32_t*)(lx + (1 + (row >= 0 ? row : 0)) * region);
-    const int H16 = H - (H & 15), nsteps = H16 / 16, nblk = nsteps / 16;
+    const int H16 = H - (H & 15), nsteps = H16 / 16;
+    // H = 64 * 2^k: 8-step blocks for every step from H = 128 on (any other
+    // count goes through the scalar loop below)
+    int done = 0;
     float acc = 0.0f;
-    // block b: steps 16 b .. 16 b + 15, this lane's columns c + 256 b + 16 j:
-    // one base address per block and immediate offsets (the LDS reads pair up
-    // two to an instruction); the next block's reads are issued before the
-    // current block's FMAs, alternating two register sets
-    const lf32_t* wp = wr + c;
-    const lf32_t* xp = xr + c;
-    if (nblk > 0) {
-        float wa[16], xa[16], wb[16], xb[16];
-#define WM_RC_LOAD(blk, W, X)                                                  \
-    {                                                                          \
-        const lf32_t* wn_ = wp + 256 * (blk);                                  \
-        const lf32_t* xn_ = xp + 256 * (blk);                                  \
-        _Pragma("unroll") for (int j = 0; j < 16; j++) {                       \
-            W[j] = wn_[16 * j];                                                \
-            X[j] = xn_[16 * j];                                                \
-        }                                                                      \
+    switch (nsteps) {
+    case 256: acc = rc_blocks<32>(wr + c, xr + c); done = 256; break;
+    case 128: acc = rc_blocks<16>(wr + c, xr + c); done = 128; break;
+    case 64: acc = rc_blocks<8>(wr + c, xr + c); done = 64; break;
+    case 32: acc = rc_blocks<4>(wr + c, xr + c); done = 32; break;
+    case 16: acc = rc_blocks<2>(wr + c, xr + c); done = 16; break;
+    case 8: acc = rc_blocks<1>(wr + c, xr + c); done = 8; break;
+    default: break;
     }
-#define WM_RC_FMA(W, X) _Pragma("unroll") for (int j = 0; j < 16; j++) acc = fmaf(W[j], X[j], acc);
-        WM_RC_LOAD(0, wa, xa)
-        int b = 0;
-        // (the compiler barriers keep each block's reads ahead of the FMAs
-        // of the block before it)
-        for (; b + 2 <= nblk; b += 2) {
-            WM_RC_LOAD(b + 1, wb, xb)
-            asm volatile("" ::: "memory");
-            WM_RC_FMA(wa, xa)
-            WM_RC_LOAD(min(b + 2, nblk - 1), wa, xa)       // (a repeat at the end is never used)
-            asm volatile("" ::: "memory");
-            WM_RC_FMA(wb, xb)
-        }
-        if (b < nblk) WM_RC_FMA(wa, xa)                    // an odd block count: the last block
-#undef WM_RC_FMA
-#undef WM_RC_LOAD
-    }
-    for (int s = 16 * nblk; s < nsteps; s++) acc = fmaf(wr[c + 16 * s], xr[c + 16 * s], acc);
+    for (int s = done; s < nsteps; s++) acc = fmaf(wr[c + 16 * s], xr[c + 16 * s], acc);
     acc += dpp_f32<DPP_ROR8>(acc);
     acc += dpp_f32<DPP_ROR4>(acc);
     acc += dpp_f32<DPP_ROR2>(acc);
