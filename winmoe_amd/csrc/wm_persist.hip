@@ -609,43 +609,6 @@ WM_DEV void router_dma(const float* x, const float* W, int H, int r0, int qa, in
     WM_WAIT_VMCNT(0);
 }
 
-// NB blocks of 8 reference-order FMA steps (block b: this lane's columns
-// 128 b + 16 j from wp / xp, one base address per block and immediate
-// offsets, the LDS reads paired two to an instruction, 8 per block).  The
-// blocks are unrolled with three register sets in rotation: the reads of
-// blocks b + 1 and b + 2 are in flight while block b's FMAs run, so those
-// FMAs wait only for reads sent two blocks earlier.  (The LDS counter tracks
-// 15 instructions: a loop over 16-step blocks in two sets waited for reads
-// just sent, and a rolled loop's copies of carried registers waited for all.)
-template <int NB> WM_DEV float rc_blocks(const lf32_t* wp, const lf32_t* xp) {
-    float acc = 0.0f;
-    float w[3][8], x[3][8];
-#pragma unroll
-    for (int b = 0; b < NB + 2; b++) {
-        if (b < NB) {
-            // block b's base addresses pass through an empty asm that takes
-            // the running sum after block b - 3: no pass can hoist the reads
-            // above those FMAs (a memory clobber or a scheduling barrier alone
-            // does not hold LDS reads in straight-line code), and the
-            // scheduling barrier below keeps them ahead of block b - 2's FMAs
-            const lf32_t* wq = wp;
-            const lf32_t* xq = xp;
-            if (b >= 3) asm volatile("" : "+v"(wq), "+v"(xq) : "v"(acc));
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                w[b % 3][j] = wq[128 * b + 16 * j];
-                x[b % 3][j] = xq[128 * b + 16 * j];
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        if (b >= 2) {
-#pragma unroll
-            for (int j = 0; j < 8; j++) acc = fmaf(w[(b - 2) % 3][j], x[(b - 2) % 3][j], acc);
-        }
-    }
-    return acc;
-}
-
 // Router logits of up to two of the rows in LDS: lanes 16i .. 16i+15 take row
 // rsel i (none when < 0), in the reference order (transformer.h:172-191; as
 // wg_router_rows): lane c of a row keeps the running fp32 FMA over columns
@@ -660,19 +623,8 @@ WM_DEV void router_chains(const lds8_t* lx, int region, int H, int r0, int ra, i
     const lf32_t* xr = (const lf32_t*)lx;
     const lf32_t* wr = (const lf32_t*)(lx + (1 + (row >= 0 ? row : 0)) * region);
     const int H16 = H - (H & 15), nsteps = H16 / 16;
-    // H = 64 * 2^k: 8-step blocks for every step from H = 128 on (any other
-    // count goes through the scalar loop below)
-    int done = 0;
-    float acc = 0.0f;
-    switch (nsteps) {
-    case 256: acc = rc_blocks<32>(wr + c, xr + c); done = 256; break;
-    case 128: acc = rc_blocks<16>(wr + c, xr + c); done = 128; break;
-    case 64: acc = rc_blocks<8>(wr + c, xr + c); done = 64; break;
-    case 32: acc = rc_blocks<4>(wr + c, xr + c); done = 32; break;
-    case 16: acc = rc_blocks<2>(wr + c, xr + c); done = 16; break;
-    case 8: acc = rc_blocks<1>(wr + c, xr + c); done = 8; break;
-    default: break;
-    }
+    float acc;
+    const int done = rc_steps(wr + c, xr + c, nsteps, acc);
     for (int s = done; s < nsteps; s++) acc = fmaf(wr[c + 16 * s], xr[c + 16 * s], acc);
     acc += dpp_f32<DPP_ROR8>(acc);
     acc += dpp_f32<DPP_ROR4>(acc);

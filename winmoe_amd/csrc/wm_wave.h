@@ -303,6 +303,58 @@ WM_HD int router_rows_per_wg(int H, bool aligned) {
     return n < 1 ? 0 : (n > 4 ? 4 : n);
 }
 
+// NB blocks of 8 reference-order FMA steps (block b: this lane's columns
+// 128 b + 16 j from wp / xp, one base address per block and immediate
+// offsets, the LDS reads paired two to an instruction, 8 per block).  The
+// blocks are unrolled with three register sets in rotation: the reads of
+// blocks b + 1 and b + 2 are in flight while block b's FMAs run, so those
+// FMAs wait only for reads sent two blocks earlier.  (The LDS counter tracks
+// 15 instructions: a loop over 16-step blocks in two sets waited for reads
+// just sent, and a rolled loop's copies of carried registers waited for all.)
+template <int NB> WM_DEV float rc_blocks(const lf32_t* wp, const lf32_t* xp) {
+    float acc = 0.0f;
+    float w[3][8], x[3][8];
+#pragma unroll
+    for (int b = 0; b < NB + 2; b++) {
+        if (b < NB) {
+            // block b's base addresses pass through an empty asm that takes
+            // the running sum after block b - 3: no pass can hoist the reads
+            // above those FMAs (a memory clobber or a scheduling barrier alone
+            // does not hold LDS reads in straight-line code), and the
+            // scheduling barrier below keeps them ahead of block b - 2's FMAs
+            const lf32_t* wq = wp;
+            const lf32_t* xq = xp;
+            if (b >= 3) asm volatile("" : "+v"(wq), "+v"(xq) : "v"(acc));
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                w[b % 3][j] = wq[128 * b + 16 * j];
+                x[b % 3][j] = xq[128 * b + 16 * j];
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (b >= 2) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc = fmaf(w[(b - 2) % 3][j], x[(b - 2) % 3][j], acc);
+        }
+    }
+    return acc;
+}
+
+// The steps of one chain in 8-step blocks for the step counts of
+// H = 128 .. 4096 (H = 64 * 2^k): acc from them, the count done (the caller
+// runs the rest, if any, one by one).
+WM_DEV int rc_steps(const lf32_t* wp, const lf32_t* xp, int nsteps, float& acc) {
+    switch (nsteps) {
+    case 256: acc = rc_blocks<32>(wp, xp); return 256;
+    case 128: acc = rc_blocks<16>(wp, xp); return 128;
+    case 64: acc = rc_blocks<8>(wp, xp); return 64;
+    case 32: acc = rc_blocks<4>(wp, xp); return 32;
+    case 16: acc = rc_blocks<2>(wp, xp); return 16;
+    case 8: acc = rc_blocks<1>(wp, xp); return 8;
+    default: acc = 0.0f; return 0;
+    }
+}
+
 // Router logits of rows [r0, r0 + nr), nr <= 4, in the reference order
 // (transformer.h:172-191): lane l of a row keeps the running fp32 FMA over
 // columns l, l+16, ...; the 16 lanes then reduce with the xor tree 8, 4, 2, 1
@@ -347,17 +399,7 @@ WM_DEV void wg_router_rows(const float* __restrict__ x, const float* __restrict_
         const lf* wr = (const lf*)(lds + (wave + 1) * region + (((uintptr_t)wsrc) & 15));
         const int H16 = H - (H & 15), nsteps = H16 / 16;
         float acc = 0.0f;
-        int s = 0;
-        for (; s + 16 <= nsteps; s += 16) {
-            float wv[16], xv[16];
-#pragma unroll
-            for (int j = 0; j < 16; j++) {
-                wv[j] = wr[lane + 16 * (s + j)];
-                xv[j] = xr[lane + 16 * (s + j)];
-            }
-#pragma unroll
-            for (int j = 0; j < 16; j++) acc = fmaf(wv[j], xv[j], acc);
-        }
+        int s = rc_steps(wr + lane, xr + lane, nsteps, acc);
         for (; s < nsteps; s++) acc = fmaf(wr[lane + 16 * s], xr[lane + 16 * s], acc);
         // xor tree 8, 4, 2, 1 over the 16 lanes as row rotations: after the
         // step of distance d the partial sums repeat with period d, so the
