@@ -18,6 +18,8 @@ own roofline and CPU baseline:
       overlap, 512 decode tokens (a step = one token through all 8 layers)
   c5  prefill of 512 bf16 tokens through the 512-expert top-10 Q8_0 layer,
       Zipf routing (a step = the whole batch)
+  c5r the same batch routed by the layer's fp32 router (router logits and
+      top-K of every token inside the timed batch)
   c3p prefill of 512 bf16 tokens through the c3 layer (Q4_K gate/up, Q6_K
       down, Q8_0 shared expert), Zipf routing
 
@@ -178,6 +180,7 @@ class Workload:
             self.hs = torch.empty(cfg.n_layers + 1, cfg.tokens, cfg.H, device="cuda")
             self.hs[0] = self.X
         self.outs = torch.empty(cfg.tokens, cfg.H, dtype=torch.float32, device="cuda")
+        self._rids = {}
 
     def step(self, i):
         cfg = self.cfg
@@ -199,6 +202,21 @@ class Workload:
             else:
                 sl.layer.decode_forced(x, self.routes[li][2][t], self.routes[li][3][t], out=o, step=i)
 
+    def route_ids(self, li: int = 0):
+        """Expert ids [T][K] of layer li: the forced routes, or for a routed
+        prefill those the router chose for the batch (read back from the
+        prefill workspace after one batch; the inputs are the same every
+        batch)."""
+        if self.routes is not None:
+            return self.routes[li][0]
+        if li not in self._rids:
+            import torch
+            self.step(0)
+            torch.cuda.synchronize()
+            ids, _ = self.layers[li].layer.prefill_routing(self.cfg.tokens)
+            self._rids[li] = ids.cpu().numpy().copy()
+        return self._rids[li]
+
     def status(self):
         return max(sl.layer.prefill_status() if self.prefill else sl.layer.check() for sl in self.layers)
 
@@ -207,7 +225,7 @@ class Workload:
 
     def step_bytes(self):
         if self.prefill:
-            return prefill_bytes(self.cfg, self.routes[0][0]) * self.cfg.n_layers
+            return prefill_bytes(self.cfg, self.route_ids(0)) * self.cfg.n_layers
         return decode_layer_bytes(self.cfg) * self.cfg.n_layers
 
 
@@ -283,7 +301,7 @@ def entry(wl, L, steps, warmup, multi_kernel=False):
     rl = None
     if wl.prefill and "gate_up_swiglu" in phases:
         gu = phases["gate_up_swiglu"]
-        rl = roofline(prefill_gateup_kernel(cfg), "k_pf_gemm", cfg.name, prefill_gateup_bytes(cfg, wl.routes[0][0]),
+        rl = roofline(prefill_gateup_kernel(cfg), "k_pf_gemm", cfg.name, prefill_gateup_bytes(cfg, wl.route_ids(0)),
                       gu["avg_us"])
     elif not wl.prefill and not multi_kernel:
         # one fused launch per layer per token moves the step's bytes; its
@@ -346,8 +364,8 @@ def cpu_baseline(wl, n_sample):
     Xh = wl.X.float().cpu().numpy()
     host = []
     for li, sl in enumerate(wl.layers):
-        if wl.routes is not None:
-            experts = np.unique(wl.routes[li][0][:n_sample])
+        if wl.routes is not None or wl.prefill:
+            experts = np.unique(wl.route_ids(li)[:n_sample])
         else:
             ids, _ = sl.layer.trace()
             experts = np.unique(ids[:n_sample].cpu().numpy())
@@ -400,8 +418,8 @@ def cpu_baseline(wl, n_sample):
 
 # ------------------------------------------------------------------ main
 
-EXTRA = ["c1", "c3", "c4", "c5", "c3p"]
-CPU_SAMPLE = {"c1": 1, "c2": 16, "c3": 16, "c4": 4, "c5": 8, "c3p": 16}
+EXTRA = ["c1", "c3", "c4", "c5", "c5r", "c3p"]
+CPU_SAMPLE = {"c1": 1, "c2": 16, "c3": 16, "c4": 4, "c5": 8, "c5r": 8, "c3p": 16}
 
 
 # marks of the persistent step's per-workgroup timeline (include/winmoe_hip.h, wm_workspace_timeline)
@@ -540,7 +558,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2048)
     ap.add_argument("--warmup", type=int, default=64)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c3p"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c5r", "c3p"])
     ap.add_argument("--only", action="store_true", help="measure --config alone (no `configs` object)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--multi-kernel", action="store_true",

@@ -288,14 +288,26 @@ int wm_pool_layer(const wm_expert_pool* pool, wm_layer_desc* d);
 /* Makes experts ids[0..n) of `layer` (n <= n_slots) resident for the next
  * steps on `stream`: a resident expert is a hit; a missing one goes to a free
  * slot, else to the least recently used slot that no unreleased acquire
- * holds, copied from gate_src + id * gate_stride (up, down alike).  Writes,
+ * holds, copied from gate_src + id * gate_stride (up, down alike).  Every id
+ * must name one of the source's n_src experts (0 <= id < n_src).  Writes,
  * in stream order, the slot of each id to slots_dev (device int32 [n]): the
  * ids to pass to wm_moe_decode_forced on the pool's layer.  Returns the
- * number of misses; WM_EINVAL for a bad argument or when every slot is held
- * by unreleased acquires. */
-int wm_pool_acquire(wm_expert_pool* pool, int layer, const int32_t* ids, int n, const void* gate_src,
+ * number of misses; WM_EINVAL, before any state changes, for a bad argument
+ * (an id outside [0, n_src) included) or when every slot is held by
+ * unreleased acquires. */
+int wm_pool_acquire(wm_expert_pool* pool, int layer, const int32_t* ids, int n, int n_src, const void* gate_src,
                     const void* up_src, const void* down_src, int64_t gate_stride, int64_t up_stride,
                     int64_t down_stride, int32_t* slots_dev, void* stream);
+/* As wm_pool_acquire, from host memory that holds each expert as one image
+ * in the slot layout -- gate at 0, up at ru(gate_bytes), down at
+ * ru(gate_bytes) + ru(up_bytes), ru() rounding up to a multiple of 256 -- at
+ * src + id * src_stride (src_stride >= wm_pool_slot_bytes): one copy per
+ * missing expert instead of three.  When every part size is a multiple of
+ * 256 bytes (every shape of the benchmarked layers) the image is the
+ * reference's RAM cache slot, gate, up and down back to back
+ * (winmoe_inference.c:1764-1786). */
+int wm_pool_acquire_packed(wm_expert_pool* pool, int layer, const int32_t* ids, int n, int n_src, const void* src,
+                           int64_t src_stride, int32_t* slots_dev, void* stream);
 /* To be called once the steps that read the slots of the acquires since the
  * last release are enqueued on `stream`: those slots may then be recycled,
  * after those steps (the pool's stream waits for them on the device). */

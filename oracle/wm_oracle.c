@@ -219,6 +219,31 @@ int wmo_dequant(int qtype, const void* blocks, int64_t nblocks, float* out) {
     return 0;
 }
 
+/* Per-block checksums of the dequantised values, for comparing a whole
+ * expert stack with a device dequantisation without moving the fp32 values:
+ * s1[i] = sum of the 32-bit patterns of block i's values, s2[i] = sum of
+ * (j + 1) * pattern of value j.  A value that differs changes s1. */
+int wmo_dequant_block_sums(int qtype, const void* blocks, int64_t nblocks, int64_t* s1, int64_t* s2) {
+    const int bs = wmo_block_bytes(qtype), ne = wmo_block_elems(qtype);
+    if (bs == 0 || nblocks < 0 || ne > 256) return -2;
+    float y[256];
+    const uint8_t* p = (const uint8_t*)blocks;
+    for (int64_t i = 0; i < nblocks; i++) {
+        int rc = wmo_dequant(qtype, p + i * bs, 1, y);
+        if (rc) return rc;
+        int64_t a = 0, b = 0;
+        for (int j = 0; j < ne; j++) {
+            uint32_t u;
+            memcpy(&u, &y[j], 4);
+            a += (int64_t)u;
+            b += (int64_t)(j + 1) * (int64_t)u;
+        }
+        s1[i] = a;
+        s2[i] = b;
+    }
+    return 0;
+}
+
 /* transformer.h:172-191 default case: AVX-512 16-lane FMA accumulation, then
  * _mm512_reduce_add_ps (GCC avx512fintrin.h: halves, quarters, then lanes
  * {0,2},{1,3}, then 0+1), then the scalar tail `s += row[c] * x[c]`, which

@@ -37,6 +37,9 @@ float wmo_fp16_to_fp32(uint16_t h);
  * q6k_dequant.h:20-25,112-141; Q2_K / Q3_K: public ggml block format (no
  * reference implementation exists). */
 int   wmo_dequant(int qtype, const void* blocks, int64_t nblocks, float* out);
+/* Per-block sums of the dequantised values' 32-bit patterns: s1[i] plain,
+ * s2[i] weighted by (position in the block + 1). */
+int   wmo_dequant_block_sums(int qtype, const void* blocks, int64_t nblocks, int64_t* s1, int64_t* s2);
 
 /* Router logits in the reference's fp32 order (transformer.h:172-191, default
  * case of quant_matvec): per row, 16 running fp32 FMA lanes over columns

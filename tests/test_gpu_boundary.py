@@ -60,8 +60,9 @@ def test_shim_expert_down(wm, orc):
 def test_shim_limit_and_round_robin_eviction(wm, orc):
     """The expert table's contract: capacity 300 by default (MAX_GPU_EXPERTS),
     gpu_set_expert_limit clamps to at least 1, slots fill in order, the 301st
-    insert recycles slot 0 and the next one slot 1 (round robin), a recycled
-    expert is no longer found, ids past 80 layers x 1024 experts are refused,
+    insert recycles slot 0 and the next one slot 1 (round robin), a lowered
+    limit leaves the cursor where it was (the next recycle takes it, then it
+    wraps), a recycled expert is no longer found, ids past 80 layers x 1024 experts are refused,
     and a recycled slot computes with its new expert's bytes."""
     L = wm.load()
     H, I = 256, 256
@@ -88,9 +89,12 @@ def test_shim_limit_and_round_robin_eviction(wm, orc):
     assert L.gpu_expert_ffn_fused(0, x.ctypes.data, H, I, out.ctypes.data) == 0
     assert rel_l2(out, orc.expert_ffn(b[0], Q8_0, b[1], Q8_0, b[2], Q8_0, x, H, I)) <= LAYER_TOL
     assert put(80, 0, a) == -1 and put(0, 1024, a) == -1 and put(-1, 0, a) == -1
-    L.gpu_set_expert_limit(0)                      # clamps to 1: every insert now recycles slot 0
-    assert put(6, 1, a) == 0 and put(6, 2, a) == 0
-    assert L.gpu_find_cached_expert(6, 1) == -1 and L.gpu_find_cached_expert(6, 2) == 0
+    # clamps to 1; the cursor is left where it was (slot 2, gpu_offload.cu:582-623),
+    # so the next insert recycles slot 2, then the cursor wraps to 0 for good
+    L.gpu_set_expert_limit(0)
+    assert put(6, 1, a) == 2 and put(6, 2, a) == 0 and put(6, 3, a) == 0
+    assert L.gpu_find_cached_expert(6, 1) == 2 and L.gpu_find_cached_expert(6, 2) == -1
+    assert L.gpu_find_cached_expert(6, 3) == 0
     assert L.gpu_vram_used_mb() > 0
     L.gpu_shutdown()
     assert L.gpu_is_initialized() == 0 and L.gpu_find_cached_expert(6, 2) == -1

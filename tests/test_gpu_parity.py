@@ -8,7 +8,8 @@ import numpy as np
 import pytest
 
 from golden.blocks import Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, rand_blocks
-from helpers import rel_l2, same_bits_nan, ulp_diff
+from helpers import (rel_l2, rms_boundary_vector, rms_ss_index_order, rms_ss_kernel_order, same_bits_nan,
+                     ulp_diff)
 
 pytestmark = pytest.mark.gpu
 
@@ -379,7 +380,6 @@ def test_decode_narrow_intermediate(wm, orc, H, I, K, shared):
                       norm_w=w, add_residual=False)
     h = (3.0 * torch.randn(H, generator=g, device="cuda")).contiguous()
     hh = host(h)
-    assert kernel_order_scale(hh, H).view(np.uint32) == reference_order_scale(hh, H).view(np.uint32)
     case(f"narrow H={H} I={I} K={K} rmsnorm")
     got = host(normed.decode(h))
     want = host(fused.decode(dev(orc.rmsnorm(hh, host(w)))))
@@ -749,34 +749,6 @@ def test_gguf_router_f16_and_quantised(wm, orc, tmp_path, rtype):
 
 # ------------------------------------------------------------------ RMSNorm in, residual out
 
-def kernel_order_scale(h, H, eps=1e-6):
-    """The RMSNorm scale as the persistent kernel forms it: lane l of 64 keeps
-    four sums s_c of (double)h[i]^2 over i = 4l + 256k + c (k in order),
-    ss_l = (s_0 + s_1) + (s_2 + s_3), then an xor butterfly over the lanes
-    (32, 16, ..., 1); scale = 1 / sqrtf((float)(ss / H) + eps)."""
-    v = np.asarray(h, np.float32).astype(np.float64)
-    lanes = np.zeros(64)
-    for l in range(64):
-        s = [0.0, 0.0, 0.0, 0.0]
-        if 4 * l < H:
-            for k in range((H + 255) // 256):
-                for c in range(4):
-                    i = 4 * l + 256 * k + c
-                    s[c] += v[i] * v[i]
-        lanes[l] = (s[0] + s[1]) + (s[2] + s[3])
-    for m in (32, 16, 8, 4, 2, 1):
-        lanes = lanes + lanes[np.arange(64) ^ m]
-    return np.float32(1.0) / np.sqrt(np.float32(lanes[0] / H) + np.float32(eps), dtype=np.float32)
-
-
-def reference_order_scale(h, H, eps=1e-6):
-    """attention.h:31-33: ss in index order, scale = 1 / sqrtf((float)(ss/dim) + 1e-6f)."""
-    ss = 0.0
-    for x in np.asarray(h, np.float32).astype(np.float64):
-        ss += x * x
-    return np.float32(1.0) / np.sqrt(np.float32(ss / H) + np.float32(eps), dtype=np.float32)
-
-
 @pytest.mark.parametrize("name,E,residual", [("c1", 64, True), ("c2", 40, True), ("c4", 24, True), ("c3", 24, True),
                                              ("c2", 512, True), ("c1", 1000, True), ("c2", 40, False)])
 def test_fused_rmsnorm_and_residual(wm, orc, name, E, residual):
@@ -785,9 +757,11 @@ def test_fused_rmsnorm_and_residual(wm, orc, name, E, residual):
     bit, with the same routing trace.  E=512 and E=1000 put two and four
     router rows on a workgroup of the persistent kernel (rows read the
     normalised x from LDS); c3 has a shared expert of another type (its x
-    operand records are built separately).  The kernel adds the squares in a
-    different order than the reference; the bit-for-bit bar holds when both
-    orders give the same scale, which the test checks first."""
+    operand records are built separately).  The kernel adds the squares in
+    its own order and falls back to the reference's index order when the two
+    could round (float)(ss / H) differently, so the bar holds for every
+    vector: the fifth token is one on a rounding boundary, where the two
+    orders do disagree (rms_boundary_vector)."""
     import torch
     from winmoe_amd import synth
     from winmoe_amd.moe import MoELayer
@@ -799,15 +773,16 @@ def test_fused_rmsnorm_and_residual(wm, orc, name, E, residual):
     normed = MoELayer(c.H, c.I, E, c.K, sl.router, sl.gate, sl.up, sl.down, c.types, shared=sl.shared, max_tokens=8,
                       norm_w=w, add_residual=residual)
     plain = synth.twin_layer(sl, multi_kernel=False)
-    Hs = 3.0 * torch.randn(4, c.H, generator=g, device="cuda")
-    routes = synth.forced_routes(cfg, E=E, tokens=4) if cfg.routing != "router" else None
-    for t in range(4):
+    Hs = 3.0 * torch.randn(5, c.H, generator=g, device="cuda")
+    Hs[4] = torch.from_numpy(rms_boundary_vector(c.H)).cuda()
+    hb = host(Hs[4])
+    fast, ref = rms_ss_kernel_order(hb), rms_ss_index_order(hb)
+    assert np.float32(fast / c.H) != np.float32(ref / c.H)      # the orders disagree on token 4
+    routes = synth.forced_routes(cfg, E=E, tokens=5) if cfg.routing != "router" else None
+    for t in range(5):
         case(f"rmsnorm {name} E={E} token={t}")
         h = Hs[t].contiguous()
         hh = host(h)
-        ks, rs = kernel_order_scale(hh, c.H), reference_order_scale(hh, c.H)
-        assert ks.view(np.uint32) == rs.view(np.uint32), \
-            f"token {t}: the kernel's and the reference's sum orders give different scales ({ks!r} vs {rs!r})"
         x = orc.rmsnorm(hh, host(w))
         if routes is None:
             a = host(normed.decode(h))
@@ -820,7 +795,7 @@ def test_fused_rmsnorm_and_residual(wm, orc, name, E, residual):
         assert np.array_equal(a.view(np.uint32), want.view(np.uint32)), t
     ta, _ = normed.trace()
     tb, _ = plain.trace()
-    assert np.array_equal(host(ta[:4]), host(tb[:4]))
+    assert np.array_equal(host(ta[:5]), host(tb[:5]))
     assert normed.status() == 0
 
 

@@ -1,12 +1,17 @@
 """GPU tests of host -> HBM expert streaming (wm_pool_*): experts held in
 pinned host memory, made resident on demand in a pool of HBM slots
 (the reference's miss path, winmoe_inference.c:1736-1789, and GPU cache
-upload, gpu_offload.cu:590-659).  A step on the pool must give the same
-output, bit for bit, as the same step on the fully resident layer, and the
-pool must replace slots as its contract says (free slots first, then the
+upload, gpu_offload.cu:590-659).  A step on the pool must agree with the
+oracle run on the host bytes the pool copied from (layer tolerance), give the
+same output, bit for bit, as the same step on the fully resident layer, and
+the pool must replace slots as its contract says (free slots first, then the
 least recently used one that no unreleased acquire holds)."""
 import numpy as np
 import pytest
+
+from helpers import rel_l2
+
+LAYER_TOL = 1e-3      # layer output rel-L2 vs the fp64 oracle
 
 pytestmark = pytest.mark.gpu
 
@@ -149,4 +154,89 @@ def test_pool_two_layers_and_limits(wm):
     pool.release()
     ref = host(sl.layer.decode_forced(X[0], torch.tensor([1, 2, 3, 4], dtype=torch.int32, device="cuda"), w))
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    pool.close()
+
+
+@pytest.mark.parametrize("name,n_slots,packed", [("c2", 24, False), ("c3", 12, True), ("c3", 12, False)])
+def test_pool_vs_oracle_e512(wm, orc, name, n_slots, packed):
+    """The C2 and C3 layers at E = 512 through a pool of a few slots (Zipf
+    routing with overlap: slots are recycled under the steps), fed from
+    pinned host tensors per part or from packed [gate | up | down] slot
+    images (one copy per expert).  Tokens after several recycles are checked
+    against the oracle run on those same host bytes with the same forced ids
+    and weights; every token equals the resident layer bit for bit."""
+    import torch
+    from winmoe_amd import synth
+    cfg, sl, src, pool, pl = _pool_setup(wm, name, 512, n_slots)
+    c = sl.cfg
+    T = 16
+    rng = np.random.default_rng(11)
+    ids = synth.zipf_routing(T, 512, c.K, rng, overlap=0.375)
+    w = synth.softmax_weights(T, c.K, rng)
+    X = synth.make_hidden(cfg, tokens=T)
+    outs = torch.empty(T, c.H, device="cuda")
+    image = pool.pack(*src) if packed else None
+    case(f"pool {name} E=512 slots={n_slots} packed={packed}: {T} tokens")
+    for t in range(T):
+        if packed:
+            slots, _ = pool.acquire_packed(0, ids[t], image)
+        else:
+            slots, _ = pool.acquire(0, ids[t], *src)
+        pl.decode_forced(X[t], slots, torch.from_numpy(w[t]).cuda(), out=outs[t], step=t)
+        pool.release()
+    torch.cuda.synchronize()
+    assert pl.check() == 0
+    hits, misses, nbytes = pool.stats()
+    assert misses > 2 * n_slots                     # slots were recycled
+    assert nbytes == misses * sum(s_.shape[1] for s_ in src)
+    # the oracle on the host bytes the pool read
+    sh = sl.shared
+    shared = None if sh is None else tuple(host(m) for m in (sh.gate, sh.up, sh.down))
+    common = dict(shared=shared, sh_types=None if sh is None else sh.types,
+                  sh_gate_inp=None if sh is None or sh.gate_inp is None else host(sh.gate_inp),
+                  I_shared=0 if sh is None else sh.inter)
+    if packed:
+        flat = image.numpy().reshape(-1)
+        sb = pool.slot_bytes
+        OL = orc.make_layer(c.H, c.I, 512, c.K, c.types, gate=flat[pool.offsets[0]:], up=flat[pool.offsets[1]:],
+                            down=flat[pool.offsets[2]:], strides=(sb, sb, sb), **common)
+    else:
+        OL = orc.make_layer(c.H, c.I, 512, c.K, c.types, gate=src[0].numpy(), up=src[1].numpy(),
+                            down=src[2].numpy(), **common)
+    for t in (3, 7, 11, 15):
+        case(f"pool {name} oracle token={t}")
+        _, _, ref, _ = orc.moe_layer(OL, host(X[t]), ids[t], w[t])
+        got = host(outs[t])
+        assert rel_l2(got, ref) <= LAYER_TOL, (t, rel_l2(got, ref))
+    for t in range(T):
+        res = host(sl.layer.decode_forced(X[t], torch.from_numpy(ids[t]).cuda(), torch.from_numpy(w[t]).cuda()))
+        assert np.array_equal(host(outs[t]).view(np.uint32), res.view(np.uint32)), t
+    pool.close()
+
+
+def test_pool_refuses_ids_past_the_source(wm):
+    """An id outside the host source's experts is refused with WM_EINVAL by
+    the C-ABI (and with ValueError by ExpertPool) before any copy or state
+    change; the pool stays usable."""
+    import ctypes as C
+    import torch
+    from winmoe_amd import _lib
+    cfg, sl, src, pool, pl = _pool_setup(wm, "c1", 16, 6)
+    out = torch.empty(4, dtype=torch.int32, device="cuda")
+    case("pool: id past the source")
+    with pytest.raises(ValueError):
+        pool.acquire(0, [1, 2, 16, 3], *src)
+    bad = np.array([1, 2, 16, 3], np.int32)
+    rc = _lib.load().wm_pool_acquire(pool._h, 0, bad.ctypes.data_as(C.POINTER(C.c_int32)), 4, 16,
+                                     src[0].data_ptr(), src[1].data_ptr(), src[2].data_ptr(), src[0].stride(0),
+                                     src[1].stride(0), src[2].stride(0), out.data_ptr(), None)
+    assert rc == -2
+    image = pool.pack(*src)
+    rc = _lib.load().wm_pool_acquire_packed(pool._h, 0, bad.ctypes.data_as(C.POINTER(C.c_int32)), 4, 16,
+                                            image.data_ptr(), image.stride(0), out.data_ptr(), None)
+    assert rc == -2
+    assert pool.stats() == (0, 0, 0)
+    s, m = pool.acquire(0, [1, 2, 15, 3], *src)
+    assert m == 4
+    pool.release()
     pool.close()

@@ -102,3 +102,21 @@ def test_config_byte_counts():
     assert c4.expert_bytes() == 4_554_752
     c1 = synth.CONFIGS["c1"]
     assert c1.expert_bytes() == 3_342_336
+
+
+def test_pool_ids_checked_against_the_source(lib):
+    """ExpertPool refuses ids outside the host source's experts before it
+    calls the library (which refuses them too, WM_EINVAL); a pool that does
+    not exist is refused without a GPU."""
+    from winmoe_amd import _lib
+    from winmoe_amd.moe import ExpertPool
+    assert ExpertPool._ids(None, [0, 3, 511], 512).tolist() == [0, 3, 511]
+    with pytest.raises(ValueError):
+        ExpertPool._ids(None, [0, 512], 512)
+    with pytest.raises(ValueError):
+        ExpertPool._ids(None, [-1, 2], 512)
+    ids = np.array([1, 2], np.int32)
+    assert lib.wm_pool_acquire(None, 0, ids.ctypes.data_as(C.POINTER(C.c_int32)), 2, 4, None, None, None, 0, 0, 0,
+                               None, None) == _lib.WM_EINVAL
+    assert lib.wm_pool_acquire_packed(None, 0, ids.ctypes.data_as(C.POINTER(C.c_int32)), 2, 4, None, 0, None,
+                                      None) == _lib.WM_EINVAL

@@ -78,8 +78,10 @@ SIGNATURES = {
     "wm_pool_create": (C.c_int, [C.c_void_p, _i64, C.c_int, _i64, _i64, _i64, C.POINTER(C.c_void_p)]),
     "wm_pool_destroy": (C.c_int, [C.c_void_p]),
     "wm_pool_layer": (C.c_int, [C.c_void_p, C.c_void_p]),
-    "wm_pool_acquire": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_int32), C.c_int, C.c_void_p, C.c_void_p,
-                                  C.c_void_p, _i64, _i64, _i64, C.c_void_p, C.c_void_p]),
+    "wm_pool_acquire": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_int32), C.c_int, C.c_int, C.c_void_p,
+                                  C.c_void_p, C.c_void_p, _i64, _i64, _i64, C.c_void_p, C.c_void_p]),
+    "wm_pool_acquire_packed": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_int32), C.c_int, C.c_int, C.c_void_p,
+                                         _i64, C.c_void_p, C.c_void_p]),
     "wm_pool_release": (C.c_int, [C.c_void_p, C.c_void_p]),
     "wm_pool_stats": (C.c_int, [C.c_void_p, C.POINTER(_i64), C.POINTER(_i64), C.POINTER(_i64)]),
     "wm_prefill_workspace_size": (_i64, [C.POINTER(LayerDesc), C.c_int]),

@@ -535,8 +535,9 @@ static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
     a.y_cap = (a.dn_tiles + nwg - 1) / nwg * rpt_dn;
     a.ring_buf = std::max(std::max(ring_tile_bytes_rt(gut), ring_tile_bytes_rt(dt)),
                           std::max(ring_tile_bytes_rt(sgut), ring_tile_bytes_rt(sdt)));
-    // LDS: control block | ring (x and the router rows at the start) |
-    // SwiGLU operand records | x operand records | gate/up row sums | down row sums
+    // LDS: control block | SwiGLU operand records | x operand records |
+    // gate/up row sums | down row sums | tile descriptors | the streaming
+    // waves' buffers | x and the router rows (or those in the first buffers)
     int o = (int)((sizeof(PersistCtl) + 255) / 256 * 256);
     a.x_region = (H * 4 + 1023) / 1024 * 1024;
     // x (normalised in place when the layer has an RMSNorm), then the router rows
@@ -553,6 +554,25 @@ static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
     if (d->norm_w) o = std::max(o, a.o_norm + a.x_region);
     a.o_gu = o; o += 2 * (K + 1) * a.gu_cap * 4;
     a.o_y = o; o += (K + 1) * a.y_cap * 4;
+    // act tiles: the SwiGLU outputs of a slot come into the streaming waves'
+    // buffers in tiles of aseg 64-value segments (4 B per value: two to a
+    // tagged 8-byte word; whole K-quant super-blocks, so every tile is a
+    // contiguous column range).  One wave builds a tile's records, 8
+    // segments at a time: with few slots a slot's down tiles wait for them,
+    // and 8-segment tiles let two waves share a slot; with many, the act
+    // tiles run well ahead and 16-segment tiles halve their number.
+    a.aseg = (K + (sh ? 1 : 0) >= 8 && a.ring_buf >= 16 * SEG * 4) ? 16 : 8;
+    a.nact = (I / SEG + a.aseg - 1) / a.aseg;
+    if (a.nact > PMAXACT || a.aseg * SEG * 4 > a.ring_buf) return 1;
+    // the tile list's descriptor table, 16 bytes an entry, for the longest
+    // list of any workgroup: per slot 2 * (gate/up tiles) + act tiles + down tiles
+    {
+        const int gu_units = a.gu_tiles / a.gu_step;
+        const int ngu_max = a.gu_step * ((gu_units + nwg - 1) / nwg), ndn_max = (a.dn_tiles + nwg - 1) / nwg;
+        a.n_desc = (K + (sh ? 1 : 0)) * (2 * ngu_max + a.nact + ndn_max);
+        a.o_desc = o;
+        o += a.n_desc * 16;
+    }
     o = (o + 255) / 256 * 256;
     // the streaming waves' rings take what is left, up to PW of them; x and
     // the router rows get a region of their own when it fits, else they sit
@@ -566,16 +586,6 @@ static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
         a.n_rwaves = 0;
     }
     if (a.nstream < a.n_rwaves + 1 || a.nstream < 4) return 1;
-    // act tiles: the SwiGLU outputs of a slot come into the streaming waves'
-    // rings in tiles of aseg 64-value segments (4 B per value: two to a
-    // tagged 8-byte word; whole K-quant super-blocks, so every tile is a
-    // contiguous column range).  One wave builds a tile's records, 8
-    // segments at a time: with few slots a slot's down tiles wait for them,
-    // and 8-segment tiles let two waves share a slot; with many, the act
-    // tiles run well ahead and 16-segment tiles halve their number.
-    a.aseg = (K + (sh ? 1 : 0) >= 8 && a.ring_buf >= 16 * SEG * 4) ? 16 : 8;
-    a.nact = (I / SEG + a.aseg - 1) / a.aseg;
-    if (a.nact > PMAXACT || a.aseg * SEG * 4 > a.ring_buf) return 1;
     // (and more than half of a CU's LDS, so that each CU holds one workgroup)
     const int lds = std::max((o + a.nstream * PRING * a.ring_buf + 255) / 256 * 256,
                              (max_lds_per_wg() / 2 + 256) / 256 * 256);

@@ -71,12 +71,14 @@ int launch_decode_step(const DecodeArgs& a, int gut, int dt, int sgut, int sdt, 
 }  // namespace wm
 
 // ------------------------------------------------------------------ persistent step
-// One workgroup per CU: PW streaming waves + 2 helper waves (router rows,
+// One workgroup per CU: PW streaming waves + 3 helper waves (router rows,
 // routing, operand staging, SwiGLU publishing, combine).  Internal.
 namespace wm {
 
-constexpr int PW = 13;                   // streaming waves per workgroup (each loads and processes tiles)
-constexpr int PRING = 1;                 // ring buffers per streaming wave
+// Streaming waves per workgroup (each loads one tile at a time into its own
+// LDS buffer and processes it; with the 3 helpers, 16 waves per CU).
+constexpr int PW = 13;
+constexpr int PRING = 1;                 // LDS buffers per streaming wave
 constexpr int PSTAGE = 2;                // helper waves besides the publisher: the router wave and the x loader
 constexpr int PTHREADS = 64 * (PW + 1 + PSTAGE);  // + publisher
 constexpr int PMAXK = 16;
@@ -98,7 +100,7 @@ WM_HD int ring_tile_bytes_rt(int t) { return t == Q8_0 ? 4416 : (t == Q6_K ? 409
 // is in flight (the compiler makes every LDS atomic wait for all of them).
 struct PersistCtl {
     uint32_t next;                 // next tile-list entry to claim
-    uint32_t n_done;               // tile-list entries processed
+    uint32_t n_done;               // down tiles processed
     uint32_t gu_done[PMAXK + 1];   // gate/up tiles of the slot processed
     uint32_t xop_built[PW];        // streaming wave w wrote its part of the x operand records
     uint32_t routed;               // routing of this step is in ids / w / valid
@@ -107,14 +109,15 @@ struct PersistCtl {
     uint32_t abort;                // a wait of this workgroup gave up: every later wait ends at once
     uint32_t rows_in;              // x and the router rows are in LDS
     uint32_t router_done[2];       // helper h is done with the router rows (their ring space is free)
-    uint32_t npicked;              // picks 0 .. npicked-1 of the routing are in ids / valid
+    uint32_t npicked;              // picks 0 .. npicked-1 of the routing are in ids / valid / rbase
     uint32_t act_done[PMAXK + 1][PMAXACT]; // the slot's SwiGLU operand records of act tile t are in LDS
     int32_t ids[PMAXK];
     float w[PMAXK];
     int32_t valid[PMAXK];
     float sgate;
     uint32_t x_in;                 // x is in LDS (the second staging wave loads it)
-    uint32_t pad2;
+    uint32_t desc_built;           // streaming waves that have written their part of the tile descriptors
+    uint64_t rbase[PMAXK][3];      // routed slot k's gate / up / down bytes | 1 (1 alone: no weights), 0 until picked
     uint64_t t[P_TL];              // timeline (device clock)
 };
 
@@ -132,6 +135,7 @@ struct PersistArgs {
     int32_t o_xop, o_xop2;             // LDS: x operand records of the routed / shared gate-up types
     int32_t o_gu, gu_cap;              // LDS: gate and up row sums [K+1][gu_cap] each
     int32_t o_y, y_cap;                // LDS: down row sums [K+1][y_cap]
+    int32_t o_desc, n_desc;            // LDS: the tile list's descriptors (16 bytes per entry, n_desc at most)
     const float* x;                    // x, or the residual stream h when norm_w is set
     float* out;
     const float* router;

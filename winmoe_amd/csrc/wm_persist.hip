@@ -82,6 +82,7 @@ WM_DEV uint64_t tagged(uint32_t tag, float v) { return ((uint64_t)tag << 32) | (
 // loads and waits for all of them first (vmcnt(0)), which would drain the
 // weight stream at every flag check.
 WM_DEV uint32_t lds_ld(const lds32_t* p) { return *(const volatile lds32_t*)p; }
+WM_DEV uint64_t lds_ld64(const lds64_t* p) { return *(const volatile lds64_t*)p; }
 
 // Every LDS write of this wave is complete, then lane 0 stores v to *p (a
 // word with one writer; volatile, not atomic, for the reason above), then
@@ -258,6 +259,18 @@ struct TileList {
     WM_DEV TRef at(int j) const {
         const int b = __builtin_popcountll(__builtin_amdgcn_ballot_w64(v_start <= j)) - 1;
         const int code = __builtin_amdgcn_readlane(v_blk, b), t = j - __builtin_amdgcn_readlane(v_start, b);
+        return decode(code, t);
+    }
+    // As at(j) for a lane-varying j in [0, n) (called with all 64 lanes
+    // active): the block is the count of block starts at or before j, minus
+    // one; its code and start come from the lane that holds them.
+    WM_DEV TRef at_lane(int j) const {
+        int b = -1;
+        for (int bb = 0; bb < 64; bb++) b += __builtin_amdgcn_readlane(v_start, bb) <= j ? 1 : 0;
+        const int code = __shfl(v_blk, b), t = j - __shfl(v_start, b);
+        return decode(code, t);
+    }
+    WM_DEV TRef decode(int code, int t) const {
         const int q = code >> 2, c = code & 3;
         const bool shared = sh && q == 0;
         TRef r;
@@ -399,6 +412,32 @@ WM_DEV TileDesc tile_desc(const PersistArgs& a, const Part& P, const TRef& r, in
     return d;
 }
 
+// A tile descriptor as the LDS table holds it (16 bytes): kind | slot << 4 |
+// rows << 12, the offset in its matrix (below 2^32 for every supported shape:
+// a matrix of 4096 x 4096 Q8_0 weights is 17.8 MB), where its row sums go,
+// its bytes.
+typedef __attribute__((address_space(3))) u32x4 lq4_t;
+WM_DEV u32x4 desc_pack(const TileDesc& d) {
+    u32x4 e;
+    e.x = (uint32_t)d.kind | ((uint32_t)d.slot << 4) | ((uint32_t)d.rows << 12);
+    e.y = (uint32_t)d.off;
+    e.z = (uint32_t)d.out;
+    e.w = (uint32_t)d.nb;
+    return e;
+}
+// (the entry is the same in every lane: read as wave-uniform values)
+WM_DEV TileDesc desc_unpack(const u32x4& e) {
+    const uint32_t w0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)e.x);
+    TileDesc d;
+    d.kind = (int)(w0 & 15u);
+    d.slot = (int)((w0 >> 4) & 255u);
+    d.rows = (int)(w0 >> 12);
+    d.off = (int64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)e.y);
+    d.out = __builtin_amdgcn_readfirstlane((int)e.z);
+    d.nb = __builtin_amdgcn_readfirstlane((int)e.w);
+    return d;
+}
+
 WM_DEV int lg_tile_lanes(int n) { return 31 - __builtin_clz((unsigned)(n / SEG)); }
 WM_DEV bool routed_kind(int k) { return k == K_RG || k == K_RU || k == K_RD; }
 
@@ -417,10 +456,15 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
     const bool active = wave < a.nstream;
     lds8_t* const buf = lds + a.o_ring + wave * a.ring_buf;
     const Part P = partition(a);
+    lq4_t* const tab = (lq4_t*)(lds + a.o_desc);
     TileList L;
     L.init(a, P.ngu, P.ndn, lane);
-    const int n = active ? L.n : 0;
+    // (the host sizes the descriptor table for the longest list; a longer one
+    // would be an invalid step, reported as a wait that gave up)
+    if (active && L.n > a.n_desc) give_up(ctl, a.status, lane);
+    const int n = active ? min(L.n, a.n_desc) : 0;
     bool rfree = wave >= a.n_rwaves;     // this wave's buffer is free of the router rows
+    bool tab_ready = false;
 
     // the claimed entry j: its tile, source address (0: no weights) and the
     // count of load instructions sent for it
@@ -428,30 +472,53 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
     TileDesc d = {};
     uint64_t G = 0ull;
     bool sent = false;
+    // The next entry and its tile: from the descriptor table once every
+    // streaming wave has written its part of it (the first claim, before
+    // that, computes its tile itself).
+    // take(v): entry v (lane 0's value) becomes the claimed one
+    auto take = [&](uint32_t v) {
+        j = min(__builtin_amdgcn_readfirstlane((int)v), n);
+        if (j < n) {
+            if (tab_ready) {
+                const u32x4 e = tab[j];
+                d = desc_unpack(e);
+            } else {
+                d = tile_desc<GUT, DT, SGUT, SDT>(a, P, L.at(j), lg_gu, lg_dn);
+            }
+        }
+        sent = false;
+    };
     auto claim = [&]() {
         uint32_t v = 0u;
         if (lane == 0) v = __hip_atomic_fetch_add(&ctl->next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        j = min(__builtin_amdgcn_readfirstlane((int)v), n);
-        if (j < n) d = tile_desc<GUT, DT, SGUT, SDT>(a, P, L.at(j), lg_gu, lg_dn);
-        sent = false;
+        take(v);
     };
+    // (the addresses of the shared expert's matrices and of the SwiGLU
+    // hand-off words, read once)
+    const uint64_t b_sg = sval(a.sh_gate), b_su = sval(a.sh_up), b_sd = sval(a.sh_down), b_act = sval(a.tact);
     // Send the claimed tile's loads; false (nothing sent) when it needs a pick
     // or its buffer that is not available yet and !block.
     auto send = [&](bool block) -> bool {
         uint64_t base;
         if (routed_kind(d.kind)) {
-            if ((int)lds_ld(&ctl->npicked) <= d.slot) {
+            // the slot's matrix address, published by the routing with the pick
+            const lds64_t* rb = (const lds64_t*)&ctl->rbase[d.slot][d.kind == K_RG ? 0 : d.kind == K_RU ? 1 : 2];
+            uint64_t b = lds_ld64(rb);
+            if (!b) {
                 if (!block) return false;
-                lds_wait(ctl, &ctl->npicked, (uint32_t)(d.slot + 1), a.status, lane);
+                uint32_t it = 0;
+                while ((b = lds_ld64(rb)) == 0ull) {
+                    if (++it > PSPIN || aborted(ctl)) {
+                        give_up(ctl, a.status, lane);
+                        b = 1ull;
+                        break;
+                    }
+                    backoff(it);
+                }
             }
-            const int64_t e = (int)lds_ld((const lds32_t*)&ctl->ids[d.slot]);
-            const bool ok = lds_ld((const lds32_t*)&ctl->valid[d.slot]) != 0u;
-            const uint64_t mb = d.kind == K_RG ? sval(a.gate) : d.kind == K_RU ? sval(a.up) : sval(a.down);
-            const uint64_t st = d.kind == K_RG ? sval64(a.gstride) : d.kind == K_RU ? sval64(a.ustride) : sval64(a.dstride);
-            base = ok ? mb + (uint64_t)e * st : 0ull;
+            base = b & ~1ull;
         } else {
-            base = d.kind == K_SG ? sval(a.sh_gate) : d.kind == K_SU ? sval(a.sh_up)
-                 : d.kind == K_ACT ? sval(a.tact) : sval(a.sh_down);
+            base = d.kind == K_SG ? b_sg : d.kind == K_SU ? b_su : d.kind == K_ACT ? b_act : b_sd;
         }
         if (!rfree) {
             if (!block) return false;
@@ -534,6 +601,15 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
     if (active) {
         claim();
         if (j < n && rfree) send(false);
+        // this wave's part of the descriptor table: entries 64 w + lane,
+        // every 64 nstream entries
+        for (int j0 = 64 * wave; j0 < n; j0 += 64 * a.nstream) {
+            const int jl = min(j0 + lane, n - 1);
+            const TileDesc e = tile_desc<GUT, DT, SGUT, SDT>(a, P, L.at_lane(jl), lg_gu, lg_dn);
+            if (j0 + lane < n) tab[jl] = desc_pack(e);
+        }
+        WM_WAIT_LGKM0();
+        if (lane == 0) __hip_atomic_fetch_add(&ctl->desc_built, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
     {
         const int nseg = H / SEG, part = lane & 7;
@@ -559,20 +635,38 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
         lds_set(&ctl->xop_built[wave], 1u, lane);
     }
     wait_all(ctl, ctl->xop_built, PW, a.status, lane);
+    if (active) {
+        lds_wait(ctl, &ctl->desc_built, (uint32_t)a.nstream, a.status, lane);
+        tab_ready = true;
+    }
     if (wave == 0 && lane == 0) ctl->t[8] = now();
 
     while (j < n) {
         if (!sent) send(true);
         WM_WAIT_VMCNT(0);         // (the claimed tile's loads are the only ones in flight)
+        // The next entry's index is taken now, its LDS atomic completing while
+        // this tile is processed -- except behind an act tile, which waits for
+        // every workgroup's SwiGLU outputs of its slot: an entry held behind
+        // it (a gate/up tile of a later slot) would hold this workgroup's
+        // outputs of that slot back from all the others.
+        const bool early = d.kind != K_ACT;
+        uint32_t nv = 0u;
+        if (early && lane == 0)
+            nv = __hip_atomic_fetch_add(&ctl->next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         process();
-        // counted after the row sums (LDS executes one wave's operations in order)
+        // counted after the row sums (LDS executes one wave's operations in
+        // order): gate/up tiles for the SwiGLU publisher, down tiles for the
+        // combine (an act tile sets its own flags)
         if (lane == 0) {
             if (d.kind <= K_RU)
                 __hip_atomic_fetch_add(&ctl->gu_done[d.slot], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            __hip_atomic_fetch_add(&ctl->n_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            else if (d.kind != K_ACT)
+                __hip_atomic_fetch_add(&ctl->n_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
         wave_lds_sync();          // every lane's reads of the buffer are done before it is refilled
-        claim();
+        if (!early && lane == 0)
+            nv = __hip_atomic_fetch_add(&ctl->next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        take(nv);
     }
     if (wave == 0 && lane == 0) ctl->t[9] = now();
 }
@@ -636,6 +730,17 @@ WM_DEV void router_chains(const lds8_t* lx, int region, int H, int r0, int ra, i
     if (c < P_REP) gst_agent64(tlogits + (int64_t)c * E + r0 + row, tagged(tag, acc));
 }
 
+// The byte addresses of expert e's gate, up and down matrices for routed
+// slot k, each | 1 (bit 0 marks the slot as published; the matrices are
+// 16-byte aligned), or 1 alone for a slot without an expert.
+WM_DEV void publish_bases(const PersistArgs& a, lctl_t* ctl, int k, int e, bool valid) {
+    typedef __attribute__((address_space(3))) uint64_t l64;
+    l64* rb = (l64*)&ctl->rbase[k][0];
+    rb[0] = valid ? ((uint64_t)(uintptr_t)a.gate + (uint64_t)e * (uint64_t)a.gstride) | 1ull : 1ull;
+    rb[1] = valid ? ((uint64_t)(uintptr_t)a.up + (uint64_t)e * (uint64_t)a.ustride) | 1ull : 1ull;
+    rb[2] = valid ? ((uint64_t)(uintptr_t)a.down + (uint64_t)e * (uint64_t)a.dstride) | 1ull : 1ull;
+}
+
 // Routing from replica `rep` of the tagged logits (polled, with a pause
 // between polls, until every one carries `tag`), then the K-pass arg-max and
 // softmax of wave_topk_n.  Lanes k < K return their pick (id, weight).
@@ -683,10 +788,13 @@ WM_DEV void route_tagged(const PersistArgs& a, lctl_t* ctl, int rep, uint32_t ta
         const uint64_t best = pk.next();
         degenerate = degenerate || best == 0ull;
         kb = lane == k ? best : kb;
-        // each pick goes out at once: its slot's weights can start streaming
+        // each pick goes out at once, with its expert's gate / up / down
+        // addresses: its slot's weights can start streaming
         if (lane == 0) {
-            ctl->ids[k] = Picker<MAXV>::id_of(best);
+            const int e = Picker<MAXV>::id_of(best);
+            ctl->ids[k] = e;
             ctl->valid[k] = 1;
+            publish_bases(a, ctl, k, e, true);
         }
         lds_set(&ctl->npicked, (uint32_t)(k + 1), lane);
     }
@@ -708,8 +816,10 @@ WM_DEV void route_tagged(const PersistArgs& a, lctl_t* ctl, int rep, uint32_t ta
 // H <= 256 * NST: ss = sum of (double)h[i]^2 (each product exact in fp64),
 // lane l keeping four sums s_c over its elements 4l + 256k + c (k in order),
 // ss_l = (s_0 + s_1) + (s_2 + s_3), then an xor tree over the lanes (32, 16,
-// ..., 1) -- the reference adds in index order, which can differ in the last
-// bits of ss --, scale = 1 / sqrtf((float)(ss / H) + eps) correctly rounded,
+// ..., 1); the reference adds in index order, which can differ in the last
+// bits of ss, so when the two could round (float)(ss / H) differently the sum
+// is taken again in index order (the scale is then the reference's bit for
+// bit); scale = 1 / sqrtf((float)(ss / H) + eps) correctly rounded,
 // x[i] = (h[i] * scale) * w[i], w in LDS at wl.  Straight-line code: the
 // reads of a batch are in flight together.  Each region holds at least 256
 // floats, so every read is inside it.
@@ -736,7 +846,27 @@ WM_DEV void rmsnorm_lds(lf32_t* xl, const lf32_t* wl, int H, float eps, int lane
     }
     double ss = in ? (s0 + s1) + (s2 + s3) : 0.0;
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
+    for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);       // (the same value in every lane)
+    // The reference adds the squares in index order (attention.h:31-34).  The
+    // terms are exact and non-negative, so any order of the H - 1 additions is
+    // within (H - 1) * 2^-53 of the exact sum relative to it: this sum and the
+    // reference's differ by less than 2H * 2^-53 * ss, and after the division
+    // (each correctly rounded) qt = ss / H differs from the reference's by
+    // less than dq.  Rounding to float is monotonic: when qt - dq and qt + dq
+    // round to the same float, so does the reference's quotient.  Otherwise (a
+    // float rounding boundary within dq of qt: about one vector in 10^5 at
+    // H = 4096) the sum is taken again in index order.
+    const double qt = ss / (double)H;
+    const double dq = qt * ((double)(2 * H + 8) * 0x1p-53) * 1.0625;
+    if ((float)(qt - dq) != (float)(qt + dq)) {
+        const lf32_t* hx = xl;
+        double s = 0.0;
+        for (int i = 0; i < H; i++) {
+            const double v = (double)hx[i];
+            s += v * v;                      // (exact product, rounded sum: the reference's step)
+        }
+        ss = s;
+    }
     const float scale = __fdiv_rn(1.0f, __fsqrt_rn((float)(ss / (double)H) + eps));
 #pragma unroll
     for (int k0 = 0; k0 < NST; k0 += B) {
@@ -892,6 +1022,7 @@ WM_DEV void helper_router(const PersistArgs& a, uint8_t* smem, int lane) {
         ctl->ids[lane] = my_e;
         ctl->w[lane] = valid ? wk : 0.0f;
         ctl->valid[lane] = valid ? 1 : 0;
+        if (a.forced) publish_bases(a, ctl, lane, my_e, valid);     // (routed: with each pick)
     }
     lds_set(&ctl->npicked, (uint32_t)K, lane);     // (forced routing: all at once)
     lds_set(&ctl->routed, 1u, lane);
@@ -934,7 +1065,7 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
     // the counts of this workgroup's list (TileList: per slot, 2 * ngu gate/up
     // tiles, nact act tiles when it has down rows, ndn down tiles); building
     // the list itself here took ~2 us of this wave's time
-    const int n_gu = 2 * P.ngu, n_all = nq * (n_gu + (P.ndn > 0 ? a.nact : 0) + P.ndn);
+    const int n_gu = 2 * P.ngu, n_dn = nq * P.ndn;
     if (P.ngu > 0) {
         const int rpt = geometry(GUT, a.H).rpt;
         const int row0 = P.tw0 * rpt, nrows = min(a.I, (P.tw0 + P.ngu) * rpt) - row0;
@@ -972,7 +1103,7 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
             vk[k] = k < K && ctl->valid[k] != 0;
             wk[k] = k < K ? ctl->w[k] : 0.0f;
         }
-        lds_wait(ctl, &ctl->n_done, (uint32_t)n_all, a.status, lane);   // every entry is processed
+        lds_wait(ctl, &ctl->n_done, (uint32_t)n_dn, a.status, lane);   // every down tile is processed
         if (lane == 0) ctl->t[6] = now();
         for (int r = lane; r < nrows; r += 64) {
             // out[h] = sum_k w_k y_k[h] (k order, invalid ids skipped) + gate * y_shared[h]

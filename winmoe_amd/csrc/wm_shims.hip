@@ -99,9 +99,11 @@ class ExpertTable {
         if (slot < 0 || slot >= count() || !slots_[slot].mem) return nullptr;
         return &slots_[slot];
     }
+    // The recycling cursor is left as it is: as in gpu_offload.cu:582-623,
+    // the next recycle of a full table takes the slot under it (which may lie
+    // past a lowered capacity) and only then wraps it modulo the capacity.
     void set_capacity(int n) {
         capacity_ = std::min(std::max(n, 1), kCapacityCeiling);
-        cursor_ %= capacity_;
         fprintf(stderr, "winmoe_hip: expert table capacity now %d slots (ceiling %d)\n", capacity_,
                 kCapacityCeiling);
     }

@@ -131,17 +131,18 @@ extern "C" int wm_pool_layer(const wm_expert_pool* pool, wm_layer_desc* d) {
     return WM_OK;
 }
 
-extern "C" int wm_pool_acquire(wm_expert_pool* pool, int layer, const int32_t* ids, int n, const void* gate_src,
-                               const void* up_src, const void* down_src, int64_t gate_stride, int64_t up_stride,
-                               int64_t down_stride, int32_t* slots_dev, void* stream) {
-    WM_CHECK_ARG(pool && ids && n >= 1 && n <= pool->n_slots && layer >= 0);
-    WM_CHECK_ARG(gate_src && up_src && down_src && slots_dev && ((uintptr_t)slots_dev % 4) == 0);
-    WM_CHECK_ARG(gate_stride >= pool->part[0] && up_stride >= pool->part[1] && down_stride >= pool->part[2]);
-    for (int i = 0; i < n; i++) WM_CHECK_ARG(ids[i] >= 0);
+// Makes ids[0..n) of `layer` resident; copy(i, slot) enqueues the copies of
+// ids[i] into `slot` on the pool's stream and returns the bytes it copies (< 0
+// on a HIP failure).  Shared by the per-part and the packed sources.
+template <class Copy>
+static int pool_acquire(wm_expert_pool* pool, int layer, const int32_t* ids, int n, int n_src, int32_t* slots_dev,
+                        void* stream, Copy copy) {
+    WM_CHECK_ARG(pool && ids && n >= 1 && n <= pool->n_slots && layer >= 0 && n_src >= 1);
+    WM_CHECK_ARG(slots_dev && ((uintptr_t)slots_dev % 4) == 0);
+    // every id names an expert of the source (checked before any state changes)
+    for (int i = 0; i < n; i++) WM_CHECK_ARG(ids[i] >= 0 && ids[i] < n_src);
     wm_expert_pool& P = *pool;
     hipStream_t s = (hipStream_t)stream;
-    const void* src[3] = {gate_src, up_src, down_src};
-    const int64_t sstride[3] = {gate_stride, up_stride, down_stride};
     // refuse up front (no state changes) when the misses would find no slot:
     // they need as many slots as are neither held by unreleased acquires nor
     // hit by this call
@@ -199,12 +200,9 @@ extern "C" int wm_pool_acquire(wm_expert_pool* pool, int layer, const int32_t* i
                 if (P.key[slot] >= 0) P.where.erase(P.key[slot]);
                 // the pool's stream rewrites the slot once the steps that read it are over
                 if (P.done_set[slot]) WM_FAIL_HIP(hipStreamWaitEvent(P.copy, P.done[slot], 0));
-                for (int m = 0; m < 3; m++) {
-                    const uint8_t* from = (const uint8_t*)src[m] + (int64_t)ids[i] * sstride[m];
-                    WM_FAIL_HIP(hipMemcpyAsync(P.base + (int64_t)slot * P.slot_bytes + P.off[m], from,
-                                               (size_t)P.part[m], hipMemcpyHostToDevice, P.copy));
-                    P.bytes += P.part[m];
-                }
+                const int64_t nb = copy(i, slot);
+                if (nb < 0) return WM_ERR;
+                P.bytes += nb;
                 WM_FAIL_HIP(hipEventRecord(P.ready[slot], P.copy));
                 P.ready_set[slot] = 1;
                 P.key[slot] = k;
@@ -228,6 +226,46 @@ extern "C" int wm_pool_acquire(wm_expert_pool* pool, int layer, const int32_t* i
     P.ring_set[P.ring_pos] = 1;
     P.ring_pos = (P.ring_pos + 1) % kRing;
     return nmiss;
+}
+
+extern "C" int wm_pool_acquire(wm_expert_pool* pool, int layer, const int32_t* ids, int n, int n_src,
+                               const void* gate_src, const void* up_src, const void* down_src, int64_t gate_stride,
+                               int64_t up_stride, int64_t down_stride, int32_t* slots_dev, void* stream) {
+    WM_CHECK_ARG(pool && gate_src && up_src && down_src);
+    WM_CHECK_ARG(gate_stride >= pool->part[0] && up_stride >= pool->part[1] && down_stride >= pool->part[2]);
+    const void* src[3] = {gate_src, up_src, down_src};
+    const int64_t sstride[3] = {gate_stride, up_stride, down_stride};
+    wm_expert_pool& P = *pool;
+    return pool_acquire(pool, layer, ids, n, n_src, slots_dev, stream, [&](int i, int slot) -> int64_t {
+        int64_t nb = 0;
+        for (int m = 0; m < 3; m++) {
+            const uint8_t* from = (const uint8_t*)src[m] + (int64_t)ids[i] * sstride[m];
+            if (hipMemcpyAsync(P.base + (int64_t)slot * P.slot_bytes + P.off[m], from, (size_t)P.part[m],
+                               hipMemcpyHostToDevice, P.copy) != hipSuccess) {
+                fprintf(stderr, "winmoe_hip: expert pool: host-to-device copy failed\n");
+                return -1;
+            }
+            nb += P.part[m];
+        }
+        return nb;
+    });
+}
+
+extern "C" int wm_pool_acquire_packed(wm_expert_pool* pool, int layer, const int32_t* ids, int n, int n_src,
+                                      const void* src, int64_t src_stride, int32_t* slots_dev, void* stream) {
+    WM_CHECK_ARG(pool && src && src_stride >= pool->slot_bytes);
+    wm_expert_pool& P = *pool;
+    return pool_acquire(pool, layer, ids, n, n_src, slots_dev, stream, [&](int i, int slot) -> int64_t {
+        // one copy of the expert's whole image: [gate | up | down] at the
+        // slot's own part offsets, up to the end of the down part
+        const int64_t nb = P.off[2] + P.part[2];
+        if (hipMemcpyAsync(P.base + (int64_t)slot * P.slot_bytes, (const uint8_t*)src + (int64_t)ids[i] * src_stride,
+                           (size_t)nb, hipMemcpyHostToDevice, P.copy) != hipSuccess) {
+            fprintf(stderr, "winmoe_hip: expert pool: host-to-device copy failed\n");
+            return -1;
+        }
+        return P.part[0] + P.part[1] + P.part[2];
+    });
 }
 
 extern "C" int wm_pool_release(wm_expert_pool* pool, void* stream) {

@@ -465,12 +465,21 @@ template <int MAXV> struct Picker {
         head = lane_max<MAXV>(key);
     }
     // Next pick: its key (0 = degenerate, nothing valid left) in every lane.
-    // The wave maximum of the 64-bit heads in two 32-bit passes: the largest
-    // upper half, then the largest lower half among the lanes holding it.
+    // The wave maximum of the 64-bit heads: the largest upper half; when one
+    // lane alone holds it (the upper half is the logit's order bits, so
+    // unless two logits are equal) that lane's head is the maximum, else a
+    // second pass takes the largest lower half among the lanes holding it.
     WM_DEV uint64_t next() {
         const uint32_t hh = (uint32_t)(head >> 32);
         const uint32_t hi = wave_max_u32(hh);
-        const uint32_t lo = wave_max_u32(hh == hi ? (uint32_t)head : 0u);
+        const uint64_t at_hi = __builtin_amdgcn_ballot_w64(hh == hi);
+        uint32_t lo;
+        if (__builtin_popcountll(at_hi) == 1) {
+            const int wl = (int)__builtin_ctzll(at_hi);
+            lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)head, wl);
+        } else {
+            lo = wave_max_u32(hh == hi ? (uint32_t)head : 0u);
+        }
         const uint64_t best = ((uint64_t)hi << 32) | lo;
         if (best != 0ull && head == best) {
 #pragma unroll

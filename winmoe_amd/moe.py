@@ -417,24 +417,57 @@ class ExpertPool:
         return MoELayer(H, I, self.n_slots, K, None, views[0], views[1], views[2], types, shared=shared,
                         max_tokens=max_tokens, strides=(self.slot_bytes,) * 3, **kw)
 
+    def _ids(self, ids, n_src: int) -> np.ndarray:
+        ids = np.ascontiguousarray(np.asarray(ids, dtype=np.int32).reshape(-1))
+        if ids.size and (ids.min() < 0 or ids.max() >= n_src):
+            raise ValueError(f"expert ids must lie in [0, {n_src}) (the host source's experts)")
+        return ids
+
     def acquire(self, layer: int, ids, gate_src: torch.Tensor, up_src: torch.Tensor, down_src: torch.Tensor,
                 out: Optional[torch.Tensor] = None, stream=None):
         """Makes experts ``ids`` of ``layer`` resident (copies the missing ones
-        from the host tensors ``*_src`` [E][bytes]); returns (slots, misses):
-        the device int32 slot indices, written in stream order, and the miss
-        count."""
-        ids = np.ascontiguousarray(np.asarray(ids, dtype=np.int32).reshape(-1))
+        from the host tensors ``*_src`` [E][bytes], three copies per expert);
+        returns (slots, misses): the device int32 slot indices, written in
+        stream order, and the miss count."""
         for t, n in ((gate_src, "gate_src"), (up_src, "up_src"), (down_src, "down_src")):
             if t.device.type != "cpu" or t.dtype != torch.uint8 or t.dim() != 2 or not t.is_contiguous():
                 raise ValueError(f"{n} must be a contiguous uint8 host tensor [E][bytes]")
+        n_src = gate_src.shape[0]
+        if up_src.shape[0] != n_src or down_src.shape[0] != n_src:
+            raise ValueError("gate_src, up_src and down_src must hold the same experts")
+        ids = self._ids(ids, n_src)
         if out is None:
             out = torch.empty(ids.size, dtype=torch.int32, device=self.mem.device)
-        rc = load().wm_pool_acquire(self._h, layer, ids.ctypes.data_as(C.POINTER(C.c_int32)), ids.size,
+        rc = load().wm_pool_acquire(self._h, layer, ids.ctypes.data_as(C.POINTER(C.c_int32)), ids.size, n_src,
                                     gate_src.data_ptr(), up_src.data_ptr(), down_src.data_ptr(),
                                     gate_src.stride(0), up_src.stride(0), down_src.stride(0), _p(out),
                                     _stream(stream))
         if rc < 0:
             check(rc, "wm_pool_acquire")
+        return out, rc
+
+    def pack(self, gate_src: torch.Tensor, up_src: torch.Tensor, down_src: torch.Tensor,
+             pin: bool = True) -> torch.Tensor:
+        """Host tensor [E][slot_bytes] holding each expert as one slot image
+        ([gate | up | down] at the slot's 256-byte aligned part offsets), the
+        source of ``acquire_packed``."""
+        E = gate_src.shape[0]
+        out = torch.zeros((E, self.slot_bytes), dtype=torch.uint8, pin_memory=pin)
+        for o, t, nb in zip(self.offsets, (gate_src, up_src, down_src), self.parts):
+            out[:, o:o + nb] = t[:, :nb]
+        return out
+
+    def acquire_packed(self, layer: int, ids, src: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None):
+        """As ``acquire``, from slot images (``pack``): one copy per missing expert."""
+        if src.device.type != "cpu" or src.dtype != torch.uint8 or src.dim() != 2 or not src.is_contiguous():
+            raise ValueError("src must be a contiguous uint8 host tensor [E][slot_bytes]")
+        ids = self._ids(ids, src.shape[0])
+        if out is None:
+            out = torch.empty(ids.size, dtype=torch.int32, device=self.mem.device)
+        rc = load().wm_pool_acquire_packed(self._h, layer, ids.ctypes.data_as(C.POINTER(C.c_int32)), ids.size,
+                                           src.shape[0], src.data_ptr(), src.stride(0), _p(out), _stream(stream))
+        if rc < 0:
+            check(rc, "wm_pool_acquire_packed")
         return out, rc
 
     def release(self, stream=None) -> None:

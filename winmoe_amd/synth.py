@@ -66,6 +66,11 @@ CONFIGS = {
                       types=(Q2_K, Q2_K, Q3_K), tokens=512, routing="zipf_overlap", n_layers=8),
     "c5": LayerConfig("e512_k10_h4096_i1024_q8_0_prefill512_zipf", E=512, K=10, H=4096, I=1024,
                       types=(Q8_0, Q8_0, Q8_0), tokens=512, routing="zipf", x_dtype="bf16"),
+    # the c5 layer routed by its own router (fp32 N(0, 0.02) weights: close to
+    # uniform routing, every expert used), so the batch includes the router
+    # logits and top-K of all 512 tokens
+    "c5r": LayerConfig("e512_k10_h4096_i1024_q8_0_prefill512_router", E=512, K=10, H=4096, I=1024,
+                       types=(Q8_0, Q8_0, Q8_0), tokens=512, routing="router", x_dtype="bf16"),
     # the c3 layer (K-quant experts, Q8_0 shared expert) under a 512-token prefill
     "c3p": LayerConfig("e512_k3_h4096_i1024_q4k_q6k_shared_q8_0_prefill512_zipf", E=512, K=3, H=4096, I=1024,
                        types=(Q4_K, Q4_K, Q6_K), shared_types=(Q8_0, Q8_0, Q8_0), shared_inter=1024,
