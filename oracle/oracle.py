@@ -62,6 +62,7 @@ def lib():
         L.wmo_fp16_to_fp32.restype = C.c_float
         L.wmo_fp16_to_fp32.argtypes = [C.c_uint16]
         L.wmo_dequant.argtypes = [C.c_int, _vp, C.c_int64, _fp]
+        L.wmo_dequant_block_sums.argtypes = [C.c_int, _vp, C.c_int64, C.POINTER(C.c_int64), C.POINTER(C.c_int64)]
         L.wmo_router_logits.argtypes = [_fp, _fp, C.c_int, C.c_int, _fp]
         L.wmo_topk_softmax.argtypes = [_fp, C.c_int, C.c_int, _ip, _fp]
         L.wmo_rmsnorm.argtypes = [_fp, _fp, _fp, C.c_int, C.c_float]
@@ -121,6 +122,40 @@ def dequant(qtype: int, blocks: np.ndarray) -> np.ndarray:
     rc = lib().wmo_dequant(qtype, _ptr(b), nb, _ptr(out, _fp))
     assert rc == 0, rc
     return out
+
+
+def dequant_block_sums(qtype: int, blocks: np.ndarray, threads: int = 1):
+    """Per-block checksums of the dequantised weights (wmo_dequant_block_sums):
+    s1[i] = sum over block i of the values' fp32 bit patterns (unsigned),
+    s2[i] = the same weighted by position + 1.  `threads` workers split the
+    blocks (the C call releases the GIL)."""
+    b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
+    bs = BLOCK_BYTES[qtype]
+    assert b.size % bs == 0
+    nb = b.size // bs
+    s1 = np.empty(nb, np.int64)
+    s2 = np.empty(nb, np.int64)
+    L = lib()
+    _i64 = C.POINTER(C.c_int64)
+
+    def part(r):
+        i0, i1 = r
+        if i1 <= i0:
+            return 0
+        return L.wmo_dequant_block_sums(qtype, b.ctypes.data + i0 * bs, i1 - i0,
+                                        C.cast(s1.ctypes.data + 8 * i0, _i64), C.cast(s2.ctypes.data + 8 * i0, _i64))
+
+    n = max(1, int(threads))
+    step = (nb + n - 1) // n
+    ranges = [(i, min(nb, i + step)) for i in range(0, nb, step)] or [(0, 0)]
+    if n == 1 or len(ranges) == 1:
+        rcs = [part(r) for r in ranges]
+    else:
+        from concurrent.futures import ThreadPoolExecutor
+        with ThreadPoolExecutor(max_workers=n) as ex:
+            rcs = list(ex.map(part, ranges))
+    assert all(rc == 0 for rc in rcs), rcs
+    return s1, s2
 
 
 def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float = 1e-6) -> np.ndarray:

@@ -391,3 +391,27 @@ def test_rmsnorm_closed_forms(orc):
     x[17] = 8.0
     scale = np.float32(1.0) / np.sqrt(np.float32(64.0 / dim) + np.float32(1e-6))
     assert same_bits(orc.rmsnorm(x, w), (x * scale) * w)
+
+
+@pytest.mark.parametrize("qt", [Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K])
+def test_dequant_block_sums(orc, qt):
+    """The per-block checksums the full-trace dequant test compares: each
+    block's sums of its dequantised bit patterns (plain and position-weighted),
+    here computed again in numpy from wmo_dequant; threaded splits agree with
+    one call; a change to one weight of one block moves that block's sums
+    and no other's."""
+    rng = np.random.default_rng(qt)
+    n = 257
+    b = rand_blocks(qt, n, rng)
+    ne = {Q8_0: 32}.get(qt, 256)
+    u = orc.dequant(qt, b).view(np.uint32).astype(np.int64).reshape(n, ne)
+    s1, s2 = orc.dequant_block_sums(qt, b)
+    assert np.array_equal(s1, u.sum(1))
+    assert np.array_equal(s2, (u * np.arange(1, ne + 1)).sum(1))
+    t1, t2 = orc.dequant_block_sums(qt, b, threads=5)
+    assert np.array_equal(s1, t1) and np.array_equal(s2, t2)
+    b2 = b.copy()
+    b2[100, -1] ^= 0x11          # the last quant byte of block 100
+    c1, c2 = orc.dequant_block_sums(qt, b2)
+    moved = (c1 != s1) | (c2 != s2)
+    assert moved[100] and moved.sum() == 1
