@@ -116,7 +116,7 @@ struct PersistCtl {
     int32_t valid[PMAXK];
     float sgate;
     uint32_t x_in;                 // x is in LDS (the second staging wave loads it)
-    uint32_t desc_built;           // streaming waves that have written their part of the tile descriptors
+    uint32_t desc_built;           // the tile descriptor table is built
     uint64_t rbase[PMAXK][3];      // routed slot k's gate / up / down bytes | 1 (1 alone: no weights), 0 until picked
     uint64_t t[P_TL];              // timeline (device clock)
 };

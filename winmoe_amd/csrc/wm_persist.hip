@@ -185,6 +185,9 @@ template <int CPOL> WM_DEV int act_dma(uint64_t G, int nbytes, int lane, lds8_t*
 }
 
 // ------------------------------------------------------------------ tile list
+// Tile lists longer than this (entries per workgroup, at most) have their
+// descriptor table built by the streaming waves, shorter ones by the x loader.
+constexpr int P_TAB_SPLIT = 128;
 enum : int { K_SG = 0, K_SU = 1, K_RG = 2, K_RU = 3, K_SD = 4, K_RD = 5, K_ACT = 6 };
 struct TRef {
     int kind, slot, t;    // t: tile within the workgroup's range
@@ -193,14 +196,29 @@ struct TRef {
 struct Part {
     int w, tw0, ngu, d0, ndn;
 };
+// floor(x / d) for wave-uniform 0 <= x <= 2^22, 0 < d <= 2^12: the fp32 quotient from
+// the hardware reciprocal is within 0.75 of x / d (relative error below
+// 1.5 * 2^-23 on a value at most 2^22), so the truncated quotient is off by
+// at most one, which the two corrections remove.  A few VALU operations where
+// the compiler's integer division is a long dependent sequence (~150
+// operations for a 64-bit one), which every wave ran at the start of a step.
+WM_DEV int udiv22(int x, int d) {
+    uint32_t q = (uint32_t)((float)x * __builtin_amdgcn_rcpf((float)d));
+    if ((int)q * d > x) q--;
+    if (((int)q + 1) * d <= x) q++;
+    return __builtin_amdgcn_readfirstlane((int)q);     // (uniform: its inputs are)
+}
+
+// The workgroup's share of every phase (rows w * n / nwg .. (w + 1) * n / nwg
+// of each split; nwg <= 1024 and n <= 4096, so every product is below 2^22).
 WM_DEV Part partition(const PersistArgs& a) {
     Part p;
     p.w = (int)blockIdx.x;
-    const int gs = a.gu_step, gu_units = a.gu_tiles / gs;
-    p.tw0 = gs * (int)((int64_t)p.w * gu_units / a.nwg);
-    p.ngu = gs * (int)((int64_t)(p.w + 1) * gu_units / a.nwg) - p.tw0;
-    p.d0 = (int)((int64_t)p.w * a.dn_tiles / a.nwg);
-    p.ndn = (int)((int64_t)(p.w + 1) * a.dn_tiles / a.nwg) - p.d0;
+    const int gs = a.gu_step, gu_units = gs == 2 ? a.gu_tiles >> 1 : a.gu_tiles;    // (gu_step is 1 or 2)
+    p.tw0 = gs * udiv22(p.w * gu_units, a.nwg);
+    p.ngu = gs * udiv22((p.w + 1) * gu_units, a.nwg) - p.tw0;
+    p.d0 = udiv22(p.w * a.dn_tiles, a.nwg);
+    p.ndn = udiv22((p.w + 1) * a.dn_tiles, a.nwg) - p.d0;
     return p;
 }
 
@@ -399,8 +417,9 @@ WM_DEV TileDesc tile_desc(const PersistArgs& a, const Part& P, const TRef& r, in
     const bool gu = r.kind <= K_RU;
     const int rpt_gu = SEG >> lg_gu, rpt_dn = SEG >> lg_dn;
     const int rpt = gu ? rpt_gu : rpt_dn, rows = gu ? I : H, abs_t = (gu ? P.tw0 : P.d0) + r.t;
-    const int tt = r.kind == K_SG || r.kind == K_SU ? SGUT : r.kind == K_SD ? SDT : gu ? GUT : DT;
-    const int64_t rb = matrix_bytes(tt, 1, gu ? H : I);
+    // (row bytes per instantiated type: divisions by constants)
+    const int64_t rb = r.kind == K_SG || r.kind == K_SU ? matrix_bytes(SGUT, 1, H) : r.kind == K_SD ? matrix_bytes(SDT, 1, I)
+                     : gu ? matrix_bytes(GUT, 1, H) : matrix_bytes(DT, 1, I);
     TileDesc d;
     d.rows = min(rpt, rows - abs_t * rpt);
     d.kind = r.kind;
@@ -472,13 +491,13 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
     TileDesc d = {};
     uint64_t G = 0ull;
     bool sent = false;
-    // The next entry and its tile: from the descriptor table once every
-    // streaming wave has written its part of it (the first claim, before
-    // that, computes its tile itself).
+    // The next entry and its tile: from the descriptor table once it is
+    // built (until then a claim computes its tile itself).
     // take(v): entry v (lane 0's value) becomes the claimed one
     auto take = [&](uint32_t v) {
         j = min(__builtin_amdgcn_readfirstlane((int)v), n);
         if (j < n) {
+            if (!tab_ready) tab_ready = lds_ld(&ctl->desc_built) >= (uint32_t)a.nstream;
             if (tab_ready) {
                 const u32x4 e = tab[j];
                 d = desc_unpack(e);
@@ -601,15 +620,6 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
     if (active) {
         claim();
         if (j < n && rfree) send(false);
-        // this wave's part of the descriptor table: entries 64 w + lane,
-        // every 64 nstream entries
-        for (int j0 = 64 * wave; j0 < n; j0 += 64 * a.nstream) {
-            const int jl = min(j0 + lane, n - 1);
-            const TileDesc e = tile_desc<GUT, DT, SGUT, SDT>(a, P, L.at_lane(jl), lg_gu, lg_dn);
-            if (j0 + lane < n) tab[jl] = desc_pack(e);
-        }
-        WM_WAIT_LGKM0();
-        if (lane == 0) __hip_atomic_fetch_add(&ctl->desc_built, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
     {
         const int nseg = H / SEG, part = lane & 7;
@@ -634,25 +644,26 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
         }
         lds_set(&ctl->xop_built[wave], 1u, lane);
     }
-    wait_all(ctl, ctl->xop_built, PW, a.status, lane);
-    if (active) {
-        lds_wait(ctl, &ctl->desc_built, (uint32_t)a.nstream, a.status, lane);
-        tab_ready = true;
+    // A long list's descriptor table is built by the streaming waves
+    // themselves (entries 64 w + lane, every 64 nstream entries), after
+    // their records: with many slots the routing leaves them time to spare
+    // and the x loader alone would finish it after the first claims.  A
+    // short one is the x loader's.
+    if (active && a.n_desc > P_TAB_SPLIT) {
+        for (int j0 = 64 * wave; j0 < n; j0 += 64 * a.nstream) {
+            const int jl = min(j0 + lane, n - 1);
+            const TileDesc e = tile_desc<GUT, DT, SGUT, SDT>(a, P, L.at_lane(jl), lg_gu, lg_dn);
+            if (j0 + lane < n) tab[jl] = desc_pack(e);
+        }
+        WM_WAIT_LGKM0();
+        if (lane == 0) __hip_atomic_fetch_add(&ctl->desc_built, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
+    wait_all(ctl, ctl->xop_built, PW, a.status, lane);
     if (wave == 0 && lane == 0) ctl->t[8] = now();
 
     while (j < n) {
         if (!sent) send(true);
         WM_WAIT_VMCNT(0);         // (the claimed tile's loads are the only ones in flight)
-        // The next entry's index is taken now, its LDS atomic completing while
-        // this tile is processed -- except behind an act tile, which waits for
-        // every workgroup's SwiGLU outputs of its slot: an entry held behind
-        // it (a gate/up tile of a later slot) would hold this workgroup's
-        // outputs of that slot back from all the others.
-        const bool early = d.kind != K_ACT;
-        uint32_t nv = 0u;
-        if (early && lane == 0)
-            nv = __hip_atomic_fetch_add(&ctl->next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         process();
         // counted after the row sums (LDS executes one wave's operations in
         // order): gate/up tiles for the SwiGLU publisher, down tiles for the
@@ -664,9 +675,10 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lan
                 __hip_atomic_fetch_add(&ctl->n_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
         wave_lds_sync();          // every lane's reads of the buffer are done before it is refilled
-        if (!early && lane == 0)
-            nv = __hip_atomic_fetch_add(&ctl->next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        take(nv);
+        // (the next entry is claimed only now: one claimed while this tile is
+        // processed would wait behind it, and an act tile held that way holds
+        // back the slot's down tiles on the other waves)
+        claim();
     }
     if (wave == 0 && lane == 0) ctl->t[9] = now();
 }
@@ -900,6 +912,28 @@ WM_DEV void vec_dma(const float* src, int H, lds8_t* dst, int lane) {
     }
 }
 
+// A short tile list as descriptors in LDS (64 entries per pass), then
+// desc_built: run by the x loader once x is in, so that no streaming wave
+// spends its start on it (a streaming wave computes the descriptor of each
+// entry it claims until the table is there).
+template <int GUT, int DT, int SGUT, int SDT>
+WM_DEV void desc_table(const PersistArgs& a, uint8_t* smem, int lane) {
+    lctl_t* ctl = (lctl_t*)smem;
+    if (a.n_desc > P_TAB_SPLIT) return;      // (the streaming waves build a long one)
+    lq4_t* const tab = (lq4_t*)((lds8_t*)smem + a.o_desc);
+    const Part P = partition(a);
+    TileList L;
+    L.init(a, P.ngu, P.ndn, lane);
+    const int n = min(L.n, a.n_desc);
+    const int lg_gu = lg_tile_lanes(a.H), lg_dn = lg_tile_lanes(a.I);
+    for (int j0 = 0; j0 < n; j0 += 64) {
+        const int jl = min(j0 + lane, n - 1);
+        const TileDesc e = tile_desc<GUT, DT, SGUT, SDT>(a, P, L.at_lane(jl), lg_gu, lg_dn);
+        if (j0 + lane < n) tab[jl] = desc_pack(e);
+    }
+    lds_set(&ctl->desc_built, (uint32_t)a.nstream, lane);
+}
+
 // x into the region at xl and the RMSNorm in place, for H <= 256 * NST; the
 // norm weights land at o_norm (over the operand records, which are built
 // only after x is in) with x.
@@ -913,7 +947,9 @@ template <int NST> WM_DEV void x_norm_in(const PersistArgs& a, uint8_t* smem, ld
 
 // The x loader (the second helper wave): x into the router region (every
 // wave's x operand records are built from there), the RMSNorm in place when
-// the layer has one (its weights come in with x).
+// the layer has one (its weights come in with x), the shared expert's gate,
+// the tile descriptor table.
+template <int GUT, int DT, int SGUT, int SDT>
 WM_DEV void helper_xload(const PersistArgs& a, uint8_t* smem, int lane) {
     lctl_t* ctl = (lctl_t*)smem;
     __builtin_amdgcn_s_setprio(3);
@@ -937,6 +973,7 @@ WM_DEV void helper_xload(const PersistArgs& a, uint8_t* smem, int lane) {
         if (lane == 0) ctl->sgate = g;
     }
     lds_set(&ctl->sgate_ready, 1u, lane);
+    desc_table<GUT, DT, SGUT, SDT>(a, smem, lane);
     // workgroup 0 advances the epoch once every workgroup has posted this
     // launch's tag (each has read the old epoch by then); the next launch
     // starts only after this one ends, so the new value is read only then
@@ -1151,7 +1188,7 @@ __global__ __launch_bounds__(PTHREADS) void k_decode_persist(PersistArgs a) {
     // routing is known (their later polling must not)
     else if (wave == PW) { __builtin_amdgcn_s_setprio(3); helper_router<GUT, DT, SGUT, SDT>(*ap, smem, lane); }
     else if (wave == PW + 1) { __builtin_amdgcn_s_setprio(3); helper_publish<GUT, DT, SGUT, SDT>(*ap, smem, lane); }
-    else if (wave == PW + 2) helper_xload(*ap, smem, lane);
+    else if (wave == PW + 2) helper_xload<GUT, DT, SGUT, SDT>(*ap, smem, lane);
 }
 
 template <int GUT, int DT, int SGUT, int SDT>
