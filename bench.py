@@ -15,7 +15,9 @@ own roofline and CPU baseline:
   c3  512 experts, top-3, Q4_K gate/up, Q6_K down, Q8_0 shared expert, decode
   c4  8 consecutive 512-expert top-3 Q2_K/Q3_K layers chained through the
       fused RMSNorm and residual add, forced Zipf(0.456) routing with 37.5 %
-      overlap, 512 decode tokens (a step = one token through all 8 layers)
+      overlap, 512 decode tokens (a step = one token through all 8 layers, in
+      one launch; ``per_layer_launches`` times the same chain one launch per
+      layer)
   c5  prefill of 512 bf16 tokens through the 512-expert top-10 Q8_0 layer,
       Zipf routing (a step = the whole batch)
   c5r the same batch routed by the layer's fp32 router (router logits and
@@ -179,6 +181,10 @@ class Workload:
         if self.chained:
             self.hs = torch.empty(cfg.n_layers + 1, cfg.tokens, cfg.H, device="cuda")
             self.hs[0] = self.X
+            self.stack_out = torch.empty(cfg.tokens, cfg.n_layers, cfg.H, device="cuda")
+        # a chained decode runs its layers in one launch per token (wm_moe_decode_stack)
+        # unless the per-layer path is asked for
+        self.stack = self.chained and not self.prefill and not multi_kernel
         self.outs = torch.empty(cfg.tokens, cfg.H, dtype=torch.float32, device="cuda")
         self._rids = {}
 
@@ -192,6 +198,11 @@ class Workload:
                     sl.layer.prefill_forced(self.X, self.routes[li][2], self.routes[li][3], out=self.outs)
             return
         t = i % cfg.tokens
+        if self.stack:
+            from winmoe_amd.moe import decode_stack
+            routes = None if self.routes is None else [(r[2][t], r[3][t]) for r in self.routes]
+            decode_stack([sl.layer for sl in self.layers], self.X[t], out=self.stack_out[t], routes=routes, step=i)
+            return
         for li, sl in enumerate(self.layers):
             if self.chained:
                 x, o = self.hs[li, t], self.hs[li + 1, t]
@@ -303,6 +314,12 @@ def entry(wl, L, steps, warmup, multi_kernel=False):
         gu = phases["gate_up_swiglu"]
         rl = roofline(prefill_gateup_kernel(cfg), "k_pf_gemm", cfg.name, prefill_gateup_bytes(cfg, wl.route_ids(0)),
                       gu["avg_us"])
+    elif wl.stack:
+        # one chained launch per token moves all the layers' bytes
+        launch_us = 1000.0 * ev_ms / steps
+        rl = roofline("k_decode_stack (the fused decode step of every layer in one launch: one persistent "
+                      "workgroup per CU, each layer's output handed to the next in tagged words)",
+                      "k_decode_stack", cfg.name, sbytes, launch_us)
     elif not wl.prefill and not multi_kernel:
         # one fused launch per layer per token moves the step's bytes; its
         # average duration is the timed region's event time over the launches
@@ -608,6 +625,12 @@ def main():
         torch.cuda.synchronize()
         log(f"built in {time.perf_counter() - t_build:.1f} s")
         e = entry(wl, L, steps, warmup, multi_kernel=args.multi_kernel and headline)
+        if wl.stack:
+            # the same chain one launch per layer (the drop-in per-layer calls)
+            wl.stack = False
+            e2 = entry(wl, L, steps, warmup)
+            wl.stack = True
+            e["per_layer_launches"] = {k: e2[k] for k in ("ms_per_step", "tokens_per_s", "timing", "roofline")}
         if not args.no_cpu_baseline:
             log(f"timing the reference CPU path on this host ({name})")
             e["cpu_baseline"] = cpu_baseline(wl, CPU_SAMPLE[name])
@@ -620,7 +643,8 @@ def main():
                        "layers": cfg.n_layers, "routing": cfg.routing,
                        "batch": cfg.tokens if wl.prefill else 1, "distinct_tokens": cfg.tokens,
                        "path": "prefill" if wl.prefill else ("multi-kernel" if args.multi_kernel and headline
-                                                             else "fused")}
+                                                             else "fused, the layers chained in one launch"
+                                                             if wl.stack else "fused")}
         e["dtype"] = ("fp16 MFMA (quantised weights exact in fp16, x fp16 per-token scaled, SwiGLU output fp16 hi+lo) "
                       "-> fp32" if wl.prefill else
                       "int8 dot (quantised weights x int8 activation digits) -> int32, fp32 scales/accumulation")
@@ -656,6 +680,8 @@ def main():
         "phases_us": head["phases_us"], "status": head["status"],
         "configs": configs,
     }
+    if "per_layer_launches" in head:
+        result["per_layer_launches"] = head["per_layer_launches"]
     print(json.dumps(result), flush=True)
 
 

@@ -204,6 +204,24 @@ int wm_moe_decode(const wm_layer_desc* d, const float* x, float* out, void* ws, 
 int wm_moe_decode_forced(const wm_layer_desc* d, const float* x, const int32_t* ids, const float* w,
                          float* out, void* ws, int64_t ws_bytes, int max_tokens, int step, void* stream);
 
+/* n_layers decode steps of one token chained as the reference chains its
+ * layers (winmoe_inference.c:1659-1668: layer l's input is layer l-1's
+ * output; with the RMSNorm and residual set on each descriptor that is
+ * h_{l+1} = h_l + moe_l(rmsnorm(h_l))).  The reference has no such call: it
+ * enters each layer on its own, as wm_moe_decode / wm_moe_decode_forced do
+ * here, and the results are the same bit for bit.  Here up to 8 layers run in
+ * one launch, each workgroup going on to the next layer as soon as it is done
+ * with the previous one.  d, ws, ws_bytes: one entry per layer (each layer
+ * its own workspace); every layer has the same hidden size; x fp32[H]; out
+ * fp32[n_layers][H] receives every layer's output; ids, w: NULL (every layer
+ * routed by its router) or one device pointer pair per layer (a NULL entry:
+ * that layer uses its router).  Layers that the chained kernel does not take
+ * (formats without an instance, LDS) run one launch each, with the same
+ * results. */
+int wm_moe_decode_stack(int n_layers, const wm_layer_desc* const* d, void* const* ws, const int64_t* ws_bytes,
+                        const float* x, float* out, const int32_t* const* ids, const float* const* w,
+                        int max_tokens, int step, void* stream);
+
 /* Batched prefill of T tokens through the layer: x bf16 [T][H] -> out fp32
  * [T][H] (moe_out of every token).  The reference has no batched path: its
  * prompt tokens go one at a time through the decode loop

@@ -70,6 +70,7 @@ SIGNATURES = {
     "wm_moe_decode": (C.c_int, [C.POINTER(LayerDesc), _vp, _vp, _vp, _i64, C.c_int, C.c_int, _vp]),
     "wm_moe_decode_forced": (C.c_int, [C.POINTER(LayerDesc), _vp, _vp, _vp, _vp, _vp, _i64, C.c_int, C.c_int,
                                        _vp]),
+    "wm_moe_decode_stack": (C.c_int, [C.c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, _vp]),
     "wm_noalloc_init": (C.c_int, []),
     "wm_noalloc_scratch_bytes": (_i64, []),
     "wm_moe_decode_noalloc": (C.c_int, [C.POINTER(LayerDesc), _vp, _vp, _vp, _vp, _vp]),

@@ -221,7 +221,7 @@ extern "C" int wm_router_topk(const float* x, const float* W, int H, int E, int 
 
 struct WsLayout {
     int64_t status, ctr, logits, tr_ids, tr_w, hits, shgate, xin, gbuf, ubuf, act, ypart, tlog, hello, pctr, tact,
-        timeline, total;
+        tx, timeline, total;
     int K1, Imax, Is;
 };
 
@@ -278,6 +278,8 @@ static WsLayout layout(const wm_layer_desc* d, int max_tokens) {
     L.hello = o; o += up256((int64_t)P_MAX_WG * 4);
     L.pctr = o; o += (int64_t)CTR_STRIDE * 4;
     L.tact = o; o += up256((int64_t)L.K1 * P_AREP * ((L.Imax + 1) / 2) * 8);
+    // the layer's output as tagged words for the next layer of a chained launch
+    L.tx = o; o += up256((int64_t)P_XREP * H * 8);
     L.timeline = o;
     if (d->flags & WM_FLAG_TIMELINE) o += up256((int64_t)TIMELINE_CAP * 8 * 8);
     L.total = o;
@@ -505,8 +507,17 @@ template <typename F> static int persistent_ordered(hipStream_t s, F&& launch) {
 
 // One launch of the persistent step kernel (wm_persist.hip); returns 1 when
 // the layer does not fit it (the caller then uses the work-item-list kernel).
-static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, const float* x, float* out,
-                       const int32_t* forced_ids, const float* forced_w, int32_t* ids, float* w, hipStream_t s) {
+// prep_persist fills the kernel's arguments, LDS bytes and instance types
+// (stage: a layer of a chained launch that takes its input from the previous
+// layer, which needs LDS for the staged tagged input).
+struct PersistPlan {
+    PersistArgs a;
+    int lds;
+    int gut, dt, sgut, sdt;
+};
+static int prep_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, const float* x, float* out,
+                        const int32_t* forced_ids, const float* forced_w, int32_t* ids, float* w, bool stage,
+                        hipStream_t s, PersistPlan& plan) {
     const bool sh = has_shared(d);
     if (d->gate_type != d->up_type || (sh && d->sh_gate_type != d->sh_up_type)) return 1;
     const int gut = d->gate_type, dt = d->down_type;
@@ -585,6 +596,16 @@ static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
         o += router_bytes;
         a.n_rwaves = 0;
     }
+    // a chained layer's input: the previous layer's tagged words (8 bytes a
+    // value, whole kilobytes) after the router region, which must have its
+    // own space
+    a.o_stage = 0;
+    if (stage) {
+        const int st = (H * 8 + 1023) / 1024 * 1024;
+        if (a.n_rwaves || a.o_router + router_bytes + st > max_lds_per_wg()) return 1;
+        a.o_stage = a.o_router + router_bytes;
+        o += st;
+    }
     if (a.nstream < a.n_rwaves + 1 || a.nstream < 4) return 1;
     // (and more than half of a CU's LDS, so that each CU holds one workgroup)
     const int lds = std::max((o + a.nstream * PRING * a.ring_buf + 255) / 256 * 256,
@@ -608,9 +629,19 @@ static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, c
     a.tact = (uint64_t*)(ws + L.tact);
     if (d->flags & WM_FLAG_TIMELINE) a.timeline = (uint64_t*)(ws + L.timeline);
     a.probe = (d->flags & WM_FLAG_SPIN_PROBE) ? 1u : 0u;
+    plan.a = a;
+    plan.lds = lds;
+    plan.gut = gut; plan.dt = dt; plan.sgut = sgut; plan.sdt = sdt;
+    return WM_OK;
+}
+
+static int run_persist(const wm_layer_desc* d, const WsLayout& L, uint8_t* ws, const float* x, float* out,
+                       const int32_t* forced_ids, const float* forced_w, int32_t* ids, float* w, hipStream_t s) {
+    PersistPlan plan;
+    if (int rc = prep_persist(d, L, ws, x, out, forced_ids, forced_w, ids, w, false, s, plan)) return rc;
     PhaseTimer pt(PH_STEP, s);
     return persistent_ordered(s, [&]() -> int {
-        WM_FAIL_HIP(launch_persist(a, (size_t)lds, gut, dt, sgut, sdt, s));
+        WM_FAIL_HIP(launch_persist(plan.a, (size_t)plan.lds, plan.gut, plan.dt, plan.sgut, plan.sdt, s));
         return WM_OK;
     });
 }
@@ -764,6 +795,82 @@ extern "C" int wm_moe_decode_forced(const wm_layer_desc* d, const float* x, cons
     WM_FAIL_HIP(hipMemcpyAsync(wts, w_in, (size_t)d->top_k * 4, hipMemcpyDeviceToDevice, s));
     WM_FAIL_HIP(launch_count_hits(ids, d->top_k, d->n_experts, (uint32_t*)(w8 + L.hits), (int32_t*)(w8 + L.status), s));
     return run_experts(d, L, w8, x, ids, wts, out, s);
+}
+
+extern "C" int wm_moe_decode_stack(int n_layers, const wm_layer_desc* const* d, void* const* ws, const int64_t* ws_bytes,
+                                   const float* x, float* out, const int32_t* const* ids_in, const float* const* w_in,
+                                   int max_tokens, int step, void* stream) {
+    WM_CHECK_ARG(n_layers >= 1 && d && ws && ws_bytes && x && out && max_tokens > 0 && step >= 0);
+    WM_CHECK_ARG(!ids_in == !w_in);
+    for (int l = 0; l < n_layers; l++) {
+        const bool forced = ids_in && ids_in[l];
+        if (int rc = validate_desc(d[l], !forced)) return rc;
+        WM_CHECK_ARG(!forced || w_in[l]);
+        WM_CHECK_ARG(ws[l] && al(ws[l], 256) && ws_bytes[l] >= layout(d[l], max_tokens).total);
+        WM_CHECK_ARG(d[l]->hidden == d[0]->hidden);
+        WM_CHECK_ARG(!d[l]->add_residual || d[l]->norm_w);
+    }
+    if (wm_init()) return WM_ERR;
+    hipStream_t s = S(stream);
+    const int H = d[0]->hidden;
+    const int slot = step % max_tokens;
+    // one layer the usual way (input xl, output ol)
+    auto one = [&](int l, const float* xl, float* ol) -> int {
+        const bool forced = ids_in && ids_in[l];
+        return forced ? wm_moe_decode_forced(d[l], xl, ids_in[l], w_in[l], ol, ws[l], ws_bytes[l], max_tokens, step, stream)
+                      : wm_moe_decode(d[l], xl, ol, ws[l], ws_bytes[l], max_tokens, step, stream);
+    };
+    const float* xin = x;
+    for (int l0 = 0; l0 < n_layers;) {
+        const int cnt = std::min(P_STACK, n_layers - l0);
+        StackArgs sa = {};
+        int lds = 0, gut = 0, dt = 0, sgut = 0, sdt = 0;
+        bool ok = cnt > 1;
+        for (int k = 0; ok && k < cnt; k++) {
+            const int l = l0 + k;
+            const wm_layer_desc* dl = d[l];
+            if (dl->flags & (WM_FLAG_MULTI_KERNEL | WM_FLAG_ITEM_KERNEL)) { ok = false; break; }
+            const WsLayout L = layout(dl, max_tokens);
+            uint8_t* w8 = (uint8_t*)ws[l];
+            int32_t* tid = (int32_t*)(w8 + L.tr_ids) + (int64_t)slot * dl->top_k;
+            float* tw = (float*)(w8 + L.tr_w) + (int64_t)slot * dl->top_k;
+            const bool forced = ids_in && ids_in[l];
+            PersistPlan plan;
+            const int rc = prep_persist(dl, L, w8, k == 0 ? xin : out + (int64_t)(l - 1) * H, out + (int64_t)l * H,
+                                        forced ? ids_in[l] : nullptr, forced ? w_in[l] : nullptr, tid, tw, k > 0, s, plan);
+            if (rc < 0) return rc;
+            if (rc > 0) { ok = false; break; }
+            if (k == 0) {
+                gut = plan.gut; dt = plan.dt; sgut = plan.sgut; sdt = plan.sdt;
+                if (!stack_supported(gut, dt, sgut, sdt)) { ok = false; break; }
+            } else if (plan.gut != gut || plan.dt != dt || plan.sgut != sgut || plan.sdt != sdt ||
+                       plan.a.nwg != sa.L[0].nwg) {
+                ok = false;
+                break;
+            }
+            plan.a.tx_out = k + 1 < cnt ? (uint64_t*)(w8 + L.tx) : nullptr;
+            plan.a.tx_in = k > 0 ? sa.L[k - 1].tx_out : nullptr;
+            sa.L[k] = plan.a;
+            lds = std::max(lds, plan.lds);
+        }
+        if (ok) {
+            sa.n = cnt;
+            PhaseTimer pt(PH_STEP, s);
+            const int rc = persistent_ordered(s, [&]() -> int {
+                WM_FAIL_HIP(launch_stack(sa, (size_t)lds, gut, dt, sgut, sdt, s));
+                return WM_OK;
+            });
+            if (rc) return rc;
+        } else {
+            for (int k = 0; k < cnt; k++) {
+                const int l = l0 + k;
+                if (int rc = one(l, k == 0 ? xin : out + (int64_t)(l - 1) * H, out + (int64_t)l * H)) return rc;
+            }
+        }
+        xin = out + (int64_t)(l0 + cnt - 1) * H;
+        l0 += cnt;
+    }
+    return WM_OK;
 }
 
 extern "C" int64_t wm_expert_workspace_size(int H, int I) {

@@ -87,6 +87,7 @@ constexpr int P_TL = 32;                 // timeline words per workgroup
 constexpr int P_MAX_WG = 1024;           // workgroups (CUs) the workspace has start-tag words for
 constexpr int P_REP = 8;                 // replicas of the tagged logits (each read by 1/8 of the workgroups)
 constexpr int P_AREP = 4;                // replicas of the tagged SwiGLU outputs
+constexpr int P_XREP = 8;                // replicas of a chained layer's tagged output (read whole by every workgroup)
 constexpr uint32_t PSPIN_G = 1u << 17;   // device-memory polls (~1 us each) before a wait gives up
 
 // Ring buffer bytes of one tile of type T: NI DMA units of 1 KB, except Q8_0
@@ -117,6 +118,7 @@ struct PersistCtl {
     float sgate;
     uint32_t x_in;                 // x is in LDS (the second staging wave loads it)
     uint32_t desc_built;           // the tile descriptor table is built
+    uint32_t xpart[PW + 1];        // a chained layer's input: wave w's part of it is in x
     uint64_t rbase[PMAXK][3];      // routed slot k's gate / up / down bytes | 1 (1 alone: no weights), 0 until picked
     uint64_t t[P_TL];              // timeline (device clock)
 };
@@ -162,9 +164,26 @@ struct PersistArgs {
     uint64_t* tact;                    // [K+1][P_AREP][I/2] (tag16 << 48) | act24(v[2i+1]) << 24 | act24(v[2i])
     uint64_t* timeline;                // NULL or [nwg][P_TL]
     uint32_t probe;                    // nonzero: every wait of the step gives up at its first unsuccessful poll
+    // layers chained in one launch (k_decode_stack): this layer's output
+    // also as tagged words (tag << 32 | value bits) for the next layer, and
+    // its input as the previous layer's tagged words (null: x), staged in
+    // LDS at o_stage (8 bytes a value)
+    uint64_t* tx_out;
+    const uint64_t* tx_in;
+    int32_t o_stage;
 };
+
+// Layers of one launch of the chained step (kernel arguments: at most 4 KB).
+constexpr int P_STACK = 8;
+struct StackArgs {
+    PersistArgs L[P_STACK];
+    int32_t n;
+};
+static_assert(sizeof(StackArgs) <= 4096, "kernel arguments");
 
 bool persist_supported(int gut, int dt, int sgut, int sdt);
 int launch_persist(const PersistArgs& a, size_t lds, int gut, int dt, int sgut, int sdt, hipStream_t s);
+int launch_stack(const StackArgs& a, size_t lds, int gut, int dt, int sgut, int sdt, hipStream_t s);
+bool stack_supported(int gut, int dt, int sgut, int sdt);     // the type sets with a chained-launch instance
 
 }  // namespace wm

@@ -83,6 +83,7 @@ WM_DEV uint64_t tagged(uint32_t tag, float v) { return ((uint64_t)tag << 32) | (
 // weight stream at every flag check.
 WM_DEV uint32_t lds_ld(const lds32_t* p) { return *(const volatile lds32_t*)p; }
 WM_DEV uint64_t lds_ld64(const lds64_t* p) { return *(const volatile lds64_t*)p; }
+WM_DEV lctl_t* ctl_of(uint8_t* smem) { return (lctl_t*)smem; }
 
 // Every LDS write of this wave is complete, then lane 0 stores v to *p (a
 // word with one writer; volatile, not atomic, for the reason above), then
@@ -460,11 +461,72 @@ WM_DEV TileDesc desc_unpack(const u32x4& e) {
 WM_DEV int lg_tile_lanes(int n) { return 31 - __builtin_clz((unsigned)(n / SEG)); }
 WM_DEV bool routed_kind(int k) { return k == K_RG || k == K_RU || k == K_RD; }
 
+// A chained layer's input, part `part` of nparts: the previous layer's
+// tagged words (tag << 32 | value bits, 8 bytes a value; P_XREP replicas,
+// replica w % P_XREP read by workgroup w) come into LDS at o_stage with
+// LDS-DMA, kilobytes part, part + nparts, ... of it, the first read through
+// the L2 and the re-reads of a kilobyte that still holds an older tag past
+// it, until every word carries the previous layer's tag (bounded); one pass
+// over each kilobyte that came in checks its tags and writes its values into
+// x.  The staged words stay for the residual add.  Every wave of the
+// workgroup loads a part: lines just written by other workgroups come slowly
+// (~6 us for 32 KB read by one wave), and fourteen waves read them side by
+// side.
+WM_DEV void x_tagged_part(const PersistArgs& a, uint8_t* smem, lds8_t* xl, uint32_t tag, int part, int nparts, int lane) {
+    lctl_t* ctl = (lctl_t*)smem;
+    lds8_t* st = (lds8_t*)smem + a.o_stage;
+    typedef __attribute__((address_space(3))) const u32x4 lq4c_t;
+    const int H = a.H, nch = H / 2, units = (nch + 63) >> 6;     // 16-byte granules (two values each), KB units
+    const uint8_t* src = (const uint8_t*)(a.tx_in + (int64_t)((int)blockIdx.x % P_XREP) * H);
+    uint32_t pend = 0u;                                            // this part's units still to (re)load
+    for (int k = part; k < units; k += nparts) pend |= 1u << k;
+    uint32_t it = 0;
+    bool first = true;
+    while (pend) {
+        for (int k = part; k < units; k += nparts) {
+            if (!((pend >> k) & 1u)) continue;
+            const int i = min(lane + 64 * k, nch - 1);
+            if (first)
+                __builtin_amdgcn_global_load_lds((const void*)(src + 16 * i), (__attribute__((address_space(3))) void*)(st + 1024 * k), 16, 0, 0);
+            else
+                __builtin_amdgcn_global_load_lds((const void*)(src + 16 * i), (__attribute__((address_space(3))) void*)(st + 1024 * k), 16, 0, CPOL_SC1);
+        }
+        WM_WAIT_VMCNT(0);
+        first = false;
+        uint32_t bad = 0u;
+        for (int k = part; k < units; k += nparts) {
+            if (!((pend >> k) & 1u)) continue;
+            const int i = lane + 64 * k;
+            const u32x4 q = *(lq4c_t*)(st + 16 * min(i, nch - 1));        // words 2i, 2i + 1: lo, hi, lo, hi
+            const bool ok = i >= nch || (q.y == tag && q.w == tag);
+            if (i < nch) {
+                // (one 64-bit store of the two value words: stored as two
+                // 32-bit values, or as a float2, this ROCm's compiler merged
+                // them into one store holding the first value twice)
+                *(lds64_t*)(xl + 8 * i) = (uint64_t)q.x | ((uint64_t)q.z << 32);
+            }
+            if (__builtin_amdgcn_ballot_w64(!ok) != 0ull) bad |= 1u << k;
+        }
+        pend = bad;
+        if (!pend) break;
+        if (++it > PSPIN_G || aborted(ctl)) {
+            give_up(ctl, a.status, lane);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(4);
+    }
+    lds_set(&ctl->xpart[part], 1u, lane);
+}
+
 template <int GUT, int DT, int SGUT, int SDT>
-WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, int lane) {
+WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, uint32_t prev_tag, int lane) {
     lctl_t* ctl = (lctl_t*)smem;
     lds8_t* lds = (lds8_t*)smem;
     const int wave = __builtin_amdgcn_readfirstlane(wave_v);
+    // a chained layer: this wave's part of the input first (it is on every
+    // path; sending the first tile before it made it later, 133.6 -> 145.5 us
+    // for the 8 C4 layers)
+    if (a.tx_in) x_tagged_part(a, smem, lds + a.o_router, prev_tag, wave, PW + 1, lane);
     const int K = a.K, sh = a.has_shared, H = a.H, I = a.I;
     const int nseg_dn = I / SEG;
     // geometry (lanes per row: powers of two; a tile is 64 segments, so every
@@ -937,10 +999,16 @@ WM_DEV void desc_table(const PersistArgs& a, uint8_t* smem, int lane) {
 // x into the region at xl and the RMSNorm in place, for H <= 256 * NST; the
 // norm weights land at o_norm (over the operand records, which are built
 // only after x is in) with x.
-template <int NST> WM_DEV void x_norm_in(const PersistArgs& a, uint8_t* smem, lds8_t* xl, int lane) {
+template <int NST> WM_DEV void x_norm_in(const PersistArgs& a, uint8_t* smem, lds8_t* xl, uint32_t prev_tag, int lane) {
     lds8_t* wl = (lds8_t*)smem + a.o_norm;
-    vec_dma(a.x, a.H, xl, lane);
-    vec_dma(a.norm_w, a.H, wl, lane);
+    if (a.tx_in) {
+        vec_dma(a.norm_w, a.H, wl, lane);
+        x_tagged_part(a, smem, xl, prev_tag, PW, PW + 1, lane);
+        wait_all(ctl_of(smem), ctl_of(smem)->xpart, PW + 1, a.status, lane);
+    } else {
+        vec_dma(a.x, a.H, xl, lane);
+        vec_dma(a.norm_w, a.H, wl, lane);
+    }
     WM_WAIT_VMCNT(0);
     rmsnorm_lds<NST>((lf32_t*)xl, (const lf32_t*)wl, a.H, a.norm_eps, lane);
 }
@@ -950,18 +1018,21 @@ template <int NST> WM_DEV void x_norm_in(const PersistArgs& a, uint8_t* smem, ld
 // the layer has one (its weights come in with x), the shared expert's gate,
 // the tile descriptor table.
 template <int GUT, int DT, int SGUT, int SDT>
-WM_DEV void helper_xload(const PersistArgs& a, uint8_t* smem, int lane) {
+WM_DEV void helper_xload(const PersistArgs& a, uint8_t* smem, uint32_t prev_tag, int lane) {
     lctl_t* ctl = (lctl_t*)smem;
     __builtin_amdgcn_s_setprio(3);
     lds8_t* xl = (lds8_t*)smem + a.o_router;
     if (a.norm_w) {
         switch ((a.H + 255) / 256) {
-        case 1: x_norm_in<1>(a, smem, xl, lane); break;
-        case 2: x_norm_in<2>(a, smem, xl, lane); break;
-        case 4: x_norm_in<4>(a, smem, xl, lane); break;
-        case 8: x_norm_in<8>(a, smem, xl, lane); break;
-        default: x_norm_in<16>(a, smem, xl, lane); break;
+        case 1: x_norm_in<1>(a, smem, xl, prev_tag, lane); break;
+        case 2: x_norm_in<2>(a, smem, xl, prev_tag, lane); break;
+        case 4: x_norm_in<4>(a, smem, xl, prev_tag, lane); break;
+        case 8: x_norm_in<8>(a, smem, xl, prev_tag, lane); break;
+        default: x_norm_in<16>(a, smem, xl, prev_tag, lane); break;
         }
+    } else if (a.tx_in) {
+        x_tagged_part(a, smem, xl, prev_tag, PW, PW + 1, lane);
+        wait_all(ctl, ctl->xpart, PW + 1, a.status, lane);
     } else {
         router_dma(a.x, nullptr, a.H, 0, -1, -1, xl, a.x_region, lane);
     }
@@ -1133,6 +1204,9 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
         const int h0 = P.d0 * rpt, nrows = min(a.H, (P.d0 + P.ndn) * rpt) - h0;
         // the routing weights into registers while the down tiles finish
         lds_wait(ctl, &ctl->routed, 1u, a.status, lane);     // the weights come after the last pick
+        typedef __attribute__((address_space(3))) const uint64_t l64c_t;
+        const l64c_t* stw = (const l64c_t*)(lds + a.o_stage);     // (a chained launch's staged input)
+        const uint32_t otag = ctl->tag;
         bool vk[PMAXK];
         float wk[PMAXK];
 #pragma unroll
@@ -1148,7 +1222,9 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
 #pragma unroll
             for (int k = 0; k < PMAXK; k++) y[k] = vk[k] ? yarr[k * a.y_cap + r] : 0.0f;
             const float ys = sh ? yarr[K * a.y_cap + r] : 0.0f;
-            const float xr = a.add_res ? a.x[h0 + r] : 0.0f;
+            // (in a chained launch the input is the staged tagged words)
+            const float xr = !a.add_res ? 0.0f
+                           : a.tx_in ? __builtin_bit_cast(float, (uint32_t)stw[h0 + r]) : a.x[h0 + r];
             float acc = 0.0f;
 #pragma unroll
             for (int k = 0; k < PMAXK; k++)
@@ -1156,6 +1232,11 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
             if (sh) acc = acc + ys;
             if (a.add_res) acc = xr + acc;          // residual + moe_out
             a.out[h0 + r] = acc;
+            if (a.tx_out) {
+                const uint64_t tw = tagged(otag, acc);
+#pragma unroll
+                for (int q = 0; q < P_XREP; q++) gst_agent64(a.tx_out + (int64_t)q * a.H + h0 + r, tw);
+            }
         }
     }
 
@@ -1182,13 +1263,78 @@ __global__ __launch_bounds__(PTHREADS) void k_decode_persist(PersistArgs a) {
     asm volatile("" : "+s"(ka));
     const PersistArgs* ap = (const PersistArgs*)ka;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (wave < PW) stream_wave<GUT, DT, SGUT, SDT>(*ap, smem, wave, lane);
+    if (wave < PW) stream_wave<GUT, DT, SGUT, SDT>(*ap, smem, wave, 0u, lane);
     // the router rows and the routing are the critical path: the helper
     // waves win the issue arbitration against the streaming waves until the
     // routing is known (their later polling must not)
     else if (wave == PW) { __builtin_amdgcn_s_setprio(3); helper_router<GUT, DT, SGUT, SDT>(*ap, smem, lane); }
     else if (wave == PW + 1) { __builtin_amdgcn_s_setprio(3); helper_publish<GUT, DT, SGUT, SDT>(*ap, smem, lane); }
-    else if (wave == PW + 2) helper_xload<GUT, DT, SGUT, SDT>(*ap, smem, lane);
+    else if (wave == PW + 2) helper_xload<GUT, DT, SGUT, SDT>(*ap, smem, 0u, lane);
+}
+
+// Layers chained in one launch: layer l's input is layer l-1's output, handed
+// over in tagged words (PersistArgs::tx_out / tx_in) so that a workgroup
+// starts a layer as soon as it is done with the previous one (its first
+// weight tiles load while the previous layer's last outputs arrive) instead
+// of after a kernel boundary.  Each layer runs the step above with its own
+// arguments and workspace; the control block is cleared between layers.
+template <int GUT, int DT, int SGUT, int SDT>
+__global__ __launch_bounds__(PTHREADS) void k_decode_stack(StackArgs sa) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    typedef const __attribute__((address_space(4))) StackArgs kargs_t;
+    kargs_t* ka = (kargs_t*)__builtin_amdgcn_kernarg_segment_ptr();      // (the only kernel argument)
+    asm volatile("" : "+s"(ka));
+    const StackArgs* sp = (const StackArgs*)ka;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nl = sp->n;
+    lctl_t* ctl = (lctl_t*)smem;
+    // Every wave meets the same three barriers per layer: the control block
+    // is clear (the x loader clears it), the layer is done, its tag is read.
+    auto layer_end = [&](uint32_t& tag) {
+        __builtin_amdgcn_s_setprio(0);
+        __syncthreads();
+        tag = *(const volatile lds32_t*)&ctl->tag;     // the tag this layer's outputs carry
+        __syncthreads();
+    };
+    uint32_t prev_tag = 0u;
+    if (wave < PW) {
+        for (int l = 0; l < nl; l++) {
+            __syncthreads();
+            int ln = lane;
+            asm volatile("" : "+v"(ln));      // (nothing derived from the lane is kept across layers)
+            stream_wave<GUT, DT, SGUT, SDT>(sp->L[l], smem, wave, prev_tag, ln);
+            layer_end(prev_tag);
+        }
+    } else if (wave == PW) {
+        for (int l = 0; l < nl; l++) {
+            __syncthreads();
+            __builtin_amdgcn_s_setprio(3);
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+            helper_router<GUT, DT, SGUT, SDT>(sp->L[l], smem, ln);
+            layer_end(prev_tag);
+        }
+    } else if (wave == PW + 1) {
+        for (int l = 0; l < nl; l++) {
+            __syncthreads();
+            __builtin_amdgcn_s_setprio(3);
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+            helper_publish<GUT, DT, SGUT, SDT>(sp->L[l], smem, ln);
+            layer_end(prev_tag);
+        }
+    } else {
+        for (int l = 0; l < nl; l++) {
+            for (int i = lane; i < (int)(sizeof(PersistCtl) / 4); i += 64) ((lds32_t*)(lds8_t*)smem)[i] = 0u;
+            if (lane == 0 && sp->L[l].probe) ctl->abort = 1u;
+            WM_WAIT_LGKM0();
+            __syncthreads();
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+            helper_xload<GUT, DT, SGUT, SDT>(sp->L[l], smem, prev_tag, ln);
+            layer_end(prev_tag);
+        }
+    }
 }
 
 template <int GUT, int DT, int SGUT, int SDT>
@@ -1201,6 +1347,19 @@ static int launch_p(const PersistArgs& a, size_t lds, hipStream_t s) {
         configured = lds;
     }
     hipLaunchKernelGGL((k_decode_persist<GUT, DT, SGUT, SDT>), dim3(a.nwg), dim3(PTHREADS), lds, s, a);
+    return (int)hipGetLastError();
+}
+
+template <int GUT, int DT, int SGUT, int SDT>
+static int launch_st(const StackArgs& a, size_t lds, hipStream_t s) {
+    static size_t configured = 0;
+    if (configured < lds) {
+        hipError_t e = hipFuncSetAttribute((const void*)k_decode_stack<GUT, DT, SGUT, SDT>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return (int)e;
+        configured = lds;
+    }
+    hipLaunchKernelGGL((k_decode_stack<GUT, DT, SGUT, SDT>), dim3(a.L[0].nwg), dim3(PTHREADS), lds, s, a);
     return (int)hipGetLastError();
 }
 
@@ -1221,6 +1380,21 @@ int launch_persist(const PersistArgs& a, size_t lds, int gut, int dt, int sgut, 
     WM_P_CASE(Q2_K, Q3_K, Q8_0, Q8_0)
     WM_P_CASE(Q2_K, Q3_K, Q2_K, Q3_K)
     return -1;
+}
+
+#define WM_S_CASE(g, d, sg, sd) \
+    if (gut == g && dt == d && sgut == sg && sdt == sd) return launch_st<g, d, sg, sd>(a, lds, s);
+
+int launch_stack(const StackArgs& a, size_t lds, int gut, int dt, int sgut, int sdt, hipStream_t s) {
+    WM_S_CASE(Q8_0, Q8_0, Q8_0, Q8_0)
+    WM_S_CASE(Q2_K, Q3_K, Q2_K, Q3_K)
+    WM_S_CASE(Q4_K, Q6_K, Q8_0, Q8_0)
+    return -1;
+}
+
+bool stack_supported(int gut, int dt, int sgut, int sdt) {
+    return (gut == Q8_0 && dt == Q8_0 && sgut == Q8_0 && sdt == Q8_0) || (gut == Q2_K && dt == Q3_K && sgut == Q2_K && sdt == Q3_K) ||
+           (gut == Q4_K && dt == Q6_K && sgut == Q8_0 && sdt == Q8_0);
 }
 
 bool persist_supported(int gut, int dt, int sgut, int sdt) { return decode_step_supported(gut, dt, sgut, sdt); }

@@ -383,6 +383,58 @@ class MoELayer:
         return v.value
 
 
+def decode_stack(layers, x: torch.Tensor, out: Optional[torch.Tensor] = None, routes=None,
+                 step: Optional[int] = None, stream=None) -> torch.Tensor:
+    """One token through a chain of layers (wm_moe_decode_stack): layer l's
+    input is layer l-1's output (x for the first), so with each layer's
+    RMSNorm and residual add out[l] = h_{l+1} = h_l + moe_l(rmsnorm(h_l)).
+    Up to 8 layers run in one launch.  routes: None (every layer routed by
+    its router) or one (ids int32[K], w fp32[K]) device pair per layer (None
+    entries: that layer's router).  Returns out fp32 [n_layers][H], each
+    layer's output, bit for bit what the layers' own decode calls give."""
+    n = len(layers)
+    if n == 0:
+        raise ValueError("no layers")
+    L0 = layers[0]
+    for m in layers:
+        if m.H != L0.H or m.max_tokens != L0.max_tokens:
+            raise ValueError("the layers of a chain share the hidden size and max_tokens")
+    L0._need_vec(x, None)
+    if out is None:
+        out = torch.empty(n, L0.H, dtype=torch.float32, device=x.device)
+    _need(out, torch.float32, "out")
+    if out.shape != (n, L0.H) or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous [{n}][{L0.H}] tensor")
+    st = L0.step if step is None else step
+    descs = (C.c_void_p * n)(*[C.cast(C.pointer(m.desc), C.c_void_p) for m in layers])
+    wss = (C.c_void_p * n)(*[m.ws.data_ptr() for m in layers])
+    wsb = (C.c_int64 * n)(*[m.ws.numel() for m in layers])
+    ids_arr = w_arr = None
+    if routes is not None:
+        if len(routes) != n:
+            raise ValueError("routes: one entry per layer")
+        pi, pw = [], []
+        for m, r in zip(layers, routes):
+            if r is None:
+                pi.append(None)
+                pw.append(None)
+                continue
+            ids, w = r
+            _need(ids, torch.int32, "ids")
+            _need(w, torch.float32, "w")
+            if ids.numel() != m.K or w.numel() != m.K:
+                raise ValueError(f"ids and w must hold K = {m.K} values")
+            pi.append(ids.data_ptr())
+            pw.append(w.data_ptr())
+        ids_arr = (C.c_void_p * n)(*pi)
+        w_arr = (C.c_void_p * n)(*pw)
+    check(load().wm_moe_decode_stack(n, descs, wss, wsb, _p(x), _p(out), ids_arr, w_arr, L0.max_tokens, st,
+                                     _stream(stream)), "wm_moe_decode_stack")
+    for m in layers:
+        m.step = st + 1
+    return out
+
+
 class ExpertPool:
     """Host -> HBM expert streaming (include/winmoe_hip.h, wm_pool_*): ``n_slots``
     expert slots in HBM filled on demand from host memory, for models whose
