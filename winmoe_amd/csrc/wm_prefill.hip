@@ -102,6 +102,105 @@ __global__ __launch_bounds__(256) void k_pf_router(const uint16_t* __restrict__ 
         }
 }
 
+// The same logits, for H a multiple of 128 and 16-byte aligned x rows and
+// router rows: tiles of 16 tokens x 32 experts, each thread the chain of
+// column residue l of 4 tokens x 8 experts (32 accumulators: 12 LDS reads per
+// 32 FMAs), the columns in chunks of 128 staged in LDS twice over: the loads
+// (16-byte vectors) of the next two chunks are in flight while the current
+// one is summed.  Every chain adds its columns in the same order as above, so the
+// logits are the same bit for bit.
+constexpr int PQ_T = 16, PQ_E = 32, PQ_CH = 128, PQ_LD = PQ_CH + 4;
+__global__ __launch_bounds__(256) void k_pf_router_v(const uint16_t* __restrict__ x, const float* __restrict__ W, int H,
+                                                     int T, int E, float* __restrict__ logits) {
+    __shared__ float xs[2][PQ_T * PQ_LD];
+    __shared__ float wsh[2][PQ_E * PQ_LD];
+    const int t0 = blockIdx.x * PQ_T, e0 = blockIdx.y * PQ_E;
+    const int tid = threadIdx.x, l = tid & 15, sb = tid >> 4, tq = sb >> 2, eq = sb & 3;
+    // staging: x row tid / 16, columns 8 (tid % 16) .. + 8 (one 16-byte load
+    // of bf16); W row tid / 8, columns 16 (tid % 8) .. + 16 (four)
+    const int xr = tid >> 4, xc = 8 * (tid & 15), wr = tid >> 3, wc = 16 * (tid & 7);
+    const bool xin = t0 + xr < T, win = e0 + wr < E;
+    const uint4* xsrc = (const uint4*)(x + (int64_t)(xin ? t0 + xr : 0) * H + xc);
+    const uint4* wsrc = (const uint4*)(W + (int64_t)(win ? e0 + wr : 0) * H + wc);
+    uint4 xv, wv[4], xv2, wv2[4];
+    auto gload = [&](int c0) {
+        const uint4 z = {0u, 0u, 0u, 0u};
+        xv = xin ? xsrc[c0 / 8] : z;
+#pragma unroll
+        for (int q = 0; q < 4; q++) wv[q] = win ? wsrc[c0 / 4 + q] : z;
+    };
+    auto gload2 = [&](int c0) {
+        const uint4 z = {0u, 0u, 0u, 0u};
+        xv2 = xin ? xsrc[c0 / 8] : z;
+#pragma unroll
+        for (int q = 0; q < 4; q++) wv2[q] = win ? wsrc[c0 / 4 + q] : z;
+    };
+    auto lstore = [&](int b) {
+        float* xd = &xs[b][xr * PQ_LD + xc];
+        const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            xd[2 * k] = bf16f((uint16_t)(xw[k] & 0xFFFFu));
+            xd[2 * k + 1] = bf16f((uint16_t)(xw[k] >> 16));
+        }
+        float* wd = &wsh[b][wr * PQ_LD + wc];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            wd[4 * q] = __builtin_bit_cast(float, wv[q].x);
+            wd[4 * q + 1] = __builtin_bit_cast(float, wv[q].y);
+            wd[4 * q + 2] = __builtin_bit_cast(float, wv[q].z);
+            wd[4 * q + 3] = __builtin_bit_cast(float, wv[q].w);
+        }
+    };
+    float acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[i][j] = 0.0f;
+    const int nch = H / PQ_CH;
+    gload(0);
+    lstore(0);
+    if (nch > 1) gload2(PQ_CH);
+    __syncthreads();
+    for (int c = 0; c < nch; c++) {
+        const int b = c & 1;
+        // chunk c + 1 is in flight in (xv2, wv2); chunk c + 2 goes out now
+        xv = xv2;
+#pragma unroll
+        for (int q = 0; q < 4; q++) wv[q] = wv2[q];
+        if (c + 2 < nch) gload2((c + 2) * PQ_CH);
+        const float* xb = &xs[b][(4 * tq) * PQ_LD + l];
+        const float* wb = &wsh[b][(8 * eq) * PQ_LD + l];
+#pragma unroll 2
+        for (int st = 0; st < PQ_CH / 16; st++) {
+            float xq[4], wq[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) xq[i] = xb[i * PQ_LD + 16 * st];
+#pragma unroll
+            for (int j = 0; j < 8; j++) wq[j] = wb[j * PQ_LD + 16 * st];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) acc[i][j] = fmaf(wq[j], xq[i], acc[i][j]);
+        }
+        // (the other buffer was last read before the previous barrier)
+        if (c + 1 < nch) lstore(b ^ 1);     // chunk c + 1
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            float v = acc[i][j];
+            v += dpp_f32<DPP_ROR8>(v);
+            v += dpp_f32<DPP_ROR4>(v);
+            v += dpp_f32<DPP_ROR2>(v);
+            v += dpp_f32<DPP_ROR1>(v);
+            const int t = t0 + 4 * tq + i, e = e0 + 8 * eq + j;
+            if (l == 0 && t < T && e < E) logits[(int64_t)t * E + e] = v;
+        }
+}
+
 // ------------------------------------------------------------------ top-K, forced routing, grouping
 
 __global__ __launch_bounds__(256) void k_pf_topk(const float* __restrict__ logits, int T, int E, int K,
@@ -400,8 +499,12 @@ int launch_prefill_route(const PrefillArgs& a, const int32_t* forced_ids, const 
         hipLaunchKernelGGL(k_pf_forced, dim3((P + 255) / 256), dim3(256), 0, s, forced_ids, forced_w, P, a.E, a.ids, a.w,
                            a.hits, a.status);
     } else {
-        hipLaunchKernelGGL(k_pf_router, dim3((a.T + PR_T - 1) / PR_T, (a.E + PR_E - 1) / PR_E), dim3(256), 0, s, a.x,
-                           a.router, a.H, a.T, a.E, a.logits);
+        if (a.H % PQ_CH == 0 && ((uintptr_t)a.x & 15) == 0 && ((uintptr_t)a.router & 15) == 0)
+            hipLaunchKernelGGL(k_pf_router_v, dim3((a.T + PQ_T - 1) / PQ_T, (a.E + PQ_E - 1) / PQ_E), dim3(256), 0, s,
+                               a.x, a.router, a.H, a.T, a.E, a.logits);
+        else
+            hipLaunchKernelGGL(k_pf_router, dim3((a.T + PR_T - 1) / PR_T, (a.E + PR_E - 1) / PR_E), dim3(256), 0, s, a.x,
+                               a.router, a.H, a.T, a.E, a.logits);
         hipLaunchKernelGGL(k_pf_topk, dim3((a.T + WAVES - 1) / WAVES), dim3(256), 0, s, a.logits, a.T, a.E, a.K, a.ids,
                            a.w, a.hits, a.status);
     }
