@@ -457,6 +457,9 @@ def timeline_report(name, steps):
     if wl.prefill:
         print("--timeline covers the decode workloads (c1-c4)", file=sys.stderr)
         sys.exit(2)
+    if wl.stack:
+        stack_timeline_report(wl, steps)
+        return
     sl, cfg = wl.layers[0], wl.cfg
     c = sl.cfg
     layer = MoELayer(c.H, c.I, sl.layer.E, c.K, sl.router, sl.gate, sl.up, sl.down, c.types, shared=sl.shared,
@@ -503,12 +506,71 @@ def timeline_report(name, steps):
     print(f"step time over the replay (HIP events): {us:.2f} us")
 
 
-def stream_report(name, n_slots, steps, warmup):
+def stack_timeline_report(wl, steps):
+    """The chained launch's timeline: every layer of the last of `steps`
+    tokens (graph replay), per layer the median workgroup's marks, in us from
+    the earliest workgroup start of the launch."""
+    import numpy as np
+    import torch
+    from winmoe_amd.moe import MoELayer, decode_stack
+    cfg = wl.cfg
+    layers = []
+    for li, sl in enumerate(wl.layers):
+        c = sl.cfg
+        layers.append(MoELayer(c.H, c.I, sl.layer.E, c.K, sl.router, sl.gate, sl.up, sl.down, c.types,
+                               shared=sl.shared, max_tokens=cfg.tokens, timeline=True, norm_w=wl.norms[li],
+                               add_residual=True))
+    out = torch.empty(cfg.tokens, cfg.n_layers, cfg.H, device="cuda")
+
+    def step(i):
+        t = i % cfg.tokens
+        routes = None if wl.routes is None else [(r[2][t], r[3][t]) for r in wl.routes]
+        decode_stack(layers, wl.X[t], out=out[t], routes=routes, step=i)
+    for i in range(16):
+        step(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            step(i)
+    g.replay()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    for m in layers:
+        m.check()
+    us = a.elapsed_time(b) * 1000.0 / steps
+    nwg = torch.cuda.get_device_properties(0).multi_processor_count
+    tick_us = 1000.0 / wm_clock_khz()
+    tls = [m.timeline().cpu().numpy().reshape(-1)[: nwg * 32].reshape(nwg, 32).astype(np.int64) for m in layers]
+    t0 = tls[0][:, 0][tls[0][:, 0] > 0].min()
+    marks = [(0, "start"), (8, "x records"), (16, "slot 0 published"), (4, "last SwiGLU"), (6, "combine"),
+             (7, "end")]
+    print(f"chained decode launch timeline, workload {cfg.name}: {cfg.n_layers} layers in one launch "
+          f"(wm_moe_decode_stack), last of {steps} tokens replayed in a HIP graph, {nwg} workgroups; per layer the "
+          f"median workgroup's marks, us from the launch's earliest workgroup start")
+    print("layer " + " ".join(f"{lab:>17s}" for _, lab in marks) + f" {'latest end':>11s}")
+    for li, tl in enumerate(tls):
+        row = []
+        for k, _ in marks:
+            v = tl[:, k]
+            v = v[v > 0]
+            row.append(f"{np.median((v - t0) * tick_us):17.2f}" if v.size else f"{'-':>17s}")
+        print(f"{li:5d} " + " ".join(row) + f" {(tl[:, 7].max() - t0) * tick_us:11.2f}")
+    print(f"time per token over the replay (HIP events): {us:.2f} us")
+
+
+def stream_report(name, n_slots, steps, warmup, layout="packed"):
     """Decode steps of the workload's layer shape with the experts in pinned
     host memory, made resident on demand in a pool of n_slots HBM slots
     (wm_pool_*), Zipf routing with consecutive-token overlap (the forced
-    routing of the C4 workload, at this layer's E and K).  One JSON line:
-    tokens/s, misses per token, achieved host -> device GB/s."""
+    routing of the C4 workload, at this layer's E and K).  layout "packed":
+    each expert one slot image in host memory, one copy per miss
+    (wm_pool_acquire_packed); "parts": gate, up and down tensors apart, three
+    copies per miss (wm_pool_acquire).  One JSON line: tokens/s, misses per
+    token, achieved host -> device GB/s."""
     import numpy as np
     import torch
     import winmoe_amd as wm
@@ -522,13 +584,18 @@ def stream_report(name, n_slots, steps, warmup):
     E = sl.layer.E
     parts = [wm.matrix_bytes(c.types[0], c.I, c.H), wm.matrix_bytes(c.types[1], c.I, c.H),
              wm.matrix_bytes(c.types[2], c.H, c.I)]
-    log(f"copying {E} experts ({E * sum(parts) / 1e9:.2f} GB) to pinned host memory")
-    src = []
-    for t in (sl.gate, sl.up, sl.down):
-        h = torch.empty(t.numel(), dtype=torch.uint8, pin_memory=True)
-        h.copy_(t)
-        src.append(h.view(E, -1))
+    log(f"copying {E} experts ({E * sum(parts) / 1e9:.2f} GB) to pinned host memory ({layout})")
     pool = wm.ExpertPool(n_slots, *parts)
+    src = []
+    if layout == "packed":
+        packed = torch.zeros((E, pool.slot_bytes), dtype=torch.uint8, pin_memory=True)
+        for o, t, nb in zip(pool.offsets, (sl.gate, sl.up, sl.down), parts):
+            packed[:, o:o + nb].copy_(t.view(E, -1)[:, :nb])
+    else:
+        for t in (sl.gate, sl.up, sl.down):
+            h = torch.empty(t.numel(), dtype=torch.uint8, pin_memory=True)
+            h.copy_(t)
+            src.append(h.view(E, -1))
     layer = pool.layer(c.H, c.I, c.K, c.types, shared=sl.shared, max_tokens=steps + warmup)
     rng = np.random.default_rng(11)
     T = steps + warmup
@@ -539,7 +606,10 @@ def stream_report(name, n_slots, steps, warmup):
     slots = torch.empty(T, c.K, dtype=torch.int32, device="cuda")
 
     def step(t):
-        pool.acquire(0, ids[t], *src, out=slots[t])
+        if layout == "packed":
+            pool.acquire_packed(0, ids[t], packed, out=slots[t])
+        else:
+            pool.acquire(0, ids[t], *src, out=slots[t])
         layer.decode_forced(X[t % X.shape[0]], slots[t], w[t], out=out, step=t)
         pool.release()
     for t in range(warmup):
@@ -554,7 +624,8 @@ def stream_report(name, n_slots, steps, warmup):
     layer.check()
     h1, m1, b1 = pool.stats()
     rec = {"report": "host -> HBM expert streaming", "workload": cfg.name, "experts": E, "top_k": c.K,
-           "expert_bytes": sum(parts), "pool_slots": n_slots, "pool_bytes": n_slots * pool.slot_bytes,
+           "expert_bytes": sum(parts), "host_layout": layout, "pool_slots": n_slots,
+           "pool_bytes": n_slots * pool.slot_bytes,
            "routing": f"zipf s={synth.ZIPF_S} overlap={synth.OVERLAP}", "steps": steps, "warmup": warmup,
            "tokens_per_s": round(steps / dt, 1), "ms_per_step": round(dt * 1e3 / steps, 4),
            "hit_rate": round((h1 - h0) / max(1, (h1 - h0) + (m1 - m0)), 4),
@@ -587,6 +658,9 @@ def main():
                     help="host -> HBM expert streaming: run --config's layer shape with its experts in pinned host "
                          "memory through a pool of this many HBM slots (Zipf routing) and print one report line "
                          "instead of the JSON line")
+    ap.add_argument("--stream-layout", default="packed", choices=["packed", "parts"],
+                    help="with --stream-slots: host copies of the experts as one slot image each (one copy per miss) "
+                         "or as separate gate / up / down tensors (three copies per miss)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run 4 plain device copies and 4 read-only reductions of this many MiB (kernels of "
                          "known traffic for the rocprofv3 FETCH_SIZE / WRITE_SIZE calibration)")
@@ -656,7 +730,7 @@ def main():
         timeline_report(args.config, min(args.steps, 256))
         return
     if args.stream_slots > 0:
-        stream_report(args.config, args.stream_slots, min(args.steps, 256), min(args.warmup, 64))
+        stream_report(args.config, args.stream_slots, min(args.steps, 256), min(args.warmup, 64), args.stream_layout)
         return
 
     head = run(args.config, args.steps, args.warmup, True)

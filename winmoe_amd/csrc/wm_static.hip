@@ -21,8 +21,11 @@
 
 using namespace wm;
 
-// The workspace of every supported decode layer without WM_FLAG_TIMELINE fits
-// (E <= 1024, K <= 16, H and I <= 4096 need at most ~3.6 MB).
+// The workspace of every supported decode layer without WM_FLAG_TIMELINE fits:
+// E <= 1024, K <= 16 and H, I, inter_shared <= 4096 need at most 2,685,440 B
+// (about 2.6 MB, of the 3 MiB here).  A layer whose workspace is larger (a
+// shared expert wider than 4096, or WM_FLAG_TIMELINE: 3,734,016 B at those
+// sizes) is refused with WM_EINVAL.
 static __device__ __align__(256) uint8_t scratch[WM_NOALLOC_SCRATCH_BYTES];
 
 namespace {
