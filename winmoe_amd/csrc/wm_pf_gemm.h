@@ -5,7 +5,8 @@
 //
 // One workgroup per CU works through a static list of items: item j of a
 // launch is (pass, block of 128 matrix rows), and workgroup b takes items
-// b, b + grid, b + 2 grid, ...  For each item it streams the block's rows (of
+// k, k + grid, k + 2 grid, ... with k = pf_item_slot(b) (the row blocks of a
+// pass on workgroups of one XCD).  For each item it streams the block's rows (of
 // gate and up, or of down) through an S-stage LDS ring, 256 columns per
 // stage (Q8_0: 8 blocks; K-quants: one super-block), filled by
 // global_load_lds:
@@ -158,6 +159,20 @@ struct PfGemm {
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
+
+// Workgroups are dispatched to the 8 XCDs in turn (workgroup b on XCD b % 8)
+// and each XCD has its own L2.  Item j of round i goes to workgroup b with
+// j - i * grid = slot(b): the R consecutive items of one pass (its row groups,
+// which read the same activations) land on workgroups of one XCD, so the
+// activations come from HBM once per pass rather than once per XCD.  A
+// bijection of [0, grid) when grid is a multiple of 8 R; the identity
+// otherwise.
+constexpr int PF_XCDS = 8;
+WM_HD int pf_item_slot(int b, int grid, int R) {
+    if (R <= 0 || grid % (PF_XCDS * R)) return b;
+    const int x = b % PF_XCDS, q = b / PF_XCDS;
+    return ((q / R) * PF_XCDS + x) * R + q % R;
+}
 
 // Raw buffer resource over [p, p + bytes) (gfx9 word 3: 32-bit data format).
 WM_DEV __amdgpu_buffer_rsrc_t gm_rsrc(const void* p, int bytes) {
@@ -469,11 +484,12 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
     const bool cw = wave < GM_CW;
     const int n_rp = a.npass[0], n_sp = a.npass[1];
     const int n_r = a.sel == 2 ? 0 : n_rp * a.nrb_r, n_items = n_r + (a.sel == 1 ? 0 : n_sp * a.nrb_s);
-    if ((int)blockIdx.x >= n_items) return;
+    const int k0 = pf_item_slot((int)blockIdx.x, (int)gridDim.x, a.sel == 2 ? a.nrb_s : a.nrb_r);
+    if (k0 >= n_items) return;
 
     // item i of this workgroup: pass, row group, column steps
     auto item = [&](int i, int& pass, int& rg, int& nkc) __attribute__((always_inline)) -> bool {
-        const int j = (int)blockIdx.x + i * (int)gridDim.x;
+        const int j = k0 + i * (int)gridDim.x;
         if (j >= n_items) return false;
         if (j < n_r) {
             pass = j / a.nrb_r;
