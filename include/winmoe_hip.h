@@ -216,8 +216,8 @@ int wm_moe_decode_forced(const wm_layer_desc* d, const float* x, const int32_t* 
  * fp32[n_layers][H] receives every layer's output; ids, w: NULL (every layer
  * routed by its router) or one device pointer pair per layer (a NULL entry:
  * that layer uses its router).  Layers that the chained kernel does not take
- * (formats without an instance, LDS) run one launch each, with the same
- * results. */
+ * (formats without an instance, LDS, workspaces that overlap another layer's
+ * of the same launch) run one launch each, with the same results. */
 int wm_moe_decode_stack(int n_layers, const wm_layer_desc* const* d, void* const* ws, const int64_t* ws_bytes,
                         const float* x, float* out, const int32_t* const* ids, const float* const* w,
                         int max_tokens, int step, void* stream);

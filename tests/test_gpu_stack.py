@@ -162,3 +162,31 @@ def test_stack_types_without_a_chained_instance(wm):
     layers, routes = _chain(cfg, 3, T, E=64)
     X = synth.make_hidden(cfg, tokens=T)
     _compare(layers, routes, X, T)
+
+
+def test_stack_layers_sharing_a_workspace(wm):
+    """Two layers of a chain on one workspace (the layer tags and hand-off
+    words live there) cannot share a launch: the call runs the chain one
+    launch per layer instead, with the same outputs."""
+    import torch
+    from winmoe_amd import synth
+    from winmoe_amd.moe import decode_stack
+    cfg = synth.CONFIGS["c1"]
+    T = 3
+    case("stack with a shared workspace")
+    layers, routes = _chain(cfg, 3, T, E=64)
+    twins = _twins(layers)
+    twins[1].ws = twins[0].ws
+    X = synth.make_hidden(cfg, tokens=T)
+    ref = torch.empty(T, 3, layers[0].H, device="cuda")
+    got = torch.empty_like(ref)
+    for t in range(T):
+        h = X[t]
+        for li, m in enumerate(layers):
+            m.decode_forced(h, routes[li][0][t], routes[li][1][t], out=ref[t, li], step=t)
+            h = ref[t, li]
+        decode_stack(twins, X[t], out=got[t], routes=[(r[0][t], r[1][t]) for r in routes], step=t)
+    torch.cuda.synchronize()
+    a, b = host(ref), host(got)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert all(tw.status() == 0 for tw in twins)

@@ -830,6 +830,14 @@ extern "C" int wm_moe_decode_stack(int n_layers, const wm_layer_desc* const* d, 
             const int l = l0 + k;
             const wm_layer_desc* dl = d[l];
             if (dl->flags & (WM_FLAG_MULTI_KERNEL | WM_FLAG_ITEM_KERNEL)) { ok = false; break; }
+            // layers of one launch need workspaces of their own (each holds
+            // the layer's launch tag and tagged hand-off words); layers that
+            // share one run one launch each, in order
+            for (int q = l0; ok && q < l; q++) {
+                const uint8_t *a0 = (const uint8_t*)ws[q], *b0 = (const uint8_t*)ws[l];
+                if (a0 < b0 + ws_bytes[l] && b0 < a0 + ws_bytes[q]) ok = false;
+            }
+            if (!ok) break;
             const WsLayout L = layout(dl, max_tokens);
             uint8_t* w8 = (uint8_t*)ws[l];
             int32_t* tid = (int32_t*)(w8 + L.tr_ids) + (int64_t)slot * dl->top_k;
