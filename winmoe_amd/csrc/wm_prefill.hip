@@ -108,12 +108,17 @@ __global__ __launch_bounds__(256) void k_pf_router(const uint16_t* __restrict__ 
 // 32 FMAs), the columns in chunks of 128 staged in LDS twice over: the loads
 // (16-byte vectors) of the next two chunks are in flight while the current
 // one is summed.  Every chain adds its columns in the same order as above, so the
-// logits are the same bit for bit.
-constexpr int PQ_T = 16, PQ_E = 32, PQ_CH = 128, PQ_LD = PQ_CH + 4;
+// logits are the same bit for bit.  LDS rows are 144 floats (16 mod 32 and
+// mod 64 banks) and the router row of local expert 8q + j is kept at row
+// q + 4j: the four expert groups of a wave (q = 0..3) read the same column of
+// rows q + 4j, 16 banks apart, with no conflict; rows stay 16-byte aligned
+// for the staging's 16-byte stores.
+constexpr int PQ_T = 16, PQ_E = 32, PQ_CH = 128, PQ_LD = PQ_CH + 16;
+WM_HD constexpr int pq_wrow(int e) { return (e >> 3) + 4 * (e & 7); }
 __global__ __launch_bounds__(256) void k_pf_router_v(const uint16_t* __restrict__ x, const float* __restrict__ W, int H,
                                                      int T, int E, float* __restrict__ logits) {
-    __shared__ float xs[2][PQ_T * PQ_LD];
-    __shared__ float wsh[2][PQ_E * PQ_LD];
+    __shared__ __attribute__((aligned(16))) float xs[2][PQ_T * PQ_LD];
+    __shared__ __attribute__((aligned(16))) float wsh[2][PQ_E * PQ_LD];
     const int t0 = blockIdx.x * PQ_T, e0 = blockIdx.y * PQ_E;
     const int tid = threadIdx.x, l = tid & 15, sb = tid >> 4, tq = sb >> 2, eq = sb & 3;
     // staging: x row tid / 16, columns 8 (tid % 16) .. + 8 (one 16-byte load
@@ -136,21 +141,14 @@ __global__ __launch_bounds__(256) void k_pf_router_v(const uint16_t* __restrict_
         for (int q = 0; q < 4; q++) wv2[q] = win ? wsrc[c0 / 4 + q] : z;
     };
     auto lstore = [&](int b) {
-        float* xd = &xs[b][xr * PQ_LD + xc];
-        const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+        f32x4* xd = (f32x4*)&xs[b][xr * PQ_LD + xc];
+        xd[0] = (f32x4){bf16f((uint16_t)(xv.x & 0xFFFFu)), bf16f((uint16_t)(xv.x >> 16)),
+                        bf16f((uint16_t)(xv.y & 0xFFFFu)), bf16f((uint16_t)(xv.y >> 16))};
+        xd[1] = (f32x4){bf16f((uint16_t)(xv.z & 0xFFFFu)), bf16f((uint16_t)(xv.z >> 16)),
+                        bf16f((uint16_t)(xv.w & 0xFFFFu)), bf16f((uint16_t)(xv.w >> 16))};
+        f32x4* wd = (f32x4*)&wsh[b][pq_wrow(wr) * PQ_LD + wc];
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            xd[2 * k] = bf16f((uint16_t)(xw[k] & 0xFFFFu));
-            xd[2 * k + 1] = bf16f((uint16_t)(xw[k] >> 16));
-        }
-        float* wd = &wsh[b][wr * PQ_LD + wc];
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            wd[4 * q] = __builtin_bit_cast(float, wv[q].x);
-            wd[4 * q + 1] = __builtin_bit_cast(float, wv[q].y);
-            wd[4 * q + 2] = __builtin_bit_cast(float, wv[q].z);
-            wd[4 * q + 3] = __builtin_bit_cast(float, wv[q].w);
-        }
+        for (int q = 0; q < 4; q++) wd[q] = __builtin_bit_cast(f32x4, wv[q]);
     };
     float acc[4][8];
 #pragma unroll
@@ -170,14 +168,14 @@ __global__ __launch_bounds__(256) void k_pf_router_v(const uint16_t* __restrict_
         for (int q = 0; q < 4; q++) wv[q] = wv2[q];
         if (c + 2 < nch) gload2((c + 2) * PQ_CH);
         const float* xb = &xs[b][(4 * tq) * PQ_LD + l];
-        const float* wb = &wsh[b][(8 * eq) * PQ_LD + l];
+        const float* wb = &wsh[b][eq * PQ_LD + l];
 #pragma unroll 2
         for (int st = 0; st < PQ_CH / 16; st++) {
             float xq[4], wq[8];
 #pragma unroll
             for (int i = 0; i < 4; i++) xq[i] = xb[i * PQ_LD + 16 * st];
 #pragma unroll
-            for (int j = 0; j < 8; j++) wq[j] = wb[j * PQ_LD + 16 * st];
+            for (int j = 0; j < 8; j++) wq[j] = wb[4 * j * PQ_LD + 16 * st];
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
