@@ -452,6 +452,37 @@ def test_prefill_router_matches_oracle(wm, orc, shared):
     assert sl.layer.prefill_status() == 0
 
 
+def test_prefill_router_kernels_agree(wm):
+    """The two prefill router kernels (16-byte aligned router rows and H a
+    multiple of 128: the vectorised tiles; otherwise the plain ones) give the
+    same logits, so the same routing and outputs bit for bit: the same layer
+    run with its router at a 16-byte aligned address and at one 4 bytes past
+    it (E = 40, H = 1024, 37 tokens: partial tiles both ways)."""
+    import torch
+    from winmoe_amd import synth
+    from winmoe_amd.moe import MoELayer
+    cfg = _pf_cfg(E=40, K=4, H=1024, I=512)
+    T = 37
+    sl = synth.build_layer(cfg, max_tokens=T)
+    X = synth.make_hidden(cfg, tokens=T)
+    E, H = cfg.E, cfg.H
+    buf = torch.zeros(E * H + 4, dtype=torch.float32, device="cuda")
+    shifted = buf[1:1 + E * H].view(E, H)
+    shifted.copy_(sl.router)
+    assert shifted.data_ptr() % 16 == 4 and sl.router.data_ptr() % 16 == 0
+    L = sl.layer
+    moved = MoELayer(H, cfg.I, E, cfg.K, shifted, L.gate_exps, L.up_exps, L.down_exps, L.types, max_tokens=T)
+    case(f"prefill router kernels T={T}")
+    a = host(L.prefill(X))
+    b = host(moved.prefill(X))
+    ia, wa = (host(v) for v in L.prefill_routing(T))
+    ib, wb = (host(v) for v in moved.prefill_routing(T))
+    assert np.array_equal(ia, ib)
+    assert np.array_equal(wa.view(np.uint32), wb.view(np.uint32))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert L.prefill_status() == 0 and moved.prefill_status() == 0
+
+
 def test_prefill_scales_and_narrow_shared(wm, orc):
     """Tokens whose magnitudes span 1e-6 .. 1e4 (one all zero, one with a
     single huge entry), a shared expert half as wide as the routed ones, an
