@@ -594,7 +594,10 @@ WM_DEV void stream_wave(const PersistArgs& a, uint8_t* smem, int wave_v, uint32_
                         b = 1ull;
                         break;
                     }
-                    backoff(it);
+                    // (a short pause throughout: picks come ~0.5 us apart, and
+                    // the growing pause of the other waits made the first
+                    // routed tiles late, C3 22.2 -> 21.8 us per step)
+                    __builtin_amdgcn_s_sleep(1);
                 }
             }
             base = b & ~1ull;
@@ -815,8 +818,8 @@ WM_DEV void publish_bases(const PersistArgs& a, lctl_t* ctl, int k, int e, bool 
     rb[2] = valid ? ((uint64_t)(uintptr_t)a.down + (uint64_t)e * (uint64_t)a.dstride) | 1ull : 1ull;
 }
 
-// Routing from replica `rep` of the tagged logits (polled, with a pause
-// between polls, until every one carries `tag`), then the K-pass arg-max and
+// Routing from replica `rep` of the tagged logits (polled until every one
+// carries `tag`), then the K-pass arg-max and
 // softmax of wave_topk_n.  Lanes k < K return their pick (id, weight).
 template <int MAXV>
 WM_DEV void route_tagged(const PersistArgs& a, lctl_t* ctl, int rep, uint32_t tag, int lane, int& my_e, float& wk,
@@ -842,7 +845,8 @@ WM_DEV void route_tagged(const PersistArgs& a, lctl_t* ctl, int rep, uint32_t ta
             give_up(ctl, a.status, lane);
             break;
         }
-        __builtin_amdgcn_s_sleep(8);
+        // (no pause: every re-read is a memory round trip of ~1 us; a
+        // 512-clock pause between them put the routing ~0.3 us later)
 #pragma unroll
         for (int i = 0; i < MAXV; i++)
             if ((uint32_t)(tv[i] >> 32) != tag) tv[i] = gld_agent64(src + 64 * i);
