@@ -129,6 +129,30 @@ WM_DEV void lds_wait(lctl_t* ctl, const lds32_t* p, uint32_t target, int32_t* st
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// As lds_wait with pauses of at most 128 clocks: the waits of the helper
+// waves (x loader, router, publisher), whose ends are on the step's critical
+// path (the SwiGLU hand-off after a slot's last gate/up tile, the combine
+// after the last down tile, a chained layer's input) while only one wave of
+// the SIMD polls.  Against the doubling pause: C4 134.1 -> 128.7 us per
+// token, C2 35.56 -> 35.36, C1 14.80 -> 14.67, C3 21.52 -> 21.35 us per
+// step; the streaming waves' waits keep it (with the short pause there C3
+// lost 0.4 us: their polls take issue slots from the tiles beside them).
+WM_DEV void lds_wait_f(lctl_t* ctl, const lds32_t* p, uint32_t target, int32_t* status, int lane) {
+    uint32_t it = 0;
+    while (lds_ld(p) < target) {
+        if (++it > PSPIN || aborted(ctl)) {
+            give_up(ctl, status, lane);
+            break;
+        }
+        if (it < 2) __builtin_amdgcn_s_sleep(1);
+        else __builtin_amdgcn_s_sleep(2);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+WM_DEV void wait_all_f(lctl_t* ctl, const lds32_t* p, int n, int32_t* status, int lane) {
+    for (int i = 0; i < n; i++) lds_wait_f(ctl, p + i, 1u, status, lane);
+}
+
 // The wave waits until all n words at p are nonzero (bounded).
 WM_DEV void wait_all(lctl_t* ctl, const lds32_t* p, int n, int32_t* status, int lane) {
     for (int i = 0; i < n; i++) lds_wait(ctl, p + i, 1u, status, lane);
@@ -1008,7 +1032,7 @@ template <int NST> WM_DEV void x_norm_in(const PersistArgs& a, uint8_t* smem, ld
     if (a.tx_in) {
         vec_dma(a.norm_w, a.H, wl, lane);
         x_tagged_part(a, smem, xl, prev_tag, PW, PW + 1, lane);
-        wait_all(ctl_of(smem), ctl_of(smem)->xpart, PW + 1, a.status, lane);
+        wait_all_f(ctl_of(smem), ctl_of(smem)->xpart, PW + 1, a.status, lane);
     } else {
         vec_dma(a.x, a.H, xl, lane);
         vec_dma(a.norm_w, a.H, wl, lane);
@@ -1036,7 +1060,7 @@ WM_DEV void helper_xload(const PersistArgs& a, uint8_t* smem, uint32_t prev_tag,
         }
     } else if (a.tx_in) {
         x_tagged_part(a, smem, xl, prev_tag, PW, PW + 1, lane);
-        wait_all(ctl, ctl->xpart, PW + 1, a.status, lane);
+        wait_all_f(ctl, ctl->xpart, PW + 1, a.status, lane);
     } else {
         router_dma(a.x, nullptr, a.H, 0, -1, -1, xl, a.x_region, lane);
     }
@@ -1053,7 +1077,7 @@ WM_DEV void helper_xload(const PersistArgs& a, uint8_t* smem, uint32_t prev_tag,
     // launch's tag (each has read the old epoch by then); the next launch
     // starts only after this one ends, so the new value is read only then
     if (blockIdx.x == 0) {
-        lds_wait(ctl, &ctl->rows_in, 1u, a.status, lane);       // (the tag is set before rows_in)
+        lds_wait_f(ctl, &ctl->rows_in, 1u, a.status, lane);       // (the tag is set before rows_in)
         const uint32_t tag = ctl->tag;
         for (int i = lane; i < a.nwg; i += 64) {
             uint32_t it = 0;
@@ -1094,7 +1118,7 @@ WM_DEV void helper_router(const PersistArgs& a, uint8_t* smem, int lane) {
         // rows 0 and 2 here, rows 1 and 3 on the publishing helper, x on the
         // second staging wave: three waves' loads land together
         if (nr > 0) router_dma(nullptr, a.router, a.H, r0, 0, nr > 2 ? 2 : -1, lds + a.o_router, a.x_region, lane);
-        lds_wait(ctl, &ctl->x_in, 1u, a.status, lane);
+        lds_wait_f(ctl, &ctl->x_in, 1u, a.status, lane);
         lds_set(&ctl->rows_in, 1u, lane);          // (also when this workgroup has no router rows)
         if (lane == 0) ctl->t[1] = now();
         if (nr > 0)   // rows 0 and 2 here, rows 1 and 3 on the other helper
@@ -1154,7 +1178,7 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
         const int r0 = P.w * a.rr, nr = max(0, min(a.rr, a.E - r0));
         if (nr > 1) router_dma(nullptr, a.router, a.H, r0, 1, nr > 3 ? 3 : -1, lds + a.o_router, a.x_region, lane);
     }
-    lds_wait(ctl, &ctl->rows_in, 1u, a.status, lane);
+    lds_wait_f(ctl, &ctl->rows_in, 1u, a.status, lane);
     const uint32_t tag = ctl->tag;
     // The SwiGLU hand-off words carry the tag's low 16 bits: every launch of
     // the layer rewrites every word a launch can read (each slot's I
@@ -1167,7 +1191,7 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
     }
     // the x loader computes the shared gate from x in the router region: that
     // region is given up (router_done) only after it is done
-    if (sh && a.sh_gate_inp) lds_wait(ctl, &ctl->sgate_ready, 1u, a.status, lane);
+    if (sh && a.sh_gate_inp) lds_wait_f(ctl, &ctl->sgate_ready, 1u, a.status, lane);
     lds_set(&ctl->router_done[1], 1u, lane);
     __builtin_amdgcn_s_setprio(0);
 
@@ -1183,7 +1207,7 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
         const int row0 = P.tw0 * rpt, nrows = min(a.I, (P.tw0 + P.ngu) * rpt) - row0;
         for (int q = 0; q < nq; q++) {
             const int slot = slot_at(q, K, sh);
-            lds_wait(ctl, &ctl->gu_done[slot], (uint32_t)n_gu, a.status, lane);
+            lds_wait_f(ctl, &ctl->gu_done[slot], (uint32_t)n_gu, a.status, lane);
             __builtin_amdgcn_s_setprio(2);
             if (lane == 0 && q < 12) ctl->t[16 + q] = now();
             const bool valid = slot == K || ctl->valid[slot] != 0;
@@ -1207,7 +1231,7 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
         const int rpt = geometry(DT, a.I).rpt;
         const int h0 = P.d0 * rpt, nrows = min(a.H, (P.d0 + P.ndn) * rpt) - h0;
         // the routing weights into registers while the down tiles finish
-        lds_wait(ctl, &ctl->routed, 1u, a.status, lane);     // the weights come after the last pick
+        lds_wait_f(ctl, &ctl->routed, 1u, a.status, lane);     // the weights come after the last pick
         typedef __attribute__((address_space(3))) const uint64_t l64c_t;
         const l64c_t* stw = (const l64c_t*)(lds + a.o_stage);     // (a chained launch's staged input)
         const uint32_t otag = ctl->tag;
@@ -1218,7 +1242,7 @@ WM_DEV void helper_publish(const PersistArgs& a, uint8_t* smem, int lane) {
             vk[k] = k < K && ctl->valid[k] != 0;
             wk[k] = k < K ? ctl->w[k] : 0.0f;
         }
-        lds_wait(ctl, &ctl->n_done, (uint32_t)n_dn, a.status, lane);   // every down tile is processed
+        lds_wait_f(ctl, &ctl->n_done, (uint32_t)n_dn, a.status, lane);   // every down tile is processed
         if (lane == 0) ctl->t[6] = now();
         for (int r = lane; r < nrows; r += 64) {
             // out[h] = sum_k w_k y_k[h] (k order, invalid ids skipped) + gate * y_shared[h]
