@@ -96,11 +96,12 @@ def _compare(layers, routes, X, T):
     return b
 
 
-@pytest.mark.parametrize("NL", [2, 8, 11])
+@pytest.mark.parametrize("NL", [1, 2, 8, 9, 11])
 def test_stack_c4_layers_forced(wm, NL):
     """The C4 layer shape (Q2_K gate/up, Q3_K down, top-3, RMSNorm in,
-    residual out, forced Zipf routes) at 64 experts: 2 layers, 8 (one
-    launch) and 11 (a launch of 8, then one of 3)."""
+    residual out, forced Zipf routes) at 64 experts: 1 layer (no chained
+    launch), 2, 8 (one launch), 9 (a launch of 8, then the last layer on its
+    own) and 11 (a launch of 8, then one of 3)."""
     from winmoe_amd import synth
     cfg = synth.CONFIGS["c4"]
     T = 5
