@@ -84,6 +84,13 @@ enum {
  * wm_workspace_reset makes the workspace usable again.  Lets a test drive the
  * timeout path without anything waiting long. */
 #define WM_FLAG_SPIN_PROBE 16
+/* wm_layer_desc.flags, prefill only: the expert GEMMs take the batch's pairs
+ * in passes of at most 16 (PASS16) or 32 (PASS32) pairs of one expert.  By
+ * default a batch that averages at most 4 pairs per expert (T*K <= 4*E) uses
+ * 16, any other 32.  The results are the same bit for bit either way; only
+ * the speed differs. */
+#define WM_FLAG_PREFILL_PASS16 32
+#define WM_FLAG_PREFILL_PASS32 64
 
 /* One MoE layer.  Expert tensors are the raw GGUF blocks, stacked by expert:
  * gate/up expert e = [inter rows][hidden/QK blocks] at gate_exps + e*gate_stride,

@@ -540,6 +540,19 @@ def test_prefill_rejects_unsupported_formats(wm, types):
     assert np.isfinite(host(sl.layer.decode(X[0].float()))).all()
 
 
+def test_prefill_rejects_two_pass_sizes(wm):
+    """Both pass-size flags at once is an argument error."""
+    from winmoe_amd import _lib, synth
+    cfg = _pf_cfg(E=16, K=4, H=512, I=256, routing="zipf")
+    sl = synth.build_layer(cfg, max_tokens=8)
+    X = synth.make_hidden(cfg, tokens=8)
+    ids = np.tile(np.arange(4, dtype=np.int32), (8, 1))
+    w = np.full((8, 4), 0.25, np.float32)
+    with pytest.raises(wm.WinMoEError) as ei:
+        _prefill_pass16(sl, X, ids, w, flag=_lib.FLAG_PREFILL_PASS16 | _lib.FLAG_PREFILL_PASS32)
+    assert ei.value.rc == _lib.WM_EINVAL
+
+
 def test_prefill_forced_multi_pass_and_bad_ids(wm, orc):
     """Caller routing: one expert used by every token (three 32-pair passes),
     one invalid id (skipped, reported)."""
@@ -576,6 +589,8 @@ def test_prefill_c5_full(wm, orc):
     case("prefill c5 full")
     out = host(sl.layer.prefill_forced(X, dev(ids), dev(w)))
     assert np.isfinite(out).all()
+    case("prefill c5 full, passes of 16 pairs")
+    assert np.array_equal(out.view(np.uint32), _prefill_pass16(sl, X, ids, w).view(np.uint32))
     for t in (0, 1, 255, T - 1):
         case(f"prefill c5 oracle token={t}")
         _, _, ref = oracle_token(orc, sl, host(X[t].float()), ids=ids[t], w=w[t])
@@ -604,6 +619,19 @@ KQ_PREFILL = [
 ]
 
 
+def _prefill_pass16(sl, X, ids, w, flag=None):
+    """The same forced prefill with the pairs taken in passes of 16 (or, with
+    flag, as flag says); the layer's flags are restored."""
+    from winmoe_amd import _lib
+    d = sl.layer.desc
+    old = d.flags
+    d.flags = old | (_lib.FLAG_PREFILL_PASS16 if flag is None else flag)
+    try:
+        return host(sl.layer.prefill_forced(X, dev(ids), dev(w)))
+    finally:
+        d.flags = old
+
+
 def _kq_routes(T, E, K, rng):
     """Every token uses expert 0 (passes of 32 + 32 + rest rows: both row
     tiles); the other slots are distinct random experts."""
@@ -619,7 +647,8 @@ def _kq_routes(T, E, K, rng):
 def test_prefill_kquant_matches_oracle(wm, orc, gu, dn, sh, H):
     """Prefill with K-quant expert matrices (and a shared expert of another
     format) == the oracle token by token, with a 70-token batch whose
-    expert 0 takes three passes."""
+    expert 0 takes three passes (five in passes of 16 pairs: the same
+    results bit for bit)."""
     from winmoe_amd import synth
     E, K, I, T = 24, 3, 512, 70
     cfg = synth.LayerConfig(f"pf_kq_{gu}_{dn}", E=E, K=K, H=H, I=I, types=(gu, gu, dn),
@@ -630,6 +659,8 @@ def test_prefill_kquant_matches_oracle(wm, orc, gu, dn, sh, H):
     ids, w = _kq_routes(T, E, K, np.random.default_rng(gu * 31 + dn))
     case(f"prefill kq gate/up={gu} down={dn} shared={sh} H={H} T={T}")
     out = host(sl.layer.prefill_forced(X, dev(ids), dev(w)))
+    case(f"prefill kq gate/up={gu} down={dn} shared={sh} H={H} T={T}, passes of 16 pairs")
+    assert np.array_equal(out.view(np.uint32), _prefill_pass16(sl, X, ids, w).view(np.uint32))
     worst = 0.0
     for t in range(T):
         _, _, ref = oracle_token(orc, sl, host(X[t].float()), ids=ids[t], w=w[t])
@@ -644,7 +675,8 @@ def test_prefill_kquant_full_layer(wm, orc, name):
     """A 512-token prefill through the full 512-expert layer of the Q4_K /
     Q6_K (shared Q8_0) and the Q2_K / Q3_K workloads with Zipf routing: a
     sample of tokens against the oracle, every token against the decode path
-    with the same routing, and a second call bit-identical to the first."""
+    with the same routing, and a second call bit-identical to the first, as
+    is a call that takes the pairs in passes of 32 instead of 16."""
     import dataclasses
     from winmoe_amd import synth
     cfg = dataclasses.replace(synth.CONFIGS[name], tokens=512, routing="zipf", n_layers=1, x_dtype="bf16")
@@ -657,6 +689,10 @@ def test_prefill_kquant_full_layer(wm, orc, name):
     again = host(sl.layer.prefill_forced(X, dev(ids), dev(w)))
     assert np.isfinite(out).all()
     assert np.array_equal(out.view(np.uint32), again.view(np.uint32))
+    from winmoe_amd import _lib
+    case(f"prefill {name} full, passes of 32 pairs")
+    p32 = _prefill_pass16(sl, X, ids, w, flag=_lib.FLAG_PREFILL_PASS32)
+    assert np.array_equal(out.view(np.uint32), p32.view(np.uint32))
     for t in (0, 1, 255, T - 1):
         case(f"prefill {name} oracle token={t}")
         _, _, ref = oracle_token(orc, sl, host(X[t].float()), ids=ids[t], w=w[t])

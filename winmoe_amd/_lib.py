@@ -29,6 +29,8 @@ FLAG_TIMELINE = 2
 FLAG_ITEM_KERNEL = 4
 FLAG_PERSIST_KERNEL = 8
 FLAG_SPIN_PROBE = 16
+FLAG_PREFILL_PASS16 = 32
+FLAG_PREFILL_PASS32 = 64
 
 _vp, _i64 = C.c_void_p, C.c_int64
 

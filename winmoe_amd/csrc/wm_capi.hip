@@ -1015,6 +1015,11 @@ static int run_prefill(const wm_layer_desc* d, const uint16_t* x, int T, const i
     a.act_hi = (uint16_t*)(w8 + L.act_hi); a.act_lo = (uint16_t*)(w8 + L.act_lo); a.act_sc = (float*)(w8 + L.act_sc);
     a.act_stride = L.act_stride; a.y = (float*)(w8 + L.y); a.out = out;
     a.n_wg = cu_count();
+    WM_CHECK_ARG((d->flags & (WM_FLAG_PREFILL_PASS16 | WM_FLAG_PREFILL_PASS32)) !=
+                 (WM_FLAG_PREFILL_PASS16 | WM_FLAG_PREFILL_PASS32));
+    a.pass_m = (d->flags & WM_FLAG_PREFILL_PASS16)   ? 16
+               : (d->flags & WM_FLAG_PREFILL_PASS32) ? 32
+                                                     : prefill_pass_size(T, a.K, a.E);
     // the expert GEMMs read 16-byte granules from row starts
     WM_CHECK_ARG(al(a.gate, 16) && al(a.up, 16) && al(a.down, 16) && a.gstride % 16 == 0 && a.ustride % 16 == 0 &&
                  a.dstride % 16 == 0 && (!sh || (al(a.sh_gate, 16) && al(a.sh_up, 16) && al(a.sh_down, 16))));

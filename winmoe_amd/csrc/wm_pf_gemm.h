@@ -17,7 +17,8 @@
 //     and Q6_K 210 B start up to 24 or 28 bytes in: 7, 9 and 15).  Longer
 //     runs per row stream faster: a probe of this one-workgroup-per-CU ring
 //     reads 136-byte row pieces at 4.6 TB/s, 272-byte ones at 5.5;
-//   * activations: the pass's 32 rows x KC fp16, rows one pad granule
+//   * activations: the pass's M rows x KC fp16 (M = 16 or 32, the pass
+//     size the launch was grouped with), rows one pad granule
 //     longer than their data, so the MFMA operand reads of 16 rows hit 16
 //     different 16-byte slots of a 256-byte bank cycle;
 //   * the activations' power-of-two scales of the stage (one dword per row
@@ -70,10 +71,12 @@ WM_DEV int pf_exp(float m) {
     return max(E - 15, -126);
 }
 
-// Expert passes: a pass is up to GM_M pairs of one expert, described by a
-// record of GM_REC ints: expert (E = shared), pair count, 0, 0, GM_M pair ids
-// (positions past the count repeat the last id), then the x scale exponents
-// of the pairs' tokens, 4 signed bytes per int.
+// Expert passes: a pass is up to M pairs of one expert (M = 16 or 32, one
+// value per launch), described by a record of GM_REC ints: expert (E =
+// shared), pair count, 0, 0, GM_M pair ids (positions past the count repeat
+// the last id), then the x scale exponents of the pairs' tokens, 4 signed
+// bytes per int, for GM_M pairs.  The record layout is the same for both pass
+// sizes.
 constexpr int GM_M = 32;
 constexpr int GM_REC = 64;
 
@@ -91,7 +94,20 @@ constexpr int gm_granules(int wt) {
     return wt == Q8_0 ? 17 : wt == Q4_K ? 9 : wt == Q5_K ? 11 : wt == Q2_K ? 7 : wt == Q3_K ? 9 : 15;
 }
 
-template <int NMAT, int AHL, int NSUB, int WT> struct GmGeo {
+// LDS bytes of a GEMM's layout (GmGeo) with an s-stage weight ring and
+// passes of m pairs.
+constexpr int gm_lds(int nmat, int ahl, int nsub, int wt, int m, int s) {
+    const bool gu = ahl == 1;
+    const int w = nmat * GM_ROWS * 16 * gm_granules(wt);
+    const int a_slot = ahl * ((m * (GM_KC / 8 + 1) + 63) / 64) * 1024 + 256;
+    const int nas = (s - 1 + nsub - 1) / nsub + 1;
+    return s * w + nas * a_slot + GM_DESC * GM_REC * 4 +
+           (gu ? m * GM_CW * 4 + m * GM_ROWS * 4 + m * 4 : 16 * GM_ROWS * 4);
+}
+
+template <int NMAT, int AHL, int NSUB, int WT, int M> struct GmGeo {
+    static_assert(M == 16 || M == 32, "pass size");
+    static constexpr int MT = M / 16;                                   // row tiles of 16 pairs
     static constexpr bool KQ = WT != Q8_0;
     static constexpr bool GU = AHL == 1;                                // gate/up (else down)
     static constexpr bool SPLIT = GU && NMAT == 1;                      // gate and up in alternate stages
@@ -104,9 +120,11 @@ template <int NMAT, int AHL, int NSUB, int WT> struct GmGeo {
     static constexpr int RSLOT = 16 * GR;                               // LDS bytes of a row's chunk
     static constexpr int GPR = KC / 8 + 1;                              // activation granules per row (+ pad)
     static constexpr int ALD = 16 * GPR;
-    static constexpr int NAU = (GM_M * GPR + 63) / 64;                  // DMA units per activation array
+    static constexpr int NAU = (M * GPR + 63) / 64;                     // DMA units per activation array
     static constexpr int APART = NAU * 1024;
-    static constexpr int S = SPLIT ? 3 : 2;                             // weight ring stages
+    // weight ring stages: one more where 16-pair passes leave the LDS for it
+    static constexpr int S0 = SPLIT ? 3 : 2;
+    static constexpr int S = M == 16 && gm_lds(NMAT, AHL, NSUB, WT, M, S0 + 1) <= 163840 ? S0 + 1 : S0;
     static constexpr int W_BYTES = NMAT * GM_ROWS * RSLOT;
     static constexpr int A_BYTES = AHL * APART;
     static constexpr int A_SLOT = A_BYTES + 256;                        // + 64 scale dwords
@@ -114,18 +132,18 @@ template <int NMAT, int AHL, int NSUB, int WT> struct GmGeo {
     static constexpr int NAS = (S - 1 + NSUB - 1) / NSUB + 1;
     static constexpr int ABASE = S * W_BYTES;
     static constexpr int DESC = ABASE + NAS * A_SLOT;
-    static constexpr int RED = DESC + GM_DESC * GM_REC * 4;             // [32 pairs][8 waves] maxima
-    static constexpr int STG = RED + (GU ? GM_M * GM_CW * 4 : 0);
-    // staging: gate/up 32 pairs x 128 rows of fp16 hi and lo + 32 scales;
+    static constexpr int RED = DESC + GM_DESC * GM_REC * 4;             // [M pairs][8 waves] maxima
+    static constexpr int STG = RED + (GU ? M * GM_CW * 4 : 0);
+    // staging: gate/up M pairs x 128 rows of fp16 hi and lo + M scales;
     // down 16 pairs x 128 rows of fp32 (the halves of a pass pass through in turn)
-    static constexpr int LDS = STG + (GU ? GM_M * GM_ROWS * 4 + GM_M * 4 : 16 * GM_ROWS * 4);
+    static constexpr int LDS = STG + (GU ? M * GM_ROWS * 4 + M * 4 : 16 * GM_ROWS * 4);
     static constexpr int NW = NMAT * GM_ROWS * GR / 64;                 // weight DMA instructions per stage
     static constexpr int NWT = (NW + GM_CW - 1) / GM_CW;
     static constexpr int NA = AHL * NAU;                                // activation DMA instructions per column step
     static constexpr int NAT = (NA + GM_CW - 1) / GM_CW;
     static_assert(NAS * NSUB >= NSUB + S - 1, "activation slot reuse");
     static_assert(GM_ROWS * GR % 64 == 0, "weight DMA units");
-    static_assert(LDS <= 163840, "LDS");
+    static_assert(LDS <= 163840 && LDS == gm_lds(NMAT, AHL, NSUB, WT, M, S), "LDS");
     static_assert(GM_M * (KC / 128) <= 64, "activation scale dwords");
 };
 
@@ -471,10 +489,10 @@ template <> struct KqRow<Q8_0> {
 // blocks in turn (one ring stage each).  WT: the weight format of every matrix the
 // launch reads (a.sel picks the routed or the shared passes when the two
 // differ).
-template <int NMAT, int AHL, int NSUB, int WT>
+template <int NMAT, int AHL, int NSUB, int WT, int M>
 __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
 #if defined(__HIP_DEVICE_COMPILE__)      // the host pass only needs the launch stub (buffer resources are device types)
-    typedef GmGeo<NMAT, AHL, NSUB, WT> G;
+    typedef GmGeo<NMAT, AHL, NSUB, WT, M> G;
     typedef KqRow<WT> F;
     constexpr bool KQ = G::KQ;
     constexpr int S = G::S;
@@ -560,11 +578,11 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
         }
         // activation instruction u = wave + 8 t: array u / NAU, LDS granules
         // 64 (u % NAU) + lane = GPR m + jj of the array (jj = GPR - 1: pad;
-        // m >= 32: slack), loaded from granule min(jj, GPR - 2) of pass row
-        // min(m, 31)
+        // m >= M: slack), loaded from granule min(jj, GPR - 2) of pass row
+        // min(m, M - 1)
 #pragma unroll
         for (int t = 0; t < G::NAT; t++) {
-            const int p = 64 * ((wave + GM_CW * t) % G::NAU) + lane, m = min(p / G::GPR, GM_M - 1),
+            const int p = 64 * ((wave + GM_CW * t) % G::NAU) + lane, m = min(p / G::GPR, M - 1),
                       jj = min(p % G::GPR, G::GPR - 2);
             const int pa = rec[4 + m], ra = a.by_token ? pair_token(pa, a.T, a.K) : pa;
             iao[t] = (uint32_t)ra * (uint32_t)a.a_ld * 2u + 16u * (uint32_t)jj;
@@ -813,7 +831,7 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
         constexpr int SUB = decltype(sub_tag)::value;
         const f32x4* scp = (const f32x4*)(gsm + G::ABASE + as * G::A_SLOT + G::A_BYTES);
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++) {
+        for (int mt = 0; mt < G::MT; mt++) {
 #pragma unroll
             for (int mat = 0; mat < NMAT; mat++) {
                 f32x4 r = acc[SUB][0][mat][mt];
@@ -849,10 +867,10 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
         const int32_t* rec = desc + (i % GM_DESC) * GM_REC;
         const int mn = rec[1];
         const uint8_t* sh = gsm + G::STG;
-        const uint8_t* sl = sh + GM_M * GM_ROWS * 2;
-        const float* ss = (const float*)(sl + GM_M * GM_ROWS * 2);
+        const uint8_t* sl = sh + M * GM_ROWS * 2;
+        const float* ss = (const float*)(sl + M * GM_ROWS * 2);
 #pragma unroll
-        for (int it = 0; it < GM_M / 4; it++) {
+        for (int it = 0; it < M / 4; it++) {
             const int m = 4 * it + (lane >> 4), seg = lane & 15;
             if (m < mn) {
                 const int64_t o = (int64_t)rec[4 + m] * a.o_ld + rb * GM_ROWS;
@@ -926,7 +944,7 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
             ++sigma;
         };
         for (;;) {
-            if (ckc == 0) two = __builtin_amdgcn_readfirstlane(desc[(ci % GM_DESC) * GM_REC + 1]) > 16;
+            if (ckc == 0) two = M > 16 && __builtin_amdgcn_readfirstlane(desc[(ci % GM_DESC) * GM_REC + 1]) > 16;
             stage(std::integral_constant<int, 0>{});
             if constexpr (NSUB > 1) stage(std::integral_constant<int, 1>{});
             if constexpr (NSUB > 2) stage(std::integral_constant<int, 2>{});
@@ -944,10 +962,10 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                 float* red = (float*)(gsm + G::RED);
                 if constexpr (!SW) {
                     const uint32_t xw = (uint32_t)desc[(ci % GM_DESC) * GM_REC + 4 + GM_M + g];   // rows 4g..4g+3
-                    const uint32_t xw1 = (uint32_t)desc[(ci % GM_DESC) * GM_REC + 4 + GM_M + 4 + g];
+                    const uint32_t xw1 = M > 16 ? (uint32_t)desc[(ci % GM_DESC) * GM_REC + 4 + GM_M + 4 + g] : 0u;
                     float* redp = red + 4 * g * GM_CW + wave;
 #pragma unroll
-                    for (int mt = 0; mt < 2; mt++)
+                    for (int mt = 0; mt < G::MT; mt++)
 #pragma unroll
                         for (int i = 0; i < 4; i++) {
                             const int xe = (int)(int8_t)((mt ? xw1 : xw) >> (8 * i));
@@ -967,18 +985,18 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                 gm_bar();
                 if constexpr (!SW) {
                     uint16_t* shp = (uint16_t*)(gsm + G::STG) + 4 * g * GM_ROWS + 16 * wave + c;
-                    uint16_t* slp = shp + GM_M * GM_ROWS;
-                    float* ss = (float*)(gsm + G::STG + GM_M * GM_ROWS * 4);
+                    uint16_t* slp = shp + M * GM_ROWS;
+                    float* ss = (float*)(gsm + G::STG + M * GM_ROWS * 4);
                     const float* redr = red + 4 * g * GM_CW;
 #pragma unroll
-                    for (int mt = 0; mt < 2; mt++)
+                    for (int mt = 0; mt < G::MT; mt++)
 #pragma unroll
                         for (int i = 0; i < 4; i++) {
                             const int o = 16 * mt + i;
                             const f32x4 r0 = *(const f32x4*)(redr + o * GM_CW), r1 = *(const f32x4*)(redr + o * GM_CW + 4);
-                            const float M = fmaxf(fmaxf(fmaxf(r0[0], r0[1]), fmaxf(r0[2], r0[3])),
-                                                  fmaxf(fmaxf(r1[0], r1[1]), fmaxf(r1[2], r1[3])));
-                            const int e = pf_exp(M);
+                            const float mx = fmaxf(fmaxf(fmaxf(r0[0], r0[1]), fmaxf(r0[2], r0[3])),
+                                                   fmaxf(fmaxf(r1[0], r1[1]), fmaxf(r1[2], r1[3])));
+                            const int e = pf_exp(mx);
                             const float v = av[mt][i] * ldexpf(1.0f, -e);
                             const _Float16 hv = (_Float16)v;
                             const _Float16 lv = (_Float16)(v - (float)hv);
@@ -1037,18 +1055,18 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
 }
 
 
-template <int NMAT, int AHL, int NSUB, int WT> int launch_pf_gemm(const PfGemm& g, int n_wg, hipStream_t s) {
-    typedef GmGeo<NMAT, AHL, NSUB, WT> G;
-    hipError_t e = hipFuncSetAttribute((const void*)k_pf_gemm<NMAT, AHL, NSUB, WT>,
+template <int NMAT, int AHL, int NSUB, int WT, int M> int launch_pf_gemm(const PfGemm& g, int n_wg, hipStream_t s) {
+    typedef GmGeo<NMAT, AHL, NSUB, WT, M> G;
+    hipError_t e = hipFuncSetAttribute((const void*)k_pf_gemm<NMAT, AHL, NSUB, WT, M>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS);
     if (e != hipSuccess) return (int)e;
-    hipLaunchKernelGGL((k_pf_gemm<NMAT, AHL, NSUB, WT>), dim3(n_wg), dim3(GM_THREADS), G::LDS, s, g);
+    hipLaunchKernelGGL((k_pf_gemm<NMAT, AHL, NSUB, WT, M>), dim3(n_wg), dim3(GM_THREADS), G::LDS, s, g);
     return (int)hipGetLastError();
 }
 
 // The K-quant instances (wm_prefill_kq.hip): gate/up (nmat = 2) and down
-// (nmat = 1, nsub = 2 or 4) of Q2_K .. Q6_K.  Returns hipErrorInvalidValue
-// for another combination.
-int launch_pf_gemm_kq(int nmat, int nsub, int wt, const PfGemm& g, int n_wg, hipStream_t s);
+// (nmat = 1, nsub = 2 or 4) of Q2_K .. Q6_K, for passes of m = 16 or 32
+// pairs.  Returns hipErrorInvalidValue for another combination.
+int launch_pf_gemm_kq(int m, int nmat, int nsub, int wt, const PfGemm& g, int n_wg, hipStream_t s);
 
 }  // namespace wm

@@ -30,7 +30,7 @@ struct PrefillArgs {
     int32_t* status;
     int32_t* offsets;           // [E + 2]: pairs of expert e are sorted[offsets[e] .. offsets[e + 1]); shared: [E] .. [E + 1]
     int32_t* sorted;            // [T * K + T] pair indices grouped by expert
-    int32_t* passes;            // [prefill_max_passes][64] pass records (up to 32 pairs of one expert)
+    int32_t* passes;            // [prefill_max_passes][64] pass records (up to pass_m pairs of one expert)
     int32_t* pass_count;        // [2]: routed passes, shared passes
     uint16_t* x16;              // fp16 [T][H]: x * 2^-e per token
     int32_t* xexp;              // [T]: e
@@ -42,10 +42,17 @@ struct PrefillArgs {
     float* sg;                  // [T] shared-expert gate
     float* out;                 // [T][H]
     int32_t n_wg;               // workgroups of the persistent expert GEMMs (one per CU)
+    int32_t pass_m;             // pairs per pass: 16 or 32 (prefill_pass_size)
 };
 
-// Pass records a prefill of T tokens may need.
-inline int64_t prefill_max_passes(int64_t T, int64_t K, int64_t E) { return (T * K + 31) / 32 + E + (T + 31) / 32 + 1; }
+// Pass records a prefill of T tokens may need (passes of 16 pairs or more).
+inline int64_t prefill_max_passes(int64_t T, int64_t K, int64_t E) { return (T * K + 15) / 16 + E + (T + 15) / 16 + 1; }
+
+// Pairs per pass: 16 when the batch averages at most 4 pairs per routed
+// expert (its passes then rarely hold more than 16, and the GEMMs' smaller
+// activation slots leave LDS for a deeper weight ring), else 32 (a pass
+// streams its expert's rows once for up to 32 tokens).
+inline int prefill_pass_size(int64_t T, int64_t K, int64_t E) { return T * K <= 4 * E ? 16 : 32; }
 
 // Weight formats the expert GEMMs read: gate and up (one format for both) and down.
 inline bool prefill_type(int t) { return t == Q8_0 || t == Q2_K || t == Q3_K || t == Q4_K || t == Q5_K || t == Q6_K; }

@@ -9,8 +9,9 @@
 //                  tokens x 16 experts, each lane one of the 16 FMA chains of
 //                  4 x 4 (token, expert) pairs)
 //   k_pf_topk      one wave per token: K-pass arg-max + softmax
-//   k_pf_group     counting sort of the pairs by expert; passes of <= 32
-//                  pairs of one expert
+//   k_pf_group     counting sort of the pairs by expert; passes of <= 16
+//                  or 32 pairs of one expert (16 when a batch averages at
+//                  most 4 pairs per expert)
 //   k_pf_xpack     x as fp16 times a power of two per token
 //   k_pf_gemm      gate and up + SwiGLU on fp16 MFMA, persistent: one
 //                  workgroup per CU streams (pass, 128-row block) items
@@ -262,10 +263,11 @@ constexpr int PG_REG = 8, PG_SORT = 10240, PG_XEXP = 2048;
 
 // One workgroup: pairs grouped by expert (order inside an expert is free:
 // every pair's output row is computed independently of the others), then
-// cut into pass records: routed passes first, in expert order, then the
-// shared expert's; pass_count = {routed passes, shared passes}.  A record
-// also carries the x scale of each pair's token.
+// cut into pass records of at most pm pairs (16 or 32): routed passes first,
+// in expert order, then the shared expert's; pass_count = {routed passes,
+// shared passes}.  A record also carries the x scale of each pair's token.
 __global__ __launch_bounds__(1024) void k_pf_group(const int32_t* __restrict__ ids, int T, int K, int E, int has_shared,
+                                                   int pm,
                                                    int32_t* __restrict__ offsets, int32_t* __restrict__ sorted,
                                                    int32_t* __restrict__ passes, int32_t* __restrict__ pass_count,
                                                    const int32_t* __restrict__ xexp) {
@@ -303,7 +305,7 @@ __global__ __launch_bounds__(1024) void k_pf_group(const int32_t* __restrict__ i
         const int e = base + tid;
         const int n = e < G ? cnt[e] : 0;
         int2 tot;
-        const int2 ex = block_excl_scan2(make_int2(n, (n + GM_M - 1) / GM_M), wsum, &tot);
+        const int2 ex = block_excl_scan2(make_int2(n, (n + pm - 1) / pm), wsum, &tot);
         if (e < G) {
             off[e] = carry.x + ex.x;
             pbase[e] = carry.y + ex.y;
@@ -358,8 +360,8 @@ __global__ __launch_bounds__(1024) void k_pf_group(const int32_t* __restrict__ i
             if (pbase[mid] <= q) lo = mid;
             else hi = mid - 1;
         }
-        const int e = lo, first = off[e] + (q - pbase[e]) * GM_M;
-        const int mn = min(GM_M, off[e + 1] - first);
+        const int e = lo, first = off[e] + (q - pbase[e]) * pm;
+        const int mn = min(pm, off[e + 1] - first);
         int32_t* rec = passes + (int64_t)q * GM_REC;
         rec[0] = e;
         rec[1] = mn;
@@ -507,31 +509,35 @@ int launch_prefill_route(const PrefillArgs& a, const int32_t* forced_ids, const 
                            a.w, a.hits, a.status);
     }
     hipLaunchKernelGGL(k_pf_xpack, dim3(a.T), dim3(256), 0, s, a.x, a.H, a.x16, a.xexp);
-    hipLaunchKernelGGL(k_pf_group, dim3(1), dim3(1024), 0, s, a.ids, a.T, a.K, a.E, a.has_shared, a.offsets, a.sorted,
-                       a.passes, a.pass_count, a.xexp);
+    hipLaunchKernelGGL(k_pf_group, dim3(1), dim3(1024), 0, s, a.ids, a.T, a.K, a.E, a.has_shared, a.pass_m, a.offsets,
+                       a.sorted, a.passes, a.pass_count, a.xexp);
     if (a.has_shared && a.sh_gate_inp)
         hipLaunchKernelGGL(k_pf_shgate, dim3(a.T), dim3(256), 0, s, a.x, a.sh_gate_inp, a.H, a.sg);
     return (int)hipGetLastError();
 }
 
-// One gate/up or down GEMM launch of format wt over the passes sel selects.
-static int launch_fmt(int nmat, int nsub, int wt, const PfGemm& g, int n_wg, hipStream_t s) {
-    if (wt != Q8_0) return launch_pf_gemm_kq(nmat, nsub, wt, g, n_wg, s);
-    if (nmat == 2) return launch_pf_gemm<1, 1, 2, Q8_0>(g, n_wg, s);     // gate and up in alternate stages
-    return nsub == 4 ? launch_pf_gemm<1, 2, 4, Q8_0>(g, n_wg, s) : launch_pf_gemm<1, 2, 2, Q8_0>(g, n_wg, s);
+// One gate/up or down GEMM launch of format wt over the passes sel selects,
+// for passes of m pairs.
+template <int M> static int launch_q8(int nmat, int nsub, const PfGemm& g, int n_wg, hipStream_t s) {
+    if (nmat == 2) return launch_pf_gemm<1, 1, 2, Q8_0, M>(g, n_wg, s);     // gate and up in alternate stages
+    return nsub == 4 ? launch_pf_gemm<1, 2, 4, Q8_0, M>(g, n_wg, s) : launch_pf_gemm<1, 2, 2, Q8_0, M>(g, n_wg, s);
+}
+static int launch_fmt(int m, int nmat, int nsub, int wt, const PfGemm& g, int n_wg, hipStream_t s) {
+    if (wt != Q8_0) return launch_pf_gemm_kq(m, nmat, nsub, wt, g, n_wg, s);
+    return m == 16 ? launch_q8<16>(nmat, nsub, g, n_wg, s) : launch_q8<32>(nmat, nsub, g, n_wg, s);
 }
 
 // Routed and shared passes in one launch when their formats agree, else in two.
-static int launch_split(int nmat, int nsub, int wt_r, int wt_s, bool has_shared, PfGemm& g, int n_wg,
+static int launch_split(int m, int nmat, int nsub, int wt_r, int wt_s, bool has_shared, PfGemm& g, int n_wg,
                         hipStream_t s) {
     if (!has_shared || wt_r == wt_s) {
         g.sel = 0;
-        return launch_fmt(nmat, nsub, wt_r, g, n_wg, s);
+        return launch_fmt(m, nmat, nsub, wt_r, g, n_wg, s);
     }
     g.sel = 1;
-    if (int rc = launch_fmt(nmat, nsub, wt_r, g, n_wg, s)) return rc;
+    if (int rc = launch_fmt(m, nmat, nsub, wt_r, g, n_wg, s)) return rc;
     g.sel = 2;
-    return launch_fmt(nmat, nsub, wt_s, g, n_wg, s);
+    return launch_fmt(m, nmat, nsub, wt_s, g, n_wg, s);
 }
 
 int launch_prefill_gateup(const PrefillArgs& a, hipStream_t s) {
@@ -549,7 +555,7 @@ int launch_prefill_gateup(const PrefillArgs& a, hipStream_t s) {
     g.nkc_r = g.nkc_s = a.H / GM_KC;
     g.recs = a.passes; g.npass = a.pass_count;
     g.o_hi = a.act_hi; g.o_lo = a.act_lo; g.o_sc = a.act_sc; g.o_ld = a.act_stride; g.osc_ld = a.act_stride / 128;
-    return launch_split(2, 1, a.gt, a.sgt, a.has_shared, g, a.n_wg, s);
+    return launch_split(a.pass_m, 2, 1, a.gt, a.sgt, a.has_shared, g, a.n_wg, s);
 }
 
 int launch_prefill_down(const PrefillArgs& a, hipStream_t s) {
@@ -569,7 +575,7 @@ int launch_prefill_down(const PrefillArgs& a, hipStream_t s) {
     // row groups of 4 blocks of 128 rows when H allows, else of 2 (H % 256 == 0)
     const int nsub = a.H % (4 * GM_ROWS) == 0 ? 4 : 2;
     g.nrb_r = g.nrb_s = a.H / (nsub * GM_ROWS);
-    return launch_split(1, nsub, a.dt, a.sdt, a.has_shared, g, a.n_wg, s);
+    return launch_split(a.pass_m, 1, nsub, a.dt, a.sdt, a.has_shared, g, a.n_wg, s);
 }
 
 int launch_prefill_combine(const PrefillArgs& a, hipStream_t s) {

@@ -7,33 +7,39 @@
 
 namespace wm {
 
-template <int WT> static int launch_down(int nsub, const PfGemm& g, int n_wg, hipStream_t s) {
-    return nsub == 4 ? launch_pf_gemm<1, 2, 4, WT>(g, n_wg, s) : launch_pf_gemm<1, 2, 2, WT>(g, n_wg, s);
+template <int WT, int M> static int launch_down(int nsub, const PfGemm& g, int n_wg, hipStream_t s) {
+    return nsub == 4 ? launch_pf_gemm<1, 2, 4, WT, M>(g, n_wg, s) : launch_pf_gemm<1, 2, 2, WT, M>(g, n_wg, s);
 }
 
-int launch_pf_gemm_kq(int nmat, int nsub, int wt, const PfGemm& g, int n_wg, hipStream_t s) {
+template <int M> static int launch_kq(int nmat, int nsub, int wt, const PfGemm& g, int n_wg, hipStream_t s) {
     if (nmat == 2) {
         // gate and up in one stage (half the stages of alternating them, at
         // a 2-deep ring: faster for these formats); Q6_K's row slots only fit
         // as alternate gate and up stages
         switch (wt) {
-        case Q2_K: return launch_pf_gemm<2, 1, 1, Q2_K>(g, n_wg, s);
-        case Q3_K: return launch_pf_gemm<2, 1, 1, Q3_K>(g, n_wg, s);
-        case Q4_K: return launch_pf_gemm<2, 1, 1, Q4_K>(g, n_wg, s);
-        case Q5_K: return launch_pf_gemm<2, 1, 1, Q5_K>(g, n_wg, s);
-        case Q6_K: return launch_pf_gemm<1, 1, 2, Q6_K>(g, n_wg, s);
+        case Q2_K: return launch_pf_gemm<2, 1, 1, Q2_K, M>(g, n_wg, s);
+        case Q3_K: return launch_pf_gemm<2, 1, 1, Q3_K, M>(g, n_wg, s);
+        case Q4_K: return launch_pf_gemm<2, 1, 1, Q4_K, M>(g, n_wg, s);
+        case Q5_K: return launch_pf_gemm<2, 1, 1, Q5_K, M>(g, n_wg, s);
+        case Q6_K: return launch_pf_gemm<1, 1, 2, Q6_K, M>(g, n_wg, s);
         default: return (int)hipErrorInvalidValue;
         }
     }
     if (nmat != 1 || (nsub != 2 && nsub != 4)) return (int)hipErrorInvalidValue;
     switch (wt) {
-    case Q2_K: return launch_down<Q2_K>(nsub, g, n_wg, s);
-    case Q3_K: return launch_down<Q3_K>(nsub, g, n_wg, s);
-    case Q4_K: return launch_down<Q4_K>(nsub, g, n_wg, s);
-    case Q5_K: return launch_down<Q5_K>(nsub, g, n_wg, s);
-    case Q6_K: return launch_down<Q6_K>(nsub, g, n_wg, s);
+    case Q2_K: return launch_down<Q2_K, M>(nsub, g, n_wg, s);
+    case Q3_K: return launch_down<Q3_K, M>(nsub, g, n_wg, s);
+    case Q4_K: return launch_down<Q4_K, M>(nsub, g, n_wg, s);
+    case Q5_K: return launch_down<Q5_K, M>(nsub, g, n_wg, s);
+    case Q6_K: return launch_down<Q6_K, M>(nsub, g, n_wg, s);
     default: return (int)hipErrorInvalidValue;
     }
+}
+
+int launch_pf_gemm_kq(int m, int nmat, int nsub, int wt, const PfGemm& g, int n_wg, hipStream_t s) {
+    if (m == 16) return launch_kq<16>(nmat, nsub, wt, g, n_wg, s);
+    if (m == 32) return launch_kq<32>(nmat, nsub, wt, g, n_wg, s);
+    return (int)hipErrorInvalidValue;
 }
 
 }  // namespace wm
