@@ -120,7 +120,11 @@ def prefill_gateup_kernel(cfg) -> str:
     sgt = TYPE_NAMES[cfg.shared_types[0]] if cfg.shared_types else gt
     what = ("fp16 MFMA over Q8_0 blocks" if gt == "Q8_0" else
             f"fp16 MFMA over {gt} super-blocks, mins from activation sums")
-    inst = {t: ("k_pf_gemm<1,1,2,Q8_0>" if t == "Q8_0" else f"k_pf_gemm<2,1,1,{t}>") for t in (gt, sgt)}
+    # pairs per pass: 16 when the batch averages at most 10 (Q8_0) or 4 (K-quant) pairs per
+    # expert (the library's rule)
+    m = 16 if cfg.tokens * cfg.K <= (10 if gt == "Q8_0" else 4) * cfg.E else 32
+    inst = {t: (f"k_pf_gemm<1,1,2,{t},{m}>" if t in ("Q8_0", "Q6_K") else f"k_pf_gemm<2,1,1,{t},{m}>")
+            for t in (gt, sgt)}
     if sgt == gt:
         return f"{inst[gt]} (prefill gate+up+SwiGLU: {what}, LDS-DMA ring)"
     return (f"{inst[gt]} + {inst[sgt]} (prefill gate+up+SwiGLU phase: routed {gt} "

@@ -86,9 +86,10 @@ enum {
 #define WM_FLAG_SPIN_PROBE 16
 /* wm_layer_desc.flags, prefill only: the expert GEMMs take the batch's pairs
  * in passes of at most 16 (PASS16) or 32 (PASS32) pairs of one expert.  By
- * default a batch that averages at most 4 pairs per expert (T*K <= 4*E) uses
- * 16, any other 32.  The results are the same bit for bit either way; only
- * the speed differs. */
+ * default a batch that averages at most 10 pairs per expert (T*K <= 10*E)
+ * with Q8_0 gate/up, or at most 4 with K-quant gate/up, uses 16, any other
+ * 32.  The results are the same bit for bit either way; only the speed
+ * differs. */
 #define WM_FLAG_PREFILL_PASS16 32
 #define WM_FLAG_PREFILL_PASS32 64
 

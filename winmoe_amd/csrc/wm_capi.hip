@@ -1019,7 +1019,7 @@ static int run_prefill(const wm_layer_desc* d, const uint16_t* x, int T, const i
                  (WM_FLAG_PREFILL_PASS16 | WM_FLAG_PREFILL_PASS32));
     a.pass_m = (d->flags & WM_FLAG_PREFILL_PASS16)   ? 16
                : (d->flags & WM_FLAG_PREFILL_PASS32) ? 32
-                                                     : prefill_pass_size(T, a.K, a.E);
+                                                     : prefill_pass_size(T, a.K, a.E, a.gt);
     // the expert GEMMs read 16-byte granules from row starts
     WM_CHECK_ARG(al(a.gate, 16) && al(a.up, 16) && al(a.down, 16) && a.gstride % 16 == 0 && a.ustride % 16 == 0 &&
                  a.dstride % 16 == 0 && (!sh || (al(a.sh_gate, 16) && al(a.sh_up, 16) && al(a.sh_down, 16))));

@@ -10,8 +10,7 @@
 //                  4 x 4 (token, expert) pairs)
 //   k_pf_topk      one wave per token: K-pass arg-max + softmax
 //   k_pf_group     counting sort of the pairs by expert; passes of <= 16
-//                  or 32 pairs of one expert (16 when a batch averages at
-//                  most 4 pairs per expert)
+//                  or 32 pairs of one expert (prefill_pass_size)
 //   k_pf_xpack     x as fp16 times a power of two per token
 //   k_pf_gemm      gate and up + SwiGLU on fp16 MFMA, persistent: one
 //                  workgroup per CU streams (pass, 128-row block) items
