@@ -606,9 +606,13 @@ def test_prefill_c5_full(wm, orc):
 
 # K-quant experts in prefill: (gate = up, down) routed, shared or None, H.
 # Routed and shared experts of different formats run as separate GEMM
-# launches; H = 256 takes the two-block down items, 1024 the four-block ones.
+# launches; H = 256 takes the two-block down items, 1024 the four-block ones;
+# with passes of 16 pairs and H a multiple of 512, Q2_K .. Q4_K gate/up take
+# stages of two super-blocks.
 KQ_PREFILL = [
     ((Q4_K, Q6_K), (Q8_0, Q8_0), 1024),
+    ((Q3_K, Q6_K), (Q4_K, Q8_0), 512),
+    ((Q2_K, Q2_K), None, 1024),
     ((Q2_K, Q3_K), None, 256),
     ((Q5_K, Q5_K), (Q5_K, Q6_K), 1024),
     ((Q3_K, Q2_K), (Q4_K, Q4_K), 256),

@@ -8,8 +8,8 @@
 // k, k + grid, k + 2 grid, ... with k = pf_item_slot(b) (the row blocks of a
 // pass on workgroups of one XCD).  For each item it streams the block's rows (of
 // gate and up, or of down) through an S-stage LDS ring, 256 columns per
-// stage (Q8_0: 8 blocks; K-quants: one super-block), filled by
-// global_load_lds:
+// stage (Q8_0: 8 blocks; K-quants: one super-block, or two when gate and up
+// alternate with passes of 16 pairs), filled by global_load_lds:
 //   * weights: each row's stage chunk as GR granules of 16 B from the
 //     16-byte boundary at or before the row start plus the 16-byte boundary
 //     at or before the chunk's offset in the row (Q8_0 272 B, Q4_K 144 B and
@@ -85,35 +85,45 @@ constexpr int GM_CW = 8;              // compute waves
 constexpr int GM_THREADS = 64 * (GM_CW + 1);
 constexpr int GM_DESC = 8;            // pass records held in LDS
 
-// Columns per stage, every format (the launcher's column-step count is the
-// matrix width over this).
+// Columns per super-block of a stage (a stage holds NSB of them; the column
+// steps of an item are the matrix width over NSB x 256).
 constexpr int GM_KC = 256;
 
-// Granules of 16 B that hold a row's stage chunk of format WT wherever it starts.
-constexpr int gm_granules(int wt) {
-    return wt == Q8_0 ? 17 : wt == Q4_K ? 9 : wt == Q5_K ? 11 : wt == Q2_K ? 7 : wt == Q3_K ? 9 : 15;
+// Granules of 16 B that hold a row's stage chunk of format WT (nsb
+// super-blocks; Q8_0: nsb x 8 blocks) wherever it starts: the chunk plus
+// the row start's and the chunk offset's distances past a 16-byte boundary
+// (none for Q8_0, Q4_K and Q5_K, whose rows and chunks start aligned; up to
+// 12 bytes each for Q2_K, 14 for Q3_K and Q6_K).
+constexpr int gm_granules(int wt, int nsb) {
+    const int bytes = wt == Q8_0 ? nsb * 272 : nsb * block_bytes(wt);
+    const int mis = wt == Q2_K ? 12 : (wt == Q3_K || wt == Q6_K) ? 14 : 0;
+    return (bytes + 2 * mis + 15) / 16;
 }
 
-// LDS bytes of a GEMM's layout (GmGeo) with an s-stage weight ring and
-// passes of m pairs.
-constexpr int gm_lds(int nmat, int ahl, int nsub, int wt, int m, int s) {
+// LDS bytes of a GEMM's layout (GmGeo) with an s-stage weight ring, passes
+// of m pairs and stages of nsb x 256 columns.
+constexpr int gm_lds(int nmat, int ahl, int nsub, int wt, int m, int s, int nsb) {
     const bool gu = ahl == 1;
-    const int w = nmat * GM_ROWS * 16 * gm_granules(wt);
-    const int a_slot = ahl * ((m * (GM_KC / 8 + 1) + 63) / 64) * 1024 + 256;
+    const int w = nmat * GM_ROWS * 16 * gm_granules(wt, nsb);
+    const int a_slot = ahl * ((m * (nsb * GM_KC / 8 + 1) + 63) / 64) * 1024 + 256;
     const int nas = (s - 1 + nsub - 1) / nsub + 1;
     return s * w + nas * a_slot + GM_DESC * GM_REC * 4 +
            (gu ? m * GM_CW * 4 + m * GM_ROWS * 4 + m * 4 : 16 * GM_ROWS * 4);
 }
 
-template <int NMAT, int AHL, int NSUB, int WT, int M> struct GmGeo {
+// NSB: 256-column super-blocks per stage (2: a K-quant row's chunk of two
+// super-blocks, twice the run per row at the same stage size when gate and
+// up alternate).
+template <int NMAT, int AHL, int NSUB, int WT, int M, int NSB> struct GmGeo {
     static_assert(M == 16 || M == 32, "pass size");
+    static_assert(NSB == 1 || NSB == 2, "super-blocks per stage");
     static constexpr int MT = M / 16;                                   // row tiles of 16 pairs
     static constexpr bool KQ = WT != Q8_0;
     static constexpr bool GU = AHL == 1;                                // gate/up (else down)
     static constexpr bool SPLIT = GU && NMAT == 1;                      // gate and up in alternate stages
-    static constexpr int KC = GM_KC;                                    // columns per stage
-    static constexpr int CHUNK = KQ ? block_bytes(WT) : KC / 32 * 34;   // bytes of a row's stage chunk
-    static constexpr int GR = gm_granules(WT);
+    static constexpr int KC = GM_KC * NSB;                              // columns per stage
+    static constexpr int CHUNK = KQ ? NSB * block_bytes(WT) : KC / 32 * 34;   // bytes of a row's stage chunk
+    static constexpr int GR = gm_granules(WT, NSB);
     static constexpr int ROWS_ITEM = SPLIT ? GM_ROWS : NSUB * GM_ROWS;  // matrix rows per item
     static_assert(!SPLIT || NSUB == 2, "split gate/up stages");
     static_assert(KQ || GR * 16 == CHUNK, "Q8_0 chunks are whole granules");
@@ -124,7 +134,7 @@ template <int NMAT, int AHL, int NSUB, int WT, int M> struct GmGeo {
     static constexpr int APART = NAU * 1024;
     // weight ring stages: one more where 16-pair passes leave the LDS for it
     static constexpr int S0 = SPLIT ? 3 : 2;
-    static constexpr int S = M == 16 && gm_lds(NMAT, AHL, NSUB, WT, M, S0 + 1) <= 163840 ? S0 + 1 : S0;
+    static constexpr int S = M == 16 && gm_lds(NMAT, AHL, NSUB, WT, M, S0 + 1, NSB) <= 163840 ? S0 + 1 : S0;
     static constexpr int W_BYTES = NMAT * GM_ROWS * RSLOT;
     static constexpr int A_BYTES = AHL * APART;
     static constexpr int A_SLOT = A_BYTES + 256;                        // + 64 scale dwords
@@ -143,8 +153,8 @@ template <int NMAT, int AHL, int NSUB, int WT, int M> struct GmGeo {
     static constexpr int NAT = (NA + GM_CW - 1) / GM_CW;
     static_assert(NAS * NSUB >= NSUB + S - 1, "activation slot reuse");
     static_assert(GM_ROWS * GR % 64 == 0, "weight DMA units");
-    static_assert(LDS <= 163840 && LDS == gm_lds(NMAT, AHL, NSUB, WT, M, S), "LDS");
-    static_assert(GM_M * (KC / 128) <= 64, "activation scale dwords");
+    static_assert(LDS <= 163840 && LDS == gm_lds(NMAT, AHL, NSUB, WT, M, S, NSB), "LDS");
+    static_assert(GU || GM_M * (KC / 128) <= 64, "activation scale dwords");
 };
 
 static_assert(4 + GM_M + GM_M / 4 <= GM_REC, "pass record");
@@ -164,7 +174,9 @@ struct PfGemm {
     int64_t sc_ld;
     int32_t a_bytes, sc_bytes;         // sizes of the activation and scale arrays
     int32_t T, K, E, by_token;         // activation row: token of the pair (1) or the pair (0)
-    int32_t nrb_r, nrb_s, nkc_r, nkc_s;    // row groups per pass and column steps per item: routed, shared
+    int32_t nrb_r, nrb_s;              // row groups per pass: routed, shared
+    int32_t ncol_r, ncol_s;            // matrix columns: routed, shared
+    int32_t nkc_r, nkc_s;              // column steps per item (launch_pf_gemm: columns / the instance's KC)
     int32_t sel;                       // passes of this launch: 0 all, 1 routed only, 2 shared only
     const int32_t* recs;
     const int32_t* npass;              // {routed passes, shared passes}
@@ -489,10 +501,10 @@ template <> struct KqRow<Q8_0> {
 // blocks in turn (one ring stage each).  WT: the weight format of every matrix the
 // launch reads (a.sel picks the routed or the shared passes when the two
 // differ).
-template <int NMAT, int AHL, int NSUB, int WT, int M>
+template <int NMAT, int AHL, int NSUB, int WT, int M, int NSB>
 __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
 #if defined(__HIP_DEVICE_COMPILE__)      // the host pass only needs the launch stub (buffer resources are device types)
-    typedef GmGeo<NMAT, AHL, NSUB, WT, M> G;
+    typedef GmGeo<NMAT, AHL, NSUB, WT, M, NSB> G;
     typedef KqRow<WT> F;
     constexpr bool KQ = G::KQ;
     constexpr int S = G::S;
@@ -721,106 +733,112 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
                 }
             }
         } else {
-            // one super-block per row: its first byte is lsh (the row start's
-            // offset past a 16-byte boundary) plus the chunk offset's into the slot
-            const int o = lsh + ((kc * G::CHUNK) & 15);
-            const uint8_t* slot[NMAT];
-            F row[NMAT];
 #pragma unroll
-            for (int mat = 0; mat < NMAT; mat++) {
-                slot[mat] = wb + (mat * GM_ROWS + 16 * wave + c) * G::RSLOT;
-                row[mat].head(slot[mat], o);
-            }
-            if constexpr (F::FOLD) {
-                // the stage's sums of q * sc and of the mins, per 128-column
-                // half, in the MFMA accumulators; d and dmin once at the end
-                f32x4 sq[NH][NMAT][2], sm[NH][NMAT][2];
-#pragma unroll
-                for (int h = 0; h < NH; h++)
-#pragma unroll
-                    for (int mat = 0; mat < NMAT; mat++) sq[h][mat][0] = sq[h][mat][1] = sm[h][mat][0] = sm[h][mat][1] = zero;
-#pragma unroll
-                for (int b = 0; b < 8; b++) {
-                    const int hs = SCALED ? b / 4 : 0;
-                    f16x8 A[AHL][2];
-#pragma unroll
-                    for (int h = 0; h < AHL; h++)
-#pragma unroll
-                        for (int mt = 0; mt < 2; mt++)
-                            A[h][mt] = *(const f16x8*)(ab + G::APART * h + (16 * mt + c) * G::ALD + 16 * (4 * b + g));
-#pragma unroll
-                    for (int mat = 0; mat < NMAT; mat++) {
-                        f16x8 Bq, Bm;
-                        row[mat].unit(slot[mat], o, b, g, Bq, Bm);
-#pragma unroll
-                        for (int mt = 0; mt < 2; mt++) {
-                            if (mt == 1 && !TWO) continue;
-#pragma unroll
-                            for (int h = 0; h < AHL; h++)
-                                sq[hs][mat][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[h][mt], Bq, sq[hs][mat][mt], 0, 0, 0);
-                            if constexpr (F::MINS) {
-#pragma unroll
-                                for (int h = 0; h < AHL; h++)
-                                    sm[hs][mat][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[h][mt], Bm, sm[hs][mat][mt], 0, 0, 0);
-                            }
-                        }
-                    }
+            for (int sb = 0; sb < NSB; sb++) {
+                // super-block sb of each row: its first byte is lsh (the row start's
+                // offset past a 16-byte boundary) plus the chunk offset's into the
+                // slot, plus sb super-blocks; its activations 512 sb bytes into
+                // the rows
+                const int o = lsh + ((kc * G::CHUNK) & 15) + sb * block_bytes(WT);
+                const int cb = 512 * sb;
+                const uint8_t* slot[NMAT];
+                F row[NMAT];
+    #pragma unroll
+                for (int mat = 0; mat < NMAT; mat++) {
+                    slot[mat] = wb + (mat * GM_ROWS + 16 * wave + c) * G::RSLOT;
+                    row[mat].head(slot[mat], o);
                 }
-#pragma unroll
-                for (int h = 0; h < NH; h++)
-#pragma unroll
-                    for (int mat = 0; mat < NMAT; mat++)
-#pragma unroll
-                        for (int mt = 0; mt < 2; mt++) {
-                            if (mt == 1 && !TWO) continue;
-                            f32x4 r = tv[h][mat][mt];
-#pragma unroll
-                            for (int i = 0; i < 4; i++) r[i] = fmaf(row[mat].d, sq[h][mat][mt][i], r[i]);
-                            if constexpr (F::MINS) {
-#pragma unroll
-                                for (int i = 0; i < 4; i++) r[i] = fmaf(-row[mat].dmin, sm[h][mat][mt][i], r[i]);
+                if constexpr (F::FOLD) {
+                    // the stage's sums of q * sc and of the mins, per 128-column
+                    // half, in the MFMA accumulators; d and dmin once at the end
+                    f32x4 sq[NH][NMAT][2], sm[NH][NMAT][2];
+    #pragma unroll
+                    for (int h = 0; h < NH; h++)
+    #pragma unroll
+                        for (int mat = 0; mat < NMAT; mat++) sq[h][mat][0] = sq[h][mat][1] = sm[h][mat][0] = sm[h][mat][1] = zero;
+    #pragma unroll
+                    for (int b = 0; b < 8; b++) {
+                        const int hs = SCALED ? 2 * sb + b / 4 : 0;
+                        f16x8 A[AHL][2];
+    #pragma unroll
+                        for (int h = 0; h < AHL; h++)
+    #pragma unroll
+                            for (int mt = 0; mt < 2; mt++)
+                                A[h][mt] = *(const f16x8*)(ab + G::APART * h + (16 * mt + c) * G::ALD + cb + 16 * (4 * b + g));
+    #pragma unroll
+                        for (int mat = 0; mat < NMAT; mat++) {
+                            f16x8 Bq, Bm;
+                            row[mat].unit(slot[mat], o, b, g, Bq, Bm);
+    #pragma unroll
+                            for (int mt = 0; mt < 2; mt++) {
+                                if (mt == 1 && !TWO) continue;
+    #pragma unroll
+                                for (int h = 0; h < AHL; h++)
+                                    sq[hs][mat][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[h][mt], Bq, sq[hs][mat][mt], 0, 0, 0);
+                                if constexpr (F::MINS) {
+    #pragma unroll
+                                    for (int h = 0; h < AHL; h++)
+                                        sm[hs][mat][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[h][mt], Bm, sm[hs][mat][mt], 0, 0, 0);
+                                }
                             }
-                            tv[h][mat][mt] = r;
-                        }
-            } else {
-                // Q6_K: two MFMAs per unit, each over one 16-weight sub-block
-                // (the other half of the weight operand zero), times d * sc;
-                // the quantised bytes of a 128-column half are read once
-#pragma unroll
-                for (int b = 0; b < 8; b++) {
-                    const int hs = SCALED ? b / 4 : 0;
-                    if ((b & 3) == 0) {
-#pragma unroll
-                        for (int mat = 0; mat < NMAT; mat++) row[mat].half(slot[mat], o, b >> 2, g);
-                    }
-                    f16x8 A[AHL][2];
-#pragma unroll
-                    for (int h = 0; h < AHL; h++)
-#pragma unroll
-                        for (int mt = 0; mt < 2; mt++)
-                            A[h][mt] = *(const f16x8*)(ab + G::APART * h + (16 * mt + c) * G::ALD + 16 * (4 * b + g));
-#pragma unroll
-                    for (int mat = 0; mat < NMAT; mat++) {
-                        float am[2];
-                        const f16x8 Bv = row[mat].unit(b >> 2, b & 3, am);
-                        const f16x8 B[2] = {half_of(Bv, 0), half_of(Bv, 1)};
-#pragma unroll
-                        for (int mt = 0; mt < 2; mt++) {
-                            if (mt == 1 && !TWO) continue;
-                            f32x4 r = tv[hs][mat][mt];
-#pragma unroll
-                            for (int hv = 0; hv < 2; hv++) {
-                                f32x4 P = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0][mt], B[hv], zero, 0, 0, 0);
-                                if constexpr (AHL == 2) P = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1][mt], B[hv], P, 0, 0, 0);
-#pragma unroll
-                                for (int i = 0; i < 4; i++) r[i] = fmaf(am[hv], P[i], r[i]);
-                            }
-                            tv[hs][mat][mt] = r;
                         }
                     }
-                    // one unit's operands live at a time (fewer registers than
-                    // letting the scheduler hoist the next units' LDS reads)
-                    __builtin_amdgcn_sched_barrier(0);
+    #pragma unroll
+                    for (int h = 0; h < NH; h++)
+    #pragma unroll
+                        for (int mat = 0; mat < NMAT; mat++)
+    #pragma unroll
+                            for (int mt = 0; mt < 2; mt++) {
+                                if (mt == 1 && !TWO) continue;
+                                f32x4 r = tv[h][mat][mt];
+    #pragma unroll
+                                for (int i = 0; i < 4; i++) r[i] = fmaf(row[mat].d, sq[h][mat][mt][i], r[i]);
+                                if constexpr (F::MINS) {
+    #pragma unroll
+                                    for (int i = 0; i < 4; i++) r[i] = fmaf(-row[mat].dmin, sm[h][mat][mt][i], r[i]);
+                                }
+                                tv[h][mat][mt] = r;
+                            }
+                } else {
+                    // Q6_K: two MFMAs per unit, each over one 16-weight sub-block
+                    // (the other half of the weight operand zero), times d * sc;
+                    // the quantised bytes of a 128-column half are read once
+    #pragma unroll
+                    for (int b = 0; b < 8; b++) {
+                        const int hs = SCALED ? 2 * sb + b / 4 : 0;
+                        if ((b & 3) == 0) {
+    #pragma unroll
+                            for (int mat = 0; mat < NMAT; mat++) row[mat].half(slot[mat], o, b >> 2, g);
+                        }
+                        f16x8 A[AHL][2];
+    #pragma unroll
+                        for (int h = 0; h < AHL; h++)
+    #pragma unroll
+                            for (int mt = 0; mt < 2; mt++)
+                                A[h][mt] = *(const f16x8*)(ab + G::APART * h + (16 * mt + c) * G::ALD + cb + 16 * (4 * b + g));
+    #pragma unroll
+                        for (int mat = 0; mat < NMAT; mat++) {
+                            float am[2];
+                            const f16x8 Bv = row[mat].unit(b >> 2, b & 3, am);
+                            const f16x8 B[2] = {half_of(Bv, 0), half_of(Bv, 1)};
+    #pragma unroll
+                            for (int mt = 0; mt < 2; mt++) {
+                                if (mt == 1 && !TWO) continue;
+                                f32x4 r = tv[hs][mat][mt];
+    #pragma unroll
+                                for (int hv = 0; hv < 2; hv++) {
+                                    f32x4 P = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0][mt], B[hv], zero, 0, 0, 0);
+                                    if constexpr (AHL == 2) P = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1][mt], B[hv], P, 0, 0, 0);
+    #pragma unroll
+                                    for (int i = 0; i < 4; i++) r[i] = fmaf(am[hv], P[i], r[i]);
+                                }
+                                tv[hs][mat][mt] = r;
+                            }
+                        }
+                        // one unit's operands live at a time (fewer registers than
+                        // letting the scheduler hoist the next units' LDS reads)
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
                 }
             }
         }
@@ -1055,12 +1073,17 @@ __global__ __launch_bounds__(GM_THREADS) void k_pf_gemm(PfGemm a) {
 }
 
 
-template <int NMAT, int AHL, int NSUB, int WT, int M> int launch_pf_gemm(const PfGemm& g, int n_wg, hipStream_t s) {
-    typedef GmGeo<NMAT, AHL, NSUB, WT, M> G;
-    hipError_t e = hipFuncSetAttribute((const void*)k_pf_gemm<NMAT, AHL, NSUB, WT, M>,
+template <int NMAT, int AHL, int NSUB, int WT, int M, int NSB = 1>
+int launch_pf_gemm(const PfGemm& g, int n_wg, hipStream_t s) {
+    typedef GmGeo<NMAT, AHL, NSUB, WT, M, NSB> G;
+    if (g.ncol_r % G::KC || g.ncol_s % G::KC) return (int)hipErrorInvalidValue;
+    PfGemm h = g;
+    h.nkc_r = g.ncol_r / G::KC;
+    h.nkc_s = g.ncol_s / G::KC;
+    hipError_t e = hipFuncSetAttribute((const void*)k_pf_gemm<NMAT, AHL, NSUB, WT, M, NSB>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS);
     if (e != hipSuccess) return (int)e;
-    hipLaunchKernelGGL((k_pf_gemm<NMAT, AHL, NSUB, WT, M>), dim3(n_wg), dim3(GM_THREADS), G::LDS, s, g);
+    hipLaunchKernelGGL((k_pf_gemm<NMAT, AHL, NSUB, WT, M, NSB>), dim3(n_wg), dim3(GM_THREADS), G::LDS, s, h);
     return (int)hipGetLastError();
 }
 

@@ -551,7 +551,7 @@ int launch_prefill_gateup(const PrefillArgs& a, hipStream_t s) {
     g.a_bytes = (int32_t)((int64_t)a.T * a.H * 2); g.sc_bytes = 0;
     g.T = a.T; g.K = a.K; g.E = a.E; g.by_token = 1;
     g.nrb_r = a.I / GM_ROWS; g.nrb_s = a.has_shared ? a.Is / GM_ROWS : 1;
-    g.nkc_r = g.nkc_s = a.H / GM_KC;
+    g.ncol_r = g.ncol_s = a.H;
     g.recs = a.passes; g.npass = a.pass_count;
     g.o_hi = a.act_hi; g.o_lo = a.act_lo; g.o_sc = a.act_sc; g.o_ld = a.act_stride; g.osc_ld = a.act_stride / 128;
     return launch_split(a.pass_m, 2, 1, a.gt, a.sgt, a.has_shared, g, a.n_wg, s);
@@ -568,7 +568,7 @@ int launch_prefill_down(const PrefillArgs& a, hipStream_t s) {
     const int64_t pairs = (int64_t)a.T * a.K + (a.has_shared ? a.T : 0);
     g.a_bytes = (int32_t)(pairs * a.act_stride * 2); g.sc_bytes = (int32_t)(pairs * (a.act_stride / 128) * 4);
     g.T = a.T; g.K = a.K; g.E = a.E; g.by_token = 0;
-    g.nkc_r = a.I / GM_KC; g.nkc_s = a.has_shared ? a.Is / GM_KC : g.nkc_r;
+    g.ncol_r = a.I; g.ncol_s = a.has_shared ? a.Is : g.ncol_r;
     g.recs = a.passes; g.npass = a.pass_count;
     g.y = a.y; g.y_ld = a.H;
     // row groups of 4 blocks of 128 rows when H allows, else of 2 (H % 256 == 0)

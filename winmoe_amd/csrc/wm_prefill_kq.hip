@@ -12,6 +12,19 @@ template <int WT, int M> static int launch_down(int nsub, const PfGemm& g, int n
 }
 
 template <int M> static int launch_kq(int nmat, int nsub, int wt, const PfGemm& g, int n_wg, hipStream_t s) {
+    if constexpr (M == 16) {
+        // with passes of 16 pairs and H a multiple of 512, Q2_K .. Q4_K run
+        // gate and up in alternate stages of two super-blocks per row: runs
+        // twice as long per row at the same stage size
+        if (nmat == 2 && g.ncol_r % 512 == 0 && g.ncol_s % 512 == 0) {
+            switch (wt) {
+            case Q2_K: return launch_pf_gemm<1, 1, 2, Q2_K, 16, 2>(g, n_wg, s);
+            case Q3_K: return launch_pf_gemm<1, 1, 2, Q3_K, 16, 2>(g, n_wg, s);
+            case Q4_K: return launch_pf_gemm<1, 1, 2, Q4_K, 16, 2>(g, n_wg, s);
+            default: break;
+            }
+        }
+    }
     if (nmat == 2) {
         // gate and up in one stage (half the stages of alternating them, at
         // a 2-deep ring: faster for these formats); Q6_K's row slots only fit
