@@ -121,10 +121,14 @@ def prefill_gateup_kernel(cfg) -> str:
     what = ("fp16 MFMA over Q8_0 blocks" if gt == "Q8_0" else
             f"fp16 MFMA over {gt} super-blocks, mins from activation sums")
     # pairs per pass: 16 when the batch averages at most 10 (Q8_0) or 4 (K-quant) pairs per
-    # expert (the library's rule)
+    # expert; then Q2_K .. Q4_K stream two super-blocks per stage when H allows (the library's rules)
     m = 16 if cfg.tokens * cfg.K <= (10 if gt == "Q8_0" else 4) * cfg.E else 32
-    inst = {t: (f"k_pf_gemm<1,1,2,{t},{m}>" if t in ("Q8_0", "Q6_K") else f"k_pf_gemm<2,1,1,{t},{m}>")
-            for t in (gt, sgt)}
+
+    def inst_name(t):
+        if m == 16 and t in ("Q2_K", "Q3_K", "Q4_K") and cfg.H % 512 == 0:
+            return f"k_pf_gemm<1,1,2,{t},16,2>"
+        return f"k_pf_gemm<1,1,2,{t},{m},1>" if t in ("Q8_0", "Q6_K") else f"k_pf_gemm<2,1,1,{t},{m},1>"
+    inst = {t: inst_name(t) for t in (gt, sgt)}
     if sgt == gt:
         return f"{inst[gt]} (prefill gate+up+SwiGLU: {what}, LDS-DMA ring)"
     return (f"{inst[gt]} + {inst[sgt]} (prefill gate+up+SwiGLU phase: routed {gt} "

@@ -89,15 +89,20 @@ constexpr int GM_DESC = 8;            // pass records held in LDS
 // steps of an item are the matrix width over NSB x 256).
 constexpr int GM_KC = 256;
 
-// Granules of 16 B that hold a row's stage chunk of format WT (nsb
-// super-blocks; Q8_0: nsb x 8 blocks) wherever it starts: the chunk plus
-// the row start's and the chunk offset's distances past a 16-byte boundary
-// (none for Q8_0, Q4_K and Q5_K, whose rows and chunks start aligned; up to
-// 12 bytes each for Q2_K, 14 for Q3_K and Q6_K).
+// Granules of 16 B loaded per row and stage for format WT (nsb
+// super-blocks; Q8_0: nsb x 8 blocks): enough to hold the chunk wherever it
+// starts (the chunk plus the row start's and the chunk offset's distances
+// past a 16-byte boundary: none for Q8_0, Q4_K and Q5_K, whose rows and
+// chunks start aligned; up to 12 bytes each for Q2_K, 14 for Q3_K and Q6_K),
+// rounded up to an odd count.  A row's LDS slot is then an odd multiple of
+// 4 dwords long, so the slots of 16 consecutive rows start on 16 different
+// groups of 4 banks (of 64) and the 8-byte reads of half a wave (16 rows x
+// 2 lanes) hit 64 different banks; with an even count rows 8 apart, or
+// closer, shared banks.
 constexpr int gm_granules(int wt, int nsb) {
     const int bytes = wt == Q8_0 ? nsb * 272 : nsb * block_bytes(wt);
     const int mis = wt == Q2_K ? 12 : (wt == Q3_K || wt == Q6_K) ? 14 : 0;
-    return (bytes + 2 * mis + 15) / 16;
+    return ((bytes + 2 * mis + 15) / 16) | 1;
 }
 
 // LDS bytes of a GEMM's layout (GmGeo) with an s-stage weight ring, passes
