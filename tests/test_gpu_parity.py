@@ -549,7 +549,7 @@ def test_prefill_rejects_two_pass_sizes(wm):
     ids = np.tile(np.arange(4, dtype=np.int32), (8, 1))
     w = np.full((8, 4), 0.25, np.float32)
     with pytest.raises(wm.WinMoEError) as ei:
-        _prefill_pass16(sl, X, ids, w, flag=_lib.FLAG_PREFILL_PASS16 | _lib.FLAG_PREFILL_PASS32)
+        _prefill_flags(sl, X, ids, w, _lib.FLAG_PREFILL_PASS16 | _lib.FLAG_PREFILL_PASS32)
     assert ei.value.rc == _lib.WM_EINVAL
 
 
@@ -589,8 +589,8 @@ def test_prefill_c5_full(wm, orc):
     case("prefill c5 full")
     out = host(sl.layer.prefill_forced(X, dev(ids), dev(w)))
     assert np.isfinite(out).all()
-    case("prefill c5 full, passes of 16 pairs")
-    assert np.array_equal(out.view(np.uint32), _prefill_pass16(sl, X, ids, w).view(np.uint32))
+    case("prefill c5 full, passes of 16 and of 32 pairs")
+    _check_pass_sizes(sl, X, ids, w, out)
     for t in (0, 1, 255, T - 1):
         case(f"prefill c5 oracle token={t}")
         _, _, ref = oracle_token(orc, sl, host(X[t].float()), ids=ids[t], w=w[t])
@@ -623,17 +623,25 @@ KQ_PREFILL = [
 ]
 
 
-def _prefill_pass16(sl, X, ids, w, flag=None):
-    """The same forced prefill with the pairs taken in passes of 16 (or, with
-    flag, as flag says); the layer's flags are restored."""
-    from winmoe_amd import _lib
+def _prefill_flags(sl, X, ids, w, flag):
+    """The same forced prefill with `flag` added to the layer's flags (restored
+    after)."""
     d = sl.layer.desc
     old = d.flags
-    d.flags = old | (_lib.FLAG_PREFILL_PASS16 if flag is None else flag)
+    d.flags = old | flag
     try:
         return host(sl.layer.prefill_forced(X, dev(ids), dev(w)))
     finally:
         d.flags = old
+
+
+def _check_pass_sizes(sl, X, ids, w, out):
+    """Passes of 16 and of 32 pairs give `out` (the default choice's result)
+    bit for bit."""
+    from winmoe_amd import _lib
+    for flag in (_lib.FLAG_PREFILL_PASS16, _lib.FLAG_PREFILL_PASS32):
+        other = _prefill_flags(sl, X, ids, w, flag)
+        assert np.array_equal(out.view(np.uint32), other.view(np.uint32)), flag
 
 
 def _kq_routes(T, E, K, rng):
@@ -663,8 +671,8 @@ def test_prefill_kquant_matches_oracle(wm, orc, gu, dn, sh, H):
     ids, w = _kq_routes(T, E, K, np.random.default_rng(gu * 31 + dn))
     case(f"prefill kq gate/up={gu} down={dn} shared={sh} H={H} T={T}")
     out = host(sl.layer.prefill_forced(X, dev(ids), dev(w)))
-    case(f"prefill kq gate/up={gu} down={dn} shared={sh} H={H} T={T}, passes of 16 pairs")
-    assert np.array_equal(out.view(np.uint32), _prefill_pass16(sl, X, ids, w).view(np.uint32))
+    case(f"prefill kq gate/up={gu} down={dn} shared={sh} H={H} T={T}, passes of 16 and of 32 pairs")
+    _check_pass_sizes(sl, X, ids, w, out)
     worst = 0.0
     for t in range(T):
         _, _, ref = oracle_token(orc, sl, host(X[t].float()), ids=ids[t], w=w[t])
@@ -693,10 +701,8 @@ def test_prefill_kquant_full_layer(wm, orc, name):
     again = host(sl.layer.prefill_forced(X, dev(ids), dev(w)))
     assert np.isfinite(out).all()
     assert np.array_equal(out.view(np.uint32), again.view(np.uint32))
-    from winmoe_amd import _lib
-    case(f"prefill {name} full, passes of 32 pairs")
-    p32 = _prefill_pass16(sl, X, ids, w, flag=_lib.FLAG_PREFILL_PASS32)
-    assert np.array_equal(out.view(np.uint32), p32.view(np.uint32))
+    case(f"prefill {name} full, passes of 16 and of 32 pairs")
+    _check_pass_sizes(sl, X, ids, w, out)
     for t in (0, 1, 255, T - 1):
         case(f"prefill {name} oracle token={t}")
         _, _, ref = oracle_token(orc, sl, host(X[t].float()), ids=ids[t], w=w[t])
