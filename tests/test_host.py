@@ -120,3 +120,32 @@ def test_pool_ids_checked_against_the_source(lib):
                                None, None) == _lib.WM_EINVAL
     assert lib.wm_pool_acquire_packed(None, 0, ids.ctypes.data_as(C.POINTER(C.c_int32)), 2, 4, None, 0, None,
                                       None) == _lib.WM_EINVAL
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus 2 exits with status 2 and says so,
+    before touching a device."""
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
+
+
+def test_bench_names_the_prefill_kernels_the_library_picks():
+    """The bench line's kernel names follow the library's pass-size rule (16
+    pairs up to 10 per expert for Q8_0, 4 for K-quants) and its
+    two-super-block stages for Q2_K .. Q4_K gate/up."""
+    import importlib.util
+    import sys
+    from winmoe_amd import synth
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    spec = importlib.util.spec_from_file_location("bench_mod", os.path.join(root, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    sys.modules["bench_mod"] = bench
+    spec.loader.exec_module(bench)
+    assert bench.prefill_gateup_kernel(synth.CONFIGS["c5"]).startswith("k_pf_gemm<1,1,2,Q8_0,16,1>")
+    c3p = bench.prefill_gateup_kernel(synth.CONFIGS["c3p"])
+    assert c3p.startswith("k_pf_gemm<1,1,2,Q4_K,16,2> + k_pf_gemm<1,1,2,Q8_0,16,1>")
