@@ -9,14 +9,16 @@
 // pass on workgroups of one XCD).  For each item it streams the block's rows (of
 // gate and up, or of down) through an S-stage LDS ring, 256 columns per
 // stage (Q8_0: 8 blocks; K-quants: one super-block, or two when gate and up
-// alternate with passes of 16 pairs), filled by global_load_lds:
+// alternate with passes of 16 pairs: 512 columns), filled by global_load_lds:
 //   * weights: each row's stage chunk as GR granules of 16 B from the
 //     16-byte boundary at or before the row start plus the 16-byte boundary
 //     at or before the chunk's offset in the row (Q8_0 272 B, Q4_K 144 B and
 //     Q5_K 176 B start aligned: 17, 9 and 11 granules; Q2_K 84 B, Q3_K 110 B
-//     and Q6_K 210 B start up to 24 or 28 bytes in: 7, 9 and 15).  Longer
-//     runs per row stream faster: a probe of this one-workgroup-per-CU ring
-//     reads 136-byte row pieces at 4.6 TB/s, 272-byte ones at 5.5;
+//     and Q6_K 210 B start up to 24 or 28 bytes in: 7, 9 and 15; two Q2_K,
+//     Q3_K or Q4_K super-blocks 13, 17 and 19, an odd count: gm_granules).
+//     Longer runs per row stream faster: a probe of this
+//     one-workgroup-per-CU ring reads 136-byte row pieces at 4.6 TB/s,
+//     272-byte ones at 5.5;
 //   * activations: the pass's M rows x KC fp16 (M = 16 or 32, the pass
 //     size the launch was grouped with), rows one pad granule
 //     longer than their data, so the MFMA operand reads of 16 rows hit 16
